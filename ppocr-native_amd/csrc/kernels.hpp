@@ -1,0 +1,152 @@
+// Launch arguments and host launchers of the backend's HIP kernels.
+//
+// Tensors are NHWC f32. A launch covers every lane of a batch: lane `l` of a
+// tensor starts `lane_stride` floats after lane 0. Launchers return a
+// hipError_t from the launch (or hipErrorInvalidValue for shapes a kernel
+// does not take); they never synchronise.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace ppocr {
+
+// ---------------------------------------------------------------- GEMM conv
+
+// One input of an implicit-GEMM convolution: `c` channels, `shift` > 0 when it
+// is read as nearest-upsampled by 2^shift (an upsampling folded in).
+struct ConvSrc {
+  const float *p;
+  long lane_stride;
+  int c;
+  int shift;
+  int chunks;  // ceil(c / BK): reduction chunks this source gives each tap
+};
+
+enum GemmMode : int { GEMM_STORE = 0, GEMM_SPREAD = 1, GEMM_CTC = 2 };
+
+struct ConvArgs {
+  int lanes;
+  int ih, iw, oh, ow;   // per-lane window image and output sizes
+  int n;                // output columns (oc, or the spread/CTC columns)
+  int kh, kw, sh, sw, pt, pl;
+  int nsrc;
+  ConvSrc src[4];
+  int chunks;           // total reduction chunks: kh * kw * sum of src chunks
+  const float *wt;      // packed weights [n_pad][chunks * BK], zero padded
+  long wt_k;            // floats per packed weight row (chunks * BK)
+  const float *bias;    // n values or null
+  const float *gate;    // per-lane channel gate of source 0, or null
+  long gate_lane_stride;
+  const float *res;     // per-lane residual [m][n], or null
+  long res_lane_stride;
+  int act, act2;
+  float *y;
+  long y_lane_stride;
+  int mode;             // GemmMode
+  int spread_kw, spread_oc;  // GEMM_SPREAD: non-overlapping transposed conv
+  float *part;          // GEMM_CTC: per row and column tile (max, sum, best)
+  int vocab;
+};
+
+struct GemmTile {
+  int wm, bn, bk;  // wave rows (4 waves per tile), tile columns, reduction chunk
+  bool vec;        // channels read 4 at a time
+  bool pointwise;  // 1x1, stride 1, no padding, one source
+};
+
+hipError_t launch_conv(const ConvArgs &a, const GemmTile &t, hipStream_t s);
+
+// CTC choice from the GEMM's per-tile partials: y[2m] = best, y[2m+1] = 1/sum.
+hipError_t launch_ctc_merge(const float *part, int rows, int ntiles, float *y, long y_lane_stride,
+                            int rows_per_lane, hipStream_t s);
+
+// ---------------------------------------------------------------- depthwise
+
+struct DwArgs {
+  int lanes, ih, iw, c, oh, ow, kh, kw, sh, sw, pt, pl;
+  const float *x;
+  long x_lane_stride;
+  const float *w;     // [kh][kw][c]
+  const float *bias;  // c or null
+  int act;
+  float *y;
+  long y_lane_stride;
+};
+hipError_t launch_dwconv(const DwArgs &a, hipStream_t s);
+
+// ---------------------------------------------------------------- elementwise
+
+enum EltMode : int {
+  ELT_ADD = 0,          // a + b
+  ELT_CHANNELMUL = 1,   // a * g[c]
+  ELT_UPSAMPLE = 2,     // a[oy / sh][ox / sw]
+  ELT_UPSAMPLEADD = 3,  // b + a[oy / sh][ox / sw]
+  ELT_CONCAT = 4,       // channels of a (ca) then of b (cb)
+  ELT_RESGATE = 5,      // a + a * g[c]
+  ELT_UPSAMPLEADD_RESGATE = 6,  // (b + b * g[c]) + a[oy / sh][ox / sw]
+  ELT_MUL = 7,          // a * b
+  ELT_ACT = 8,          // a
+};
+
+struct EltArgs {
+  int mode, lanes;
+  int oh, ow, c;        // output size
+  int iw, sh, sw;       // upsampling source width and factors
+  int ca, cb;           // concat channel counts
+  const float *a; long a_lane_stride;
+  const float *b; long b_lane_stride;
+  const float *g; long g_lane_stride;
+  int act;
+  float *y; long y_lane_stride;
+};
+hipError_t launch_eltwise(const EltArgs &a, hipStream_t s);
+
+struct PoolArgs {
+  int avg, lanes, ih, iw, c, oh, ow, kh, kw, sh, sw;
+  const float *x; long x_lane_stride;
+  float *y; long y_lane_stride;
+};
+hipError_t launch_pool(const PoolArgs &a, hipStream_t s);
+
+// ---------------------------------------------------------------- reductions
+
+// Channel mean of every lane, two passes through `partial` (f64, at least
+// mean_partial_doubles(pixels, c, lanes) values). With `se` set, the squeeze
+// and excite that follows is computed too: y = act2(W2 act1(W1 mean + b1) + b2)
+// (two 1x1 convolutions of one pixel), written to `y` (c2 values per lane).
+struct SeArgs {
+  const float *w1, *b1; int mid, act1;
+  const float *w2, *b2; int cout, act2;
+};
+size_t mean_partial_doubles(int pixels, int c, int lanes);
+hipError_t launch_mean(const float *x, long x_lane_stride, int pixels, int c, int lanes,
+                       double *partial, const SeArgs *se, float *y, long y_lane_stride,
+                       hipStream_t s);
+
+hipError_t launch_layernorm(const float *x, long x_lane_stride, const float *w, int rows, int c,
+                            int lanes, float *y, long y_lane_stride, hipStream_t s);
+
+// Attention keeps K and V of a head in LDS; score rows go to LDS too unless
+// the line is long, when they take attention_scratch_floats() floats of
+// `scratch` (nonzero only then).
+size_t attention_scratch_floats(int t, int c, int heads, int lanes);
+hipError_t launch_attention(const float *x, long x_lane_stride, float scale, int t, int c,
+                            int heads, int lanes, float *y, long y_lane_stride, float *scratch,
+                            hipStream_t s);
+
+hipError_t launch_row_argmax(const float *x, float *y, int rows, int cols, hipStream_t s);
+
+// Transposed convolution with few outputs per pixel (kh*kw*oc <= 16): one
+// thread per input pixel, all its outputs.
+struct ConvtArgs {
+  int lanes, ih, iw, ic, oc, kh, kw;
+  const float *x; long x_lane_stride;
+  const float *w;     // [ic][kh][kw][oc]
+  const float *bias;  // kh*kw*oc or null
+  int act;
+  float *y; long y_lane_stride;
+};
+hipError_t launch_convt_small(const ConvtArgs &a, hipStream_t s);
+
+}  // namespace ppocr

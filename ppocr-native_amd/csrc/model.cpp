@@ -1,0 +1,1036 @@
+// The GPU model: the HIP counterpart of the engine's `GpuModel`
+// (src/engine/gpu/mod.rs:81-291) behind the C ABI of include/ppocr_hip.h.
+//
+// Load: parse and check the plan, refuse what the GPU does not run, upload
+// the weights, build the steps (fusion), repack the weights of every step
+// that runs as an implicit GEMM, set one lane at the stored size.
+//
+// Lanes: every image of a run. Lanes of equal size form a batch that every
+// launch covers at once (lanes stacked along the GEMM rows, or a grid axis),
+// so sixteen recogniser lines cost one launch per step, not sixteen. Each
+// batch owns one device arena in which every materialised plan buffer has a
+// home, reused by liveness as `Lane::arrange` does (src/engine/gpu/mod.rs:
+// 297-388), each lane of a home `stride` floats after the previous one.
+//
+// Run: per batch, a pitched copy of the inputs to the device, the batch's
+// launch list (built once per size configuration), pitched copies of the
+// outputs back, all on the model's stream, then one synchronisation.
+#include <hip/hip_runtime.h>
+#include <string.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <fstream>
+#include <functional>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "kernels.hpp"
+#include "plan.hpp"
+#include "ppocr_hip.h"
+
+namespace ppocr {
+
+namespace {
+
+std::string fmt(const char *f, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, f);
+  vsnprintf(buf, sizeof buf, f, ap);
+  va_end(ap);
+  return buf;
+}
+
+void put_err(const std::string &m, char *err, size_t len) {
+  if (!err || !len) return;
+  size_t n = std::min(m.size(), len - 1);
+  memcpy(err, m.data(), n);
+  err[n] = 0;
+}
+
+#define HIPTRY(call, what)                                                       \
+  do {                                                                           \
+    hipError_t e_ = (call);                                                      \
+    if (e_ != hipSuccess) {                                                      \
+      err = std::string(what) + ": " + hipGetErrorString(e_);                    \
+      return false;                                                              \
+    }                                                                            \
+  } while (0)
+
+size_t round_up(size_t v, size_t m) { return (v + m - 1) / m * m; }
+
+enum StepKind { S_GEMM, S_DW, S_ELT, S_POOL, S_MEAN, S_LN, S_ATTN, S_CTC, S_CONVT };
+
+struct Source {
+  size_t slot;
+  int c, shift;
+};
+
+struct Step {
+  StepKind kind;
+  int op;
+  int gate = -1;     // Channelmul folded into a convolution's first input
+  int add = -1;      // Add folded into a convolution's output / of a residual gate
+  int resgate = -1;  // Channelmul of a residual gate, x + x * g
+  int fc1 = -1, fc2 = -1;  // squeeze-and-excite 1x1 layers after a Mean
+  int elt = 0;             // EltMode
+  std::vector<Source> sources;
+  // Implicit-GEMM steps
+  GemmTile tile{};
+  int gemm_n = 0, chunks = 0;
+  size_t wt_off = 0, wt_k = 0;
+  std::vector<int> src_chunks;
+};
+
+struct Launch {
+  std::string name;
+  int op;
+  std::function<hipError_t(hipStream_t)> fn;
+};
+
+// A batch of lanes of one size.
+struct Batch {
+  size_t h = 0, w = 0;
+  std::vector<size_t> lanes;  // model lane indices, in order
+  Plan plan;
+  std::vector<size_t> home;   // plan buffer -> home, or SIZE_MAX
+  std::vector<size_t> home_floats, home_off;
+  size_t ws_off = 0;          // workspace in the arena, floats
+  float *arena = nullptr;
+  size_t arena_floats = 0;
+  float *host_in = nullptr;   // pinned, lanes * in_len
+  size_t host_in_cap = 0;
+  std::vector<float *> host_out;
+  std::vector<size_t> host_out_cap;
+  size_t in_len = 0;
+  std::vector<Launch> launches;
+
+  float *dev(size_t slot) const { return arena + home_off[home[slot]]; }
+  long stride(size_t slot) const { return long(home_floats[home[slot]]); }
+};
+
+}  // namespace
+
+struct Model {
+  int device = 0;
+  std::string name;
+  int integrated = 0;
+  hipStream_t stream = nullptr;
+  Plan plan;
+  std::vector<float> weights;     // host copy of the plan's weights
+  float *dweights = nullptr;      // the plan's weights on the device
+  float *dpacked = nullptr;       // GEMM-packed weights
+  std::vector<Step> steps;
+  std::vector<std::unique_ptr<Batch>> batches;
+  std::vector<std::pair<size_t, size_t>> lane_at;  // lane -> (batch, index in batch)
+  std::vector<std::pair<size_t, size_t>> sizes;
+  size_t active_batches = 0;
+
+  ~Model();
+  bool load(const uint8_t *bytes, size_t len, std::string &err);
+  bool build_steps(std::string &err);
+  bool pack(std::string &err);
+  bool set_sizes(const size_t *hw, size_t n, std::string &err);
+  bool arrange(Batch &b, std::string &err);
+  void build_launches(Batch &b);
+  bool run(bool copy_in, bool copy_out, std::string &err);
+  std::vector<size_t> step_reads(const Step &s) const;
+  size_t step_writes(const Step &s) const;
+};
+
+Model::~Model() {
+  if (stream) hipStreamSynchronize(stream);
+  for (auto &b : batches) {
+    if (b->arena) hipFree(b->arena);
+    if (b->host_in) hipHostFree(b->host_in);
+    for (float *p : b->host_out)
+      if (p) hipHostFree(p);
+  }
+  if (dweights) hipFree(dweights);
+  if (dpacked) hipFree(dpacked);
+  if (stream) hipStreamDestroy(stream);
+}
+
+// ---------------------------------------------------------------- steps
+
+std::vector<size_t> Model::step_reads(const Step &s) const {
+  const Op &op = plan.ops[s.op];
+  std::vector<size_t> r;
+  switch (s.kind) {
+    case S_GEMM:
+      for (const Source &src : s.sources) r.push_back(src.slot);
+      if (s.gate >= 0) r.push_back(plan.ops[s.gate].x2);
+      if (s.add >= 0) {
+        const Op &a = plan.ops[s.add];
+        r.push_back(a.x == op.y ? a.x2 : a.x);
+      }
+      break;
+    case S_ELT:
+      if (s.elt == ELT_RESGATE) {
+        r = {plan.ops[s.resgate].x, plan.ops[s.resgate].x2};
+      } else if (s.elt == ELT_UPSAMPLEADD_RESGATE) {
+        r = {op.x, plan.ops[s.resgate].x, plan.ops[s.resgate].x2};
+      } else {
+        r.push_back(op.x);
+        size_t x2;
+        if (op.has_second(&x2)) r.push_back(x2);
+      }
+      break;
+    default:
+      r.push_back(op.x);
+  }
+  return r;
+}
+
+size_t Model::step_writes(const Step &s) const {
+  if (s.kind == S_MEAN && s.fc2 >= 0) return plan.ops[s.fc2].y;
+  if (s.kind == S_ELT && s.elt == ELT_UPSAMPLEADD_RESGATE) return plan.ops[s.op].y;
+  if (s.add >= 0) return plan.ops[s.add].y;
+  return plan.ops[s.op].y;
+}
+
+// The fusion rules. Each folded operation's output is never materialised.
+//  - Mean, then two 1x1 layers of its single pixel, each read only by the
+//    next: one squeeze-and-excite step (mean + both layers).
+//  - Channelmul whose product only the Add after it reads, adding it to the
+//    multiply's own input: x + x * g (src/engine/gpu/mod.rs:607-617); when
+//    that sum only feeds an Upsampleadd's addend, it folds into that step.
+//  - Channelmul only a convolution reads: the gate scales the convolution's
+//    first input as it is staged (gpu/mod.rs:501-505).
+//  - Nearest upsamplings by powers of two and channel concatenations that
+//    only feed a convolution: up to four shifted sources (gpu/mod.rs:506-521,
+//    535-605).
+//  - An Add that is the only reader of a convolution's output: the
+//    convolution's epilogue (gpu/mod.rs:522-526).
+bool Model::build_steps(std::string &err) {
+  const auto &ops = plan.ops;
+  const size_t n = ops.size();
+  std::vector<size_t> readers(plan.pool.size(), 0);
+  std::vector<size_t> writer(plan.pool.size(), SIZE_MAX);
+  for (size_t i = 0; i < n; i++) {
+    readers[ops[i].x]++;
+    size_t x2;
+    if (ops[i].has_second(&x2)) readers[x2]++;
+    if (writer[ops[i].y] != SIZE_MAX) {
+      err = fmt("operation %zu writes buffer %zu again", i, ops[i].y);  // gpu/mod.rs:622-630
+      return false;
+    }
+    writer[ops[i].y] = i;
+  }
+  for (size_t s : plan.out_slot) readers[s]++;
+
+  for (size_t i = 0; i < n; i++) {  // gpu/mod.rs:633-649
+    const Op &op = ops[i];
+    if (op.kind == K_CTCHEAD) return err = fmt("operation %zu: the CTC head with probabilities", i), false;
+    if (op.kind == K_ATTENTION && op.oc / op.n2 > 64)
+      return err = fmt("operation %zu: attention heads too large", i), false;
+  }
+
+  auto residual_gate = [&](size_t m) {
+    if (m + 1 >= n) return false;
+    const Op &g = ops[m], &a = ops[m + 1];
+    return g.kind == K_CHANNELMUL && g.fused == 0 && readers[g.y] == 1 && a.kind == K_ADD &&
+           a.fused == 0 && a.x == g.x && a.x2 == g.y;
+  };
+  auto foldable = [&](size_t i, size_t slot) -> int {
+    size_t p = writer[slot];
+    if (p == SIZE_MAX || p >= i || readers[slot] != 1) return -1;
+    const Op &o = ops[p];
+    bool up = o.kind == K_UPSAMPLE && o.sh == o.sw && o.sh > 1 && (o.sh & (o.sh - 1)) == 0;
+    return (o.kind == K_CONCATC || up) ? int(p) : -1;
+  };
+  std::function<void(size_t, size_t, int, int, std::vector<Source> &, std::vector<int> &)> expand =
+      [&](size_t i, size_t slot, int ch, int shift, std::vector<Source> &srcs,
+          std::vector<int> &producers) {
+        int p = foldable(i, slot);
+        if (p < 0) {
+          srcs.push_back({slot, ch, shift});
+          return;
+        }
+        producers.push_back(p);
+        const Op &o = ops[p];
+        if (o.kind == K_CONCATC) {
+          expand(p, o.x, int(o.ic), shift, srcs, producers);
+          expand(p, o.x2, int(o.n2), shift, srcs, producers);
+        } else {
+          int k = 0;
+          while ((size_t(1) << k) < o.sh) k++;
+          expand(p, o.x, ch, shift + k, srcs, producers);
+        }
+      };
+
+  std::vector<bool> folded(n, false);
+  std::vector<int> inside;
+  steps.clear();
+  for (size_t i = 0; i < n; i++) {
+    if (folded[i]) continue;
+    const Op &op = ops[i];
+    Step s{};
+    s.op = int(i);
+    switch (op.kind) {
+      case K_MEAN: {
+        s.kind = S_MEAN;
+        if (i + 2 < n && readers[op.y] == 1) {
+          const Op &f1 = ops[i + 1], &f2 = ops[i + 2];
+          if (f1.kind == K_CONV && f1.is_pointwise() && f1.x == op.y && f2.kind == K_CONV &&
+              f2.is_pointwise() && f2.x == f1.y && readers[f1.y] == 1) {
+            s.fc1 = int(i + 1), s.fc2 = int(i + 2);
+            folded[i + 1] = folded[i + 2] = true;
+          }
+        }
+        break;
+      }
+      case K_CHANNELMUL:
+        s.kind = S_ELT;
+        if (residual_gate(i)) {
+          s.elt = ELT_RESGATE;
+          s.resgate = int(i);
+          s.add = int(i + 1);
+          folded[i + 1] = true;
+        } else {
+          s.elt = ELT_CHANNELMUL;
+        }
+        break;
+      case K_CONV: {
+        s.kind = S_GEMM;
+        size_t p = writer[op.x];
+        if (p != SIZE_MAX && p < i && ops[p].kind == K_CHANNELMUL && readers[op.x] == 1 &&
+            op.x != op.x2 && !residual_gate(p)) {
+          s.gate = int(p);
+          inside.push_back(int(p));
+          s.sources.push_back({ops[p].x, int(op.ic), 0});
+          if (op.n2) s.sources.push_back({op.x2, int(op.n2), 0});
+        } else {
+          std::vector<Source> srcs;
+          std::vector<int> producers;
+          expand(i, op.x, int(op.ic), 0, srcs, producers);
+          if (op.n2) expand(i, op.x2, int(op.n2), 0, srcs, producers);
+          bool plain = srcs.size() <= 2;
+          for (auto &x : srcs) plain = plain && x.shift == 0;
+          if (srcs.size() <= 4 && !plain) {
+            s.sources = srcs;
+            inside.insert(inside.end(), producers.begin(), producers.end());
+          } else {
+            s.sources.push_back({op.x, int(op.ic), 0});
+            if (op.n2) s.sources.push_back({op.x2, int(op.n2), 0});
+          }
+        }
+        if (readers[op.y] == 1 && i + 1 < n && ops[i + 1].kind == K_ADD &&
+            ((ops[i + 1].x == op.y) != (ops[i + 1].x2 == op.y))) {
+          s.add = int(i + 1);
+          folded[i + 1] = true;
+        }
+        break;
+      }
+      case K_DWCONV: s.kind = S_DW; break;
+      case K_ADD: s.kind = S_ELT, s.elt = ELT_ADD; break;
+      case K_MAXPOOL: case K_AVGPOOL: s.kind = S_POOL; break;
+      case K_CONCATC: s.kind = S_ELT, s.elt = ELT_CONCAT; break;
+      case K_UPSAMPLE: s.kind = S_ELT, s.elt = ELT_UPSAMPLE; break;
+      case K_UPSAMPLEADD: {
+        s.kind = S_ELT, s.elt = ELT_UPSAMPLEADD;
+        size_t a = writer[op.x2];
+        if (readers[op.x2] == 1 && a != SIZE_MAX && a > 0 && a < i && residual_gate(a - 1)) {
+          s.elt = ELT_UPSAMPLEADD_RESGATE;
+          s.resgate = int(a - 1);
+          inside.push_back(int(a - 1));
+        }
+        break;
+      }
+      case K_LAYERNORM: s.kind = S_LN; break;
+      case K_ATTENTION: s.kind = S_ATTN; break;
+      case K_CTCARGMAX: s.kind = S_CTC; break;
+      case K_CONVTRANSPOSE:
+        s.kind = op.kh * op.kw * op.oc <= 16 ? S_CONVT : S_GEMM;
+        if (s.kind == S_GEMM) s.sources.push_back({op.x, int(op.ic), 0});
+        break;
+      default:
+        return err = fmt("operation %zu: %s is not supported on the GPU", i, kind_name(op.kind)), false;
+    }
+    steps.push_back(s);
+  }
+  steps.erase(std::remove_if(steps.begin(), steps.end(),
+                             [&](const Step &s) {
+                               return std::find(inside.begin(), inside.end(), s.op) != inside.end();
+                             }),
+              steps.end());
+  return true;
+}
+
+// Choose each GEMM step's tile and repack its weights: row n of the packed
+// matrix holds column n's reduction in the kernel's chunk order (tap, source,
+// channel chunk), zero where a source's channels do not fill a chunk.
+bool Model::pack(std::string &err) {
+  std::vector<float> packed;
+  const auto &ops = plan.ops;
+  for (Step &s : steps) {
+    if (s.kind != S_GEMM && s.kind != S_CTC) continue;
+    const Op &op = ops[s.op];
+    int K_taps = 1, N;
+    std::vector<Source> srcs = s.sources;
+    if (s.kind == S_CTC) {
+      srcs = {{op.x, int(op.ic), 0}};
+      N = int(op.n2);
+    } else if (op.kind == K_CONVTRANSPOSE) {
+      N = int(op.kh * op.kw * op.oc);
+    } else {
+      K_taps = int(op.kh * op.kw);
+      N = int(op.oc);
+    }
+    bool vec = true;
+    for (auto &x : srcs) vec = vec && x.c % 4 == 0;
+    bool pw = (op.kind != K_CONV || op.is_pointwise()) && srcs.size() == 1 && srcs[0].shift == 0 && vec;
+    int bk = 4;
+    if (vec) {
+      long k16 = 0, k8 = 0;
+      for (auto &x : srcs) k16 += (x.c + 15) / 16 * 16, k8 += (x.c + 7) / 8 * 8;
+      bk = k8 < k16 ? 8 : 16;
+    }
+    int bn = N <= 16 ? 16 : (N <= 32 ? 32 : 64);
+    int wm = 32;
+    if (s.kind == S_CTC) bn = 64;
+    s.tile = GemmTile{wm, bn, bk, vec, pw};
+    s.gemm_n = N;
+    s.src_chunks.clear();
+    int cpt = 0;
+    for (auto &x : srcs) {
+      int ch = (x.c + bk - 1) / bk;
+      s.src_chunks.push_back(ch);
+      cpt += ch;
+    }
+    s.chunks = K_taps * cpt;
+    s.wt_k = size_t(s.chunks) * bk;
+    int n_pad = (N + bn - 1) / bn * bn;
+    size_t start = round_up(packed.size(), 64);
+    packed.resize(start + size_t(n_pad) * s.wt_k, 0.0f);
+    s.wt_off = start;
+    float *dst = packed.data() + start;
+    const float *w = weights.data() + op.w0;
+    int ctot = 0;
+    for (auto &x : srcs) ctot += x.c;
+    for (int nn = 0; nn < N; nn++) {
+      float *row = dst + size_t(nn) * s.wt_k;
+      size_t k = 0;
+      for (int tap = 0; tap < K_taps; tap++) {
+        int coff = 0;
+        for (size_t si = 0; si < srcs.size(); si++) {
+          int c = srcs[si].c;
+          for (int cc = 0; cc < s.src_chunks[si] * bk; cc++, k++) {
+            if (cc >= c) continue;
+            size_t kk = size_t(tap) * ctot + coff + cc;  // plan reduction index
+            float v;
+            if (s.kind == S_CTC) v = w[(size_t(nn) / 16) * op.ic * 16 + kk * 16 + nn % 16];
+            else v = w[kk * N + nn];
+            row[k] = v;
+          }
+          coff += c;
+        }
+      }
+    }
+  }
+  if (packed.empty()) return true;
+  HIPTRY(hipMalloc(&dpacked, packed.size() * sizeof(float)), "allocating packed weights");
+  HIPTRY(hipMemcpy(dpacked, packed.data(), packed.size() * sizeof(float), hipMemcpyHostToDevice),
+         "uploading packed weights");
+  return true;
+}
+
+bool Model::load(const uint8_t *bytes, size_t len, std::string &err) {
+  if (!plan.parse(bytes, len, weights, err)) return false;
+  if (!build_steps(err)) return false;
+  HIPTRY(hipGetDevice(&device), "no GPU");
+  hipDeviceProp_t prop;
+  HIPTRY(hipGetDeviceProperties(&prop, device), "reading the GPU's properties");
+  name = prop.name;
+  if (name.empty()) name = prop.gcnArchName;
+  integrated = prop.integrated;
+  HIPTRY(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking), "creating a stream");
+  HIPTRY(hipMalloc(&dweights, std::max<size_t>(weights.size(), 1) * sizeof(float)),
+         "allocating the weights");
+  if (!weights.empty())
+    HIPTRY(hipMemcpy(dweights, weights.data(), weights.size() * sizeof(float),
+                     hipMemcpyHostToDevice),
+           "uploading the weights");
+  if (!pack(err)) return false;
+  size_t hw[2] = {plan.in_h, plan.in_w};
+  return set_sizes(hw, 1, err);
+}
+
+// ---------------------------------------------------------------- memory
+
+bool Model::arrange(Batch &b, std::string &err) {
+  const Plan &p = b.plan;
+  const size_t L = b.lanes.size();
+  std::vector<size_t> last(p.pool.size(), 0);
+  for (size_t i = 0; i < steps.size(); i++)
+    for (size_t s : step_reads(steps[i])) last[s] = i;
+  for (size_t s : p.out_slot) last[s] = SIZE_MAX;
+  b.home.assign(p.pool.size(), SIZE_MAX);
+  std::vector<size_t> sizes, freel;
+  // The smallest free home that holds n floats, else the largest grown.
+  auto place = [&](size_t n) {
+    n = round_up(std::max<size_t>(n, 1), 64);
+    int best = -1;
+    for (size_t k = 0; k < freel.size(); k++)
+      if (sizes[freel[k]] >= n && (best < 0 || sizes[freel[k]] < sizes[freel[best]])) best = int(k);
+    if (best < 0)
+      for (size_t k = 0; k < freel.size(); k++)
+        if (best < 0 || sizes[freel[k]] > sizes[freel[best]]) best = int(k);
+    if (best >= 0) {
+      size_t h = freel[best];
+      freel.erase(freel.begin() + best);
+      sizes[h] = std::max(sizes[h], n);
+      return h;
+    }
+    sizes.push_back(n);
+    return sizes.size() - 1;
+  };
+  b.home[p.in_slot] = place(p.pool[p.in_slot]);
+  for (size_t i = 0; i < steps.size(); i++) {
+    size_t y = step_writes(steps[i]);
+    b.home[y] = place(p.pool[y]);
+    for (size_t s : step_reads(steps[i]))
+      if (last[s] == i && std::find(freel.begin(), freel.end(), b.home[s]) == freel.end())
+        freel.push_back(b.home[s]);
+  }
+  b.home_floats = sizes;
+  b.home_off.resize(sizes.size());
+  size_t off = 0;
+  for (size_t h = 0; h < sizes.size(); h++) {
+    b.home_off[h] = off;
+    off += round_up(sizes[h] * L, 64);
+  }
+  // Workspace: channel-mean partials (f64) and CTC tile partials.
+  size_t ws = 0;
+  for (const Step &s : steps) {
+    const Op &op = p.ops[s.op];
+    if (s.kind == S_MEAN) ws = std::max(ws, 2 * mean_partial_doubles(int(op.ih * op.iw), int(op.ic), int(L)));
+    if (s.kind == S_CTC) {
+      size_t ntn = (s.gemm_n + s.tile.bn - 1) / s.tile.bn;
+      ws = std::max(ws, L * op.iw * ntn * 4);
+    }
+    if (s.kind == S_ATTN)
+      ws = std::max(ws, attention_scratch_floats(int(op.iw), int(op.oc), int(op.n2), int(L)));
+  }
+  b.ws_off = off;
+  off += round_up(std::max<size_t>(ws, 64), 64);
+  if (off > b.arena_floats) {
+    if (b.arena) {
+      hipFree(b.arena);
+      b.arena = nullptr;
+      b.arena_floats = 0;
+    }
+    size_t want = off + off / 4;  // a quarter more for the next, slightly larger size
+    HIPTRY(hipMalloc(&b.arena, want * sizeof(float)), fmt("allocating %zu bytes of device memory", want * 4).c_str());
+    b.arena_floats = want;
+  }
+  b.in_len = p.in_h * p.in_w * p.in_c;
+  if (b.host_in_cap < b.in_len * L) {
+    if (b.host_in) hipHostFree(b.host_in);
+    b.host_in = nullptr;
+    b.host_in_cap = 0;
+    size_t want = b.in_len * L + b.in_len * L / 4;
+    HIPTRY(hipHostMalloc(&b.host_in, want * sizeof(float), hipHostMallocDefault), "allocating pinned input");
+    b.host_in_cap = want;
+  }
+  b.host_out.resize(p.out_slot.size(), nullptr);
+  b.host_out_cap.resize(p.out_slot.size(), 0);
+  for (size_t k = 0; k < p.out_slot.size(); k++) {
+    size_t need = p.out_n[k] * L;
+    if (b.host_out_cap[k] < need) {
+      if (b.host_out[k]) hipHostFree(b.host_out[k]);
+      b.host_out[k] = nullptr;
+      b.host_out_cap[k] = 0;
+      size_t want = need + need / 4;
+      HIPTRY(hipHostMalloc(&b.host_out[k], want * sizeof(float), hipHostMallocDefault), "allocating pinned output");
+      b.host_out_cap[k] = want;
+    }
+  }
+  build_launches(b);
+  return true;
+}
+
+void Model::build_launches(Batch &b) {
+  b.launches.clear();
+  const Plan &p = b.plan;
+  const int L = int(b.lanes.size());
+  const float *W = dweights;
+  for (const Step &s : steps) {
+    const Op &op = p.ops[s.op];
+    const size_t y = step_writes(s);
+    float *Y = b.dev(y);
+    const long ys = b.stride(y);
+    const float *bias = op.b1 ? W + op.b0 : nullptr;
+    switch (s.kind) {
+      case S_GEMM: {
+        ConvArgs a{};
+        a.lanes = L;
+        a.n = s.gemm_n;
+        if (op.kind == K_CONVTRANSPOSE) {
+          a.ih = int(op.ih), a.iw = int(op.iw), a.oh = int(op.ih), a.ow = int(op.iw);
+          a.kh = a.kw = a.sh = a.sw = 1;
+          a.mode = GEMM_SPREAD;
+          a.spread_kw = int(op.kw), a.spread_oc = int(op.oc);
+        } else {
+          a.ih = int(op.ih), a.iw = int(op.iw), a.oh = int(op.oh), a.ow = int(op.ow);
+          a.kh = int(op.kh), a.kw = int(op.kw), a.sh = int(op.sh), a.sw = int(op.sw);
+          a.pt = int(op.pt), a.pl = int(op.pl);
+          a.mode = GEMM_STORE;
+        }
+        a.nsrc = int(s.sources.size());
+        for (size_t k = 0; k < s.sources.size(); k++) {
+          const Source &src = s.sources[k];
+          a.src[k] = ConvSrc{b.dev(src.slot), b.stride(src.slot), src.c, src.shift, s.src_chunks[k]};
+        }
+        a.chunks = s.chunks;
+        a.wt = dpacked + s.wt_off;
+        a.wt_k = long(s.wt_k);
+        a.bias = bias;
+        if (s.gate >= 0) {
+          size_t g = p.ops[s.gate].x2;
+          a.gate = b.dev(g), a.gate_lane_stride = b.stride(g);
+        }
+        a.act = op.fused;
+        if (s.add >= 0) {
+          const Op &ad = p.ops[s.add];
+          size_t r = ad.x == op.y ? ad.x2 : ad.x;
+          a.res = b.dev(r), a.res_lane_stride = b.stride(r);
+          a.act2 = ad.fused;
+        }
+        a.y = Y, a.y_lane_stride = ys;
+        GemmTile t = s.tile;
+        long M = long(L) * a.oh * a.ow;
+        long tiles = (M + 127) / 128 * ((a.n + t.bn - 1) / t.bn);
+        if (t.bn == 64 && tiles < 1024) t.wm = 16;
+        const char *nm = op.kind == K_CONVTRANSPOSE ? "convt_gemm" : (t.pointwise ? "pointwise_gemm" : "conv_gemm");
+        b.launches.push_back({nm, s.op, [a, t](hipStream_t st) { return launch_conv(a, t, st); }});
+        break;
+      }
+      case S_CTC: {
+        ConvArgs a{};
+        a.lanes = L;
+        a.ih = 1, a.iw = int(op.iw), a.oh = 1, a.ow = int(op.iw);
+        a.n = s.gemm_n;
+        a.kh = a.kw = a.sh = a.sw = 1;
+        a.nsrc = 1;
+        a.src[0] = ConvSrc{b.dev(op.x), b.stride(op.x), int(op.ic), 0, s.src_chunks[0]};
+        a.chunks = s.chunks;
+        a.wt = dpacked + s.wt_off;
+        a.wt_k = long(s.wt_k);
+        a.bias = W + op.b0;
+        a.mode = GEMM_CTC;
+        a.vocab = int(op.n2);
+        float *part = b.arena + b.ws_off;
+        a.part = part;
+        a.y = Y, a.y_lane_stride = ys;
+        GemmTile t = s.tile;
+        int ntn = (a.n + t.bn - 1) / t.bn;
+        int rows = L * int(op.iw), T = int(op.iw);
+        b.launches.push_back({"ctc_gemm", s.op, [a, t](hipStream_t st) { return launch_conv(a, t, st); }});
+        b.launches.push_back({"ctc_merge", s.op, [part, rows, ntn, Y, ys, T](hipStream_t st) {
+                                return launch_ctc_merge(part, rows, ntn, Y, ys, T, st);
+                              }});
+        break;
+      }
+      case S_DW: {
+        DwArgs a{L, int(op.ih), int(op.iw), int(op.oc), int(op.oh), int(op.ow), int(op.kh), int(op.kw),
+                 int(op.sh), int(op.sw), int(op.pt), int(op.pl), b.dev(op.x), b.stride(op.x), W + op.w0,
+                 bias, op.fused, Y, ys};
+        b.launches.push_back({"dwconv", s.op, [a](hipStream_t st) { return launch_dwconv(a, st); }});
+        break;
+      }
+      case S_ELT: {
+        EltArgs a{};
+        a.mode = s.elt, a.lanes = L;
+        a.oh = int(op.oh), a.ow = int(op.ow), a.c = int(op.oc);
+        a.iw = int(op.iw), a.sh = int(std::max<size_t>(op.sh, 1)), a.sw = int(std::max<size_t>(op.sw, 1));
+        a.act = op.fused;
+        a.y = Y, a.y_lane_stride = ys;
+        a.a = b.dev(op.x), a.a_lane_stride = b.stride(op.x);
+        switch (s.elt) {
+          case ELT_ADD: case ELT_UPSAMPLEADD:
+            a.b = b.dev(op.x2), a.b_lane_stride = b.stride(op.x2);
+            break;
+          case ELT_CHANNELMUL:
+            a.g = b.dev(op.x2), a.g_lane_stride = b.stride(op.x2);
+            break;
+          case ELT_CONCAT:
+            a.b = b.dev(op.x2), a.b_lane_stride = b.stride(op.x2);
+            a.ca = int(op.ic), a.cb = int(op.n2);
+            break;
+          case ELT_RESGATE: {
+            const Op &cm = p.ops[s.resgate];
+            a.a = b.dev(cm.x), a.a_lane_stride = b.stride(cm.x);
+            a.g = b.dev(cm.x2), a.g_lane_stride = b.stride(cm.x2);
+            a.act = p.ops[s.add].fused;
+            break;
+          }
+          case ELT_UPSAMPLEADD_RESGATE: {
+            const Op &cm = p.ops[s.resgate];
+            a.b = b.dev(cm.x), a.b_lane_stride = b.stride(cm.x);
+            a.g = b.dev(cm.x2), a.g_lane_stride = b.stride(cm.x2);
+            break;
+          }
+          default: break;
+        }
+        static const char *names[] = {"add", "channel_mul", "upsample", "upsample_add", "concat",
+                                      "residual_gate", "upsample_add_gate", "mul", "activation"};
+        b.launches.push_back({names[s.elt], s.op, [a](hipStream_t st) { return launch_eltwise(a, st); }});
+        break;
+      }
+      case S_POOL: {
+        PoolArgs a{op.kind == K_AVGPOOL, L, int(op.ih), int(op.iw), int(op.oc), int(op.oh), int(op.ow),
+                   int(op.kh), int(op.kw), int(op.sh), int(op.sw), b.dev(op.x), b.stride(op.x), Y, ys};
+        b.launches.push_back({op.kind == K_AVGPOOL ? "avgpool" : "maxpool", s.op,
+                              [a](hipStream_t st) { return launch_pool(a, st); }});
+        break;
+      }
+      case S_MEAN: {
+        const float *x = b.dev(op.x);
+        long xs = b.stride(op.x);
+        int pixels = int(op.ih * op.iw), c = int(op.ic);
+        double *part = reinterpret_cast<double *>(b.arena + b.ws_off);
+        bool se = s.fc1 >= 0;
+        SeArgs sa{};
+        if (se) {
+          const Op &f1 = p.ops[s.fc1], &f2 = p.ops[s.fc2];
+          sa = SeArgs{W + f1.w0, f1.b1 ? W + f1.b0 : nullptr, int(f1.oc), f1.fused,
+                      W + f2.w0, f2.b1 ? W + f2.b0 : nullptr, int(f2.oc), f2.fused};
+        }
+        b.launches.push_back({se ? "se_squeeze" : "channel_mean", s.op,
+                              [=](hipStream_t st) {
+                                return launch_mean(x, xs, pixels, c, L, part, se ? &sa : nullptr, Y, ys, st);
+                              }});
+        break;
+      }
+      case S_LN: {
+        const float *x = b.dev(op.x);
+        long xs = b.stride(op.x);
+        const float *w = W + op.w0;
+        int rows = int(op.oh * op.ow), c = int(op.oc);
+        b.launches.push_back({"layernorm", s.op, [=](hipStream_t st) {
+                                return launch_layernorm(x, xs, w, rows, c, L, Y, ys, st);
+                              }});
+        break;
+      }
+      case S_ATTN: {
+        const float *x = b.dev(op.x);
+        long xs = b.stride(op.x);
+        float scale = weights[op.w0];
+        int t = int(op.iw), c = int(op.oc), heads = int(op.n2);
+        float *scratch = b.arena + b.ws_off;
+        b.launches.push_back({"attention", s.op, [=](hipStream_t st) {
+                                return launch_attention(x, xs, scale, t, c, heads, L, Y, ys, scratch, st);
+                              }});
+        break;
+      }
+      case S_CONVT: {
+        ConvtArgs a{L, int(op.ih), int(op.iw), int(op.ic), int(op.oc), int(op.kh), int(op.kw),
+                    b.dev(op.x), b.stride(op.x), W + op.w0, bias, op.fused, Y, ys};
+        b.launches.push_back({"convt_small", s.op, [a](hipStream_t st) { return launch_convt_small(a, st); }});
+        break;
+      }
+    }
+  }
+}
+
+bool Model::set_sizes(const size_t *hw, size_t n, std::string &err) {
+  HIPTRY(hipSetDevice(device), "selecting the GPU");
+  std::vector<std::pair<size_t, size_t>> want;
+  for (size_t i = 0; i < n; i++) want.push_back({hw[2 * i], hw[2 * i + 1]});
+  if (want == sizes && !batches.empty() && !lane_at.empty()) return true;
+  // Check every size on a copy of the plan first; lanes before the first
+  // that fails stay valid, as src/engine/gpu/mod.rs:188-190 promises.
+  size_t good = 0;
+  std::string size_err;
+  for (; good < n; good++) {
+    Plan probe = plan;
+    if (!probe.set_size(want[good].first, want[good].second, weights.size(), size_err)) break;
+  }
+  if (good < n) want.resize(good);
+  // Batches: one per distinct size, in order of first appearance.
+  std::vector<std::pair<size_t, size_t>> order;
+  std::vector<std::pair<size_t, size_t>> at(want.size());
+  std::vector<std::vector<size_t>> members;
+  for (size_t i = 0; i < want.size(); i++) {
+    auto it = std::find(order.begin(), order.end(), want[i]);
+    size_t g = size_t(it - order.begin());
+    if (it == order.end()) {
+      order.push_back(want[i]);
+      members.push_back({});
+    }
+    at[i] = {g, members[g].size()};
+    members[g].push_back(i);
+  }
+  while (batches.size() < order.size()) batches.emplace_back(new Batch());
+  lane_at.clear();
+  sizes.clear();
+  for (size_t g = 0; g < order.size(); g++) {
+    Batch &b = *batches[g];
+    b.h = order[g].first, b.w = order[g].second;
+    b.lanes = members[g];
+    b.plan = plan;
+    std::string e;
+    if (!b.plan.set_size(b.h, b.w, weights.size(), e)) return err = e, false;
+    if (!arrange(b, err)) return false;
+  }
+  // Memory of batches no longer used is kept for later runs.
+  lane_at = at;
+  sizes = want;
+  active_batches = order.size();
+  if (good < n) return err = size_err, false;
+  return true;
+}
+
+bool Model::run(bool copy_in, bool copy_out, std::string &err) {
+  HIPTRY(hipSetDevice(device), "selecting the GPU");
+  if (lane_at.empty()) return err = "no lanes are set", false;
+  for (size_t g = 0; g < active_batches; g++) {
+    Batch &b = *batches[g];
+    const size_t L = b.lanes.size();
+    const Plan &p = b.plan;
+    if (copy_in)
+      HIPTRY(hipMemcpy2DAsync(b.dev(p.in_slot), b.stride(p.in_slot) * sizeof(float), b.host_in,
+                              b.in_len * sizeof(float), b.in_len * sizeof(float), L,
+                              hipMemcpyHostToDevice, stream),
+             "copying the input");
+    for (const Launch &l : b.launches) {
+      hipError_t e = l.fn(stream);
+      if (e != hipSuccess) return err = fmt("launching %s (operation %d): %s", l.name.c_str(), l.op, hipGetErrorString(e)), false;
+    }
+    if (copy_out)
+      for (size_t k = 0; k < p.out_slot.size(); k++)
+        HIPTRY(hipMemcpy2DAsync(b.host_out[k], p.out_n[k] * sizeof(float), b.dev(p.out_slot[k]),
+                                b.stride(p.out_slot[k]) * sizeof(float), p.out_n[k] * sizeof(float), L,
+                                hipMemcpyDeviceToHost, stream),
+               "copying the results");
+  }
+  HIPTRY(hipStreamSynchronize(stream), "running the plan");
+  return true;
+}
+
+}  // namespace ppocr
+
+// ---------------------------------------------------------------- C ABI
+
+struct ppocr_gpu_model {
+  ppocr::Model m;
+};
+
+using ppocr::Batch;
+using ppocr::put_err;
+
+extern "C" {
+
+int ppocr_gpu_load_bytes(const void *bytes, size_t len, ppocr_gpu_model **out, char *err,
+                         size_t err_len) {
+  if (!out) return put_err("no output handle", err, err_len), 1;
+  *out = nullptr;
+  std::unique_ptr<ppocr_gpu_model> h(new (std::nothrow) ppocr_gpu_model());
+  if (!h) return put_err("out of memory", err, err_len), 1;
+  std::string e;
+  if (!h->m.load(static_cast<const uint8_t *>(bytes), len, e)) return put_err(e, err, err_len), 1;
+  *out = h.release();
+  return 0;
+}
+
+int ppocr_gpu_load(const char *plan_path, ppocr_gpu_model **out, char *err, size_t err_len) {
+  if (out) *out = nullptr;
+  std::ifstream f(plan_path ? plan_path : "", std::ios::binary);
+  if (!f) return put_err(std::string("reading the plan: cannot open ") + (plan_path ? plan_path : "(null)"), err, err_len), 1;
+  std::vector<char> bytes((std::istreambuf_iterator<char>(f)), std::istreambuf_iterator<char>());
+  return ppocr_gpu_load_bytes(bytes.data(), bytes.size(), out, err, err_len);
+}
+
+void ppocr_gpu_free(ppocr_gpu_model *model) { delete model; }
+
+const char *ppocr_gpu_device(const ppocr_gpu_model *model) { return model ? model->m.name.c_str() : ""; }
+
+int ppocr_gpu_integrated(const ppocr_gpu_model *model) { return model ? model->m.integrated : 0; }
+
+int ppocr_gpu_set_sizes(ppocr_gpu_model *model, const size_t *hw, size_t n_lanes, char *err,
+                        size_t err_len) {
+  if (!model) return put_err("no model", err, err_len), 1;
+  if (n_lanes > ppocr_gpu_max_lanes(model))
+    return put_err(ppocr::fmt("%zu lanes, more than the %zu a run takes", n_lanes, ppocr_gpu_max_lanes(model)), err, err_len), 1;
+  std::string e;
+  if (!model->m.set_sizes(hw, n_lanes, e)) return put_err(e, err, err_len), 1;
+  return 0;
+}
+
+int ppocr_gpu_set_input_size(ppocr_gpu_model *model, size_t height, size_t width, char *err,
+                             size_t err_len) {
+  size_t hw[2] = {height, width};
+  return ppocr_gpu_set_sizes(model, hw, 1, err, err_len);
+}
+
+size_t ppocr_gpu_max_lanes(const ppocr_gpu_model *model) { return model ? 4096 : 0; }
+
+size_t ppocr_gpu_lanes(const ppocr_gpu_model *model) { return model ? model->m.lane_at.size() : 0; }
+
+float *ppocr_gpu_lane_input(ppocr_gpu_model *model, size_t lane, size_t *len) {
+  if (!model || lane >= model->m.lane_at.size()) return nullptr;
+  auto [g, i] = model->m.lane_at[lane];
+  Batch &b = *model->m.batches[g];
+  if (len) *len = b.in_len;
+  return b.host_in + i * b.in_len;
+}
+
+const float *ppocr_gpu_lane_output(const ppocr_gpu_model *model, size_t lane, size_t index,
+                                   size_t *len) {
+  if (!model || lane >= model->m.lane_at.size()) return nullptr;
+  auto [g, i] = model->m.lane_at[lane];
+  const Batch &b = *model->m.batches[g];
+  if (index >= b.plan.out_slot.size()) return nullptr;
+  size_t n = b.plan.out_n[index];
+  if (len) *len = n;
+  return b.host_out[index] + i * n;
+}
+
+size_t ppocr_gpu_output_count(const ppocr_gpu_model *model) {
+  return model ? model->m.plan.out_slot.size() : 0;
+}
+
+int ppocr_gpu_run(ppocr_gpu_model *model, char *err, size_t err_len) {
+  if (!model) return put_err("no model", err, err_len), 1;
+  std::string e;
+  if (!model->m.run(true, true, e)) return put_err(e, err, err_len), 1;
+  return 0;
+}
+
+int ppocr_gpu_upload(ppocr_gpu_model *model, char *err, size_t err_len) {
+  if (!model) return put_err("no model", err, err_len), 1;
+  ppocr::Model &m = model->m;
+  std::string e;
+  hipSetDevice(m.device);
+  for (size_t g = 0; g < m.active_batches; g++) {
+    Batch &b = *m.batches[g];
+    const ppocr::Plan &p = b.plan;
+    hipError_t r = hipMemcpy2DAsync(b.dev(p.in_slot), b.stride(p.in_slot) * sizeof(float), b.host_in,
+                                    b.in_len * sizeof(float), b.in_len * sizeof(float), b.lanes.size(),
+                                    hipMemcpyHostToDevice, m.stream);
+    if (r != hipSuccess) return put_err(std::string("copying the input: ") + hipGetErrorString(r), err, err_len), 1;
+  }
+  hipError_t r = hipStreamSynchronize(m.stream);
+  if (r != hipSuccess) return put_err(std::string("copying the input: ") + hipGetErrorString(r), err, err_len), 1;
+  return 0;
+}
+
+int ppocr_gpu_download(ppocr_gpu_model *model, char *err, size_t err_len) {
+  if (!model) return put_err("no model", err, err_len), 1;
+  ppocr::Model &m = model->m;
+  hipSetDevice(m.device);
+  for (size_t g = 0; g < m.active_batches; g++) {
+    Batch &b = *m.batches[g];
+    const ppocr::Plan &p = b.plan;
+    for (size_t k = 0; k < p.out_slot.size(); k++) {
+      hipError_t r = hipMemcpy2DAsync(b.host_out[k], p.out_n[k] * sizeof(float), b.dev(p.out_slot[k]),
+                                      b.stride(p.out_slot[k]) * sizeof(float), p.out_n[k] * sizeof(float),
+                                      b.lanes.size(), hipMemcpyDeviceToHost, m.stream);
+      if (r != hipSuccess) return put_err(std::string("copying the results: ") + hipGetErrorString(r), err, err_len), 1;
+    }
+  }
+  hipError_t r = hipStreamSynchronize(m.stream);
+  if (r != hipSuccess) return put_err(std::string("copying the results: ") + hipGetErrorString(r), err, err_len), 1;
+  return 0;
+}
+
+int ppocr_gpu_run_resident(ppocr_gpu_model *model, int repeats, float *ms, char *err, size_t err_len) {
+  if (!model) return put_err("no model", err, err_len), 1;
+  ppocr::Model &m = model->m;
+  hipSetDevice(m.device);
+  if (m.lane_at.empty()) return put_err("no lanes are set", err, err_len), 1;
+  hipEvent_t t0 = nullptr, t1 = nullptr;
+  if (ms) {
+    hipEventCreate(&t0);
+    hipEventCreate(&t1);
+    hipEventRecord(t0, m.stream);
+  }
+  for (int r = 0; r < repeats; r++) {
+    for (size_t g = 0; g < m.active_batches; g++) {
+      for (const ppocr::Launch &l : m.batches[g]->launches) {
+        hipError_t e = l.fn(m.stream);
+        if (e != hipSuccess) {
+          if (t0) hipEventDestroy(t0), hipEventDestroy(t1);
+          return put_err(ppocr::fmt("launching %s (operation %d): %s", l.name.c_str(), l.op, hipGetErrorString(e)), err, err_len), 1;
+        }
+      }
+    }
+  }
+  hipError_t e = hipSuccess;
+  if (ms) {
+    hipEventRecord(t1, m.stream);
+    e = hipEventSynchronize(t1);
+    if (e == hipSuccess) hipEventElapsedTime(ms, t0, t1);
+    hipEventDestroy(t0);
+    hipEventDestroy(t1);
+  }
+  if (e == hipSuccess) e = hipStreamSynchronize(m.stream);
+  if (e != hipSuccess) return put_err(std::string("running the plan: ") + hipGetErrorString(e), err, err_len), 1;
+  return 0;
+}
+
+void *ppocr_gpu_stream(ppocr_gpu_model *model) { return model ? (void *)model->m.stream : nullptr; }
+
+size_t ppocr_gpu_launch_count(const ppocr_gpu_model *model) {
+  if (!model) return 0;
+  size_t n = 0;
+  for (size_t g = 0; g < model->m.active_batches; g++) n += model->m.batches[g]->launches.size();
+  return n;
+}
+
+static const ppocr::Launch *launch_at(const ppocr_gpu_model *model, size_t i) {
+  for (size_t g = 0; g < model->m.active_batches; g++) {
+    const auto &ls = model->m.batches[g]->launches;
+    if (i < ls.size()) return &ls[i];
+    i -= ls.size();
+  }
+  return nullptr;
+}
+
+const char *ppocr_gpu_launch_name(const ppocr_gpu_model *model, size_t i, size_t *op) {
+  if (!model) return nullptr;
+  const ppocr::Launch *l = launch_at(model, i);
+  if (!l) return nullptr;
+  if (op) *op = size_t(l->op);
+  return l->name.c_str();
+}
+
+int ppocr_gpu_profile_launches(ppocr_gpu_model *model, int repeats, float *ms, char *err, size_t err_len) {
+  if (!model || !ms || repeats < 1) return put_err("bad arguments", err, err_len), 1;
+  ppocr::Model &m = model->m;
+  hipSetDevice(m.device);
+  size_t n = ppocr_gpu_launch_count(model);
+  hipEvent_t t0, t1;
+  hipEventCreate(&t0);
+  hipEventCreate(&t1);
+  for (size_t i = 0; i < n; i++) {
+    const ppocr::Launch *l = launch_at(model, i);
+    hipEventRecord(t0, m.stream);
+    for (int r = 0; r < repeats; r++) {
+      hipError_t e = l->fn(m.stream);
+      if (e != hipSuccess) {
+        hipEventDestroy(t0), hipEventDestroy(t1);
+        return put_err(ppocr::fmt("launching %s: %s", l->name.c_str(), hipGetErrorString(e)), err, err_len), 1;
+      }
+    }
+    hipEventRecord(t1, m.stream);
+    hipError_t e = hipEventSynchronize(t1);
+    if (e != hipSuccess) {
+      hipEventDestroy(t0), hipEventDestroy(t1);
+      return put_err(std::string("profiling: ") + hipGetErrorString(e), err, err_len), 1;
+    }
+    float t = 0;
+    hipEventElapsedTime(&t, t0, t1);
+    ms[i] = t / repeats;
+  }
+  hipEventDestroy(t0);
+  hipEventDestroy(t1);
+  return 0;
+}
+
+}  // extern "C"

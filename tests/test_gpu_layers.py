@@ -1,0 +1,218 @@
+"""Each layer on the GPU (through the C ABI) against the CPU oracle, as
+single-operation plans on seeded inputs, several lanes at once.
+
+Bit-exact where the kernel keeps the engine's order (depthwise, pooling,
+elementwise modes, upsampling, concatenation, layer norm, attention, the
+narrow transposed convolution, the squeeze-and-excite layers given the same
+mean); within a tolerance for the MFMA products, whose sums run in another
+order: |gpu - cpu| <= 1e-5 * max(1, max|cpu|) + 1e-5 * |cpu|.
+"""
+import numpy as np
+import pytest
+
+from ppocr_native_amd import GpuModel
+from ppocr_native_amd.planfile import PlanBuilder
+
+pytestmark = pytest.mark.gpu
+RNG = np.random.default_rng(99)
+
+
+def both(build, shape, oracle, lanes=3, seed=0):
+    """Run `build` as a plan over `lanes` seeded images on the GPU and on the
+    oracle; returns (gpu outputs, oracle outputs) per lane."""
+    h, w, c = shape
+    b = PlanBuilder(h, w, c)
+    outs = build(b, b.input)
+    outs = outs if isinstance(outs, list) else [outs]
+    plan = b.to_bytes(outs)
+    rng = np.random.default_rng(seed)
+    xs = [rng.uniform(-1, 1, shape).astype(np.float32) for _ in range(lanes)]
+    g = GpuModel.load(plan)
+    g.set_sizes([(h, w)] * lanes)
+    for i, x in enumerate(xs):
+        g.lane_input_mut(i)[:] = x.reshape(-1)
+    g.run()
+    got = [[g.lane_output(i, k) for k in range(len(outs))] for i in range(lanes)]
+    m = oracle.OracleModel(plan)
+    want = [m.run(x) for x in xs]
+    g.close()
+    return got, want
+
+
+def exact(got, want):
+    for gl, wl in zip(got, want):
+        for a, b in zip(gl, wl):
+            assert a.shape == b.shape
+            bad = np.flatnonzero(a.view(np.uint32) != b.view(np.uint32))
+            assert bad.size == 0, f"{bad.size} of {a.size} differ, first {bad[:5]}: {a[bad[:5]]} vs {b[bad[:5]]}"
+
+
+def near(got, want, tol=1e-5):
+    for gl, wl in zip(got, want):
+        for a, b in zip(gl, wl):
+            assert a.shape == b.shape
+            scale = max(1.0, float(np.abs(b).max()))
+            err = np.abs(a.astype(np.float64) - b)
+            lim = tol * scale + tol * np.abs(b)
+            assert np.all(err <= lim), f"max err {err.max():.3g} (scale {scale:.3g})"
+
+
+@pytest.mark.parametrize("k,s,c", [(3, 1, 16), (3, 2, 24), (5, 1, 48), (5, 2, 12), (7, 1, 32),
+                                   (3, 1, 6), (7, 1, 5)])
+def test_depthwise_exact(oracle, k, s, c):
+    w = RNG.normal(0, 0.3, (k, k, c)).astype(np.float32)
+    bias = RNG.normal(0, 0.3, c).astype(np.float32)
+    got, want = both(lambda b, t: b.dwconv(t, w, bias, k=(k, k), s=(s, s), fused="hardswish"),
+                     (19, 23, c), oracle)
+    exact(got, want)
+
+
+@pytest.mark.parametrize("ci,co", [(16, 16), (24, 48), (96, 96), (12, 20), (480, 120), (8, 64)])
+def test_pointwise_gemm(oracle, ci, co):
+    w = RNG.normal(0, 1 / np.sqrt(ci), (1, 1, ci, co)).astype(np.float32)
+    bias = RNG.normal(0, 0.3, co).astype(np.float32)
+    got, want = both(lambda b, t: b.conv(t, w, bias, fused="relu"), (13, 17, ci), oracle)
+    near(got, want)
+
+
+@pytest.mark.parametrize("k,s,pad,ci,co", [((3, 3), (2, 2), (1, 1, 1, 1), 3, 24),
+                                           ((3, 3), (1, 1), (1, 1, 1, 1), 96, 24),
+                                           ((2, 2), (1, 1), (0, 1, 0, 1), 24, 12),
+                                           ((1, 3), (1, 1), (0, 0, 1, 1), 40, 60),
+                                           ((3, 3), (2, 1), (1, 1, 1, 1), 7, 33)])
+def test_windowed_gemm(oracle, k, s, pad, ci, co):
+    w = RNG.normal(0, 1 / np.sqrt(ci * k[0] * k[1]), (k[0], k[1], ci, co)).astype(np.float32)
+    bias = RNG.normal(0, 0.3, co).astype(np.float32)
+    got, want = both(lambda b, t: b.conv(t, w, bias, k=k, s=s, pad=pad, fused="swish"),
+                     (15, 18, ci), oracle)
+    near(got, want)
+
+
+def test_gemm_gate_and_residual(oracle):
+    # dw -> SE (mean, 1x1 ReLU, 1x1 hard sigmoid) -> gated pointwise + input.
+    c = 32
+    wd = RNG.normal(0, 0.3, (3, 3, c)).astype(np.float32)
+    w1 = RNG.normal(0, 0.3, (1, 1, c, 8)).astype(np.float32)
+    w2 = RNG.normal(0, 0.3, (1, 1, 8, c)).astype(np.float32)
+    wp = RNG.normal(0, 0.2, (1, 1, c, c)).astype(np.float32)
+    bv = RNG.normal(0, 0.3, c).astype(np.float32)
+
+    def build(b, t):
+        d = b.dwconv(t, wd, bv, k=(3, 3), fused="hardswish")
+        m = b.mean(d)
+        h = b.conv(m, w1, bv[:8], fused="relu")
+        g = b.conv(h, w2, bv, fused="hardsigmoid")
+        y = b.conv(b.channelmul(d, g), wp, bv)
+        return [b.add(y, t), g]
+
+    got, want = both(build, (21, 19, c), oracle)
+    near([[gl[0]] for gl in got], [[wl[0]] for wl in want])
+    # The gate: the same mean to f64 rounding, then the same 1x1 sums.
+    near([[gl[1]] for gl in got], [[wl[1]] for wl in want], tol=1e-6)
+
+
+def test_upsampled_concat_sources(oracle):
+    # The DB head's input: maps at 1/8, 1/4, 1/2 upsampled and stacked with a
+    # full-size one under a 3x3 convolution (four shifted sources).
+    c = 8
+    wq = RNG.normal(0, 0.3, (1, 1, 4, c)).astype(np.float32)
+    wh = RNG.normal(0, 0.2, (3, 3, 4 * c, 12)).astype(np.float32)
+
+    def build(b, t):
+        full = b.conv(t, wq, None)
+        half = b.avgpool(full, (2, 2), (2, 2))
+        quarter = b.avgpool(half, (2, 2), (2, 2))
+        eighth = b.avgpool(quarter, (2, 2), (2, 2))
+        cat = b.concat(b.upsample(eighth, 8), b.upsample(quarter, 4))
+        cat = b.concat(cat, b.upsample(half, 2))
+        return b.conv(cat, wh, None, k=(3, 3), pad=(1, 1, 1, 1), fused="relu", x2=full)
+
+    got, want = both(build, (16, 24, 4), oracle)
+    near(got, want)
+
+
+@pytest.mark.parametrize("mode", ["add", "resgate", "upsampleadd_resgate", "concat", "upsample"])
+def test_elementwise_exact(oracle, mode):
+    c = 12
+    w1 = RNG.normal(0, 0.5, (1, 1, c, 4)).astype(np.float32)
+    w2 = RNG.normal(0, 0.5, (1, 1, 4, c)).astype(np.float32)
+
+    def build(b, t):
+        if mode == "add":
+            return b.add(t, b.dwconv(t, np.ones((1, 1, c), np.float32), None, k=(1, 1)),
+                         fused="gelu")
+        # A gate from the squeeze-and-excite step: the CPU's bits.
+        h = b.conv(b.mean(t), w1, None, fused="relu")
+        g = b.conv(h, w2, None, fused="hardsigmoidfifth")
+        if mode == "resgate":
+            return b.add(t, b.channelmul(t, g))
+        if mode == "concat":
+            return b.concat(t, b.channelmul(t, g))
+        small = b.avgpool(t, (2, 2), (2, 2))
+        if mode == "upsample":
+            return b.upsample(small, 2)
+        r = b.add(t, b.channelmul(t, g))
+        return b.upsampleadd(small, r, 2)
+
+    got, want = both(build, (10, 14, c), oracle)
+    exact(got, want)
+
+
+def test_pools_exact(oracle):
+    def build(b, t):
+        return [b.maxpool(t), b.avgpool(t, (3, 1), (3, 1))]
+
+    got, want = both(build, (6, 11, 20), oracle)
+    exact(got, want)
+
+
+def test_layernorm_attention_exact(oracle):
+    c, heads = 120, 8
+    g = RNG.normal(1, 0.1, c).astype(np.float32)
+    be = RNG.normal(0, 0.1, c).astype(np.float32)
+    wq = RNG.normal(0, 1 / np.sqrt(c), (1, 1, c, 3 * c)).astype(np.float32)
+
+    def build(b, t):
+        n = b.layernorm(t, g, be, 1e-6)
+        qkv = b.conv(n, wq, None)
+        return [n, qkv, b.attention(qkv, heads, float(np.float32(15 ** -0.5)))]
+
+    got, want = both(build, (1, 80, c), oracle)
+    exact([[gl[0]] for gl in got], [[wl[0]] for wl in want])
+    # Attention's own arithmetic is the CPU's: fed the GPU's qkv, it is exact.
+    near([[gl[1]] for gl in got], [[wl[1]] for wl in want])
+    qkv = [gl[1] for gl in got]
+    b = PlanBuilder(1, 80, 3 * c)
+    plan = b.to_bytes([b.attention(b.input, heads, float(np.float32(15 ** -0.5)))])
+    m = oracle.OracleModel(plan)
+    for gl, q in zip(got, qkv):
+        assert np.array_equal(gl[2], m.run(q)[0])
+
+
+@pytest.mark.parametrize("oc", [1, 4])
+def test_narrow_convtranspose_exact(oracle, oc):
+    w = RNG.normal(0, 0.3, (24, 2, 2, oc)).astype(np.float32)
+    bias = RNG.normal(0, 0.3, oc).astype(np.float32)
+    got, want = both(lambda b, t: b.convtranspose(t, w, bias, k=(2, 2), fused="sigmoid"),
+                     (9, 13, 24), oracle)
+    exact(got, want)
+
+
+def test_wide_convtranspose(oracle):
+    w = RNG.normal(0, 0.3, (24, 2, 2, 24)).astype(np.float32)
+    bias = RNG.normal(0, 0.3, 24).astype(np.float32)
+    got, want = both(lambda b, t: b.convtranspose(t, w, bias, k=(2, 2), fused="relu"),
+                     (9, 13, 24), oracle)
+    near(got, want)
+
+
+@pytest.mark.parametrize("vocab", [37, 6625, 18385])
+def test_ctc_argmax(oracle, vocab):
+    c = 120
+    w = RNG.normal(0, 1 / np.sqrt(c), (c, vocab)).astype(np.float32)
+    bias = RNG.normal(0, 0.5, vocab).astype(np.float32)
+    got, want = both(lambda b, t: b.ctcargmax(t, w, bias), (1, 80, c), oracle, lanes=4)
+    for gl, wl in zip(got, want):
+        a, b = gl[0].reshape(-1, 2), wl[0].reshape(-1, 2)
+        assert np.array_equal(a[:, 0], b[:, 0])
+        np.testing.assert_allclose(a[:, 1], b[:, 1], rtol=1e-5, atol=1e-5)
