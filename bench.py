@@ -1,0 +1,283 @@
+#!/usr/bin/env python3
+"""Throughput of the GPU path on one MI355X, as one JSON line.
+
+value: detector images/s on 1x3x960x960 (the synthetic PP-OCR mobile DB
+detector plan, weights N(0, 0.05)), inputs resident in HBM, `--steps`
+forward passes timed with HIP events on the model's stream after
+`--warmup` untimed ones. Beside it: recogniser lines/s on batches of 16
+lines of 3x48x320 (weights N(0, 0.02), 18385 classes, CTC argmax), the
+fused depthwise block on 1x96x160x160, the layer microkernels, the
+roofline of the dominant launch of the detector, and the CPU oracle timed
+on this host on a bounded sample.
+"""
+from __future__ import annotations
+
+import argparse
+import importlib.util
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+PEAK_HBM_GBS = 8000.0
+PEAK_FP32_MFMA_TFLOPS = 157.3
+GEMM_LAUNCHES = {"pointwise_gemm", "conv_gemm", "convt_gemm", "ctc_gemm"}
+
+
+def package():
+    d = ROOT / "ppocr-native_amd"
+    spec = importlib.util.spec_from_file_location("ppocr_native_amd", d / "__init__.py",
+                                                  submodule_search_locations=[str(d)])
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules["ppocr_native_amd"] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def roofline(name: str, flops: float, nbytes: float, ms: float) -> dict:
+    if name in GEMM_LAUNCHES and flops > 0:
+        ach = flops / (ms * 1e-3) / 1e12
+        return {"bound": "mfma", "achieved": round(ach, 3), "peak": PEAK_FP32_MFMA_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(ach / PEAK_FP32_MFMA_TFLOPS, 4)}
+    ach = nbytes / (ms * 1e-3) / 1e9
+    return {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+            "frac": round(ach / PEAK_HBM_GBS, 4)}
+
+
+def profile(model, repeats: int) -> list[dict]:
+    names = model.launches()
+    work = model.launch_work()
+    times = model.profile_launches(repeats)
+    rows = []
+    for (name, op), (fl, by), ms in zip(names, work, times):
+        r = {"name": name, "op": op, "ms": ms, "flops": fl, "bytes": by}
+        r.update(roofline(name, fl, by, ms))
+        rows.append(r)
+    return rows
+
+
+def by_kernel(rows: list[dict]) -> dict:
+    agg: dict = {}
+    for r in rows:
+        a = agg.setdefault(r["name"], {"launches": 0, "ms": 0.0, "flops": 0.0, "bytes": 0.0})
+        a["launches"] += 1
+        a["ms"] += r["ms"]
+        a["flops"] += r["flops"]
+        a["bytes"] += r["bytes"]
+    out = {}
+    for k, a in sorted(agg.items(), key=lambda kv: -kv[1]["ms"]):
+        rl = roofline(k, a["flops"], a["bytes"], a["ms"])
+        out[k] = {"launches": a["launches"], "ms": round(a["ms"], 4), "achieved": rl["achieved"],
+                  "unit": rl["unit"], "frac": rl["frac"]}
+    return out
+
+
+def time_model(model, steps: int, warmup: int) -> tuple[float, float]:
+    """(device ms per step, wall ms per step) of resident runs."""
+    model.run_resident(warmup)
+    t0 = time.perf_counter()
+    ms = model.run_resident(steps)
+    wall = (time.perf_counter() - t0) * 1e3
+    return ms / steps, wall / steps
+
+
+def bench_detector(P, nets, steps, warmup):
+    plan = nets.detector_plan(h=960, w=960, init="baseline")
+    g = P.GpuModel.load(plan)
+    g.input_mut()[:] = nets.page_image(960, 960).reshape(-1)
+    g.upload()
+    ms, wall = time_model(g, steps, warmup)
+    # With the host copies of run() (pinned memory, PCIe), for reference.
+    g.run()
+    t0 = time.perf_counter()
+    n = max(5, steps // 4)
+    for _ in range(n):
+        g.run()
+    pcie_ms = (time.perf_counter() - t0) * 1e3 / n
+    rows = profile(g, 20)
+    g.close()
+    return plan, ms, wall, pcie_ms, rows
+
+
+def bench_recognizer(P, nets, steps, warmup):
+    plan = nets.recognizer_plan(init="baseline")
+    g = P.GpuModel.load(plan)
+    lines = nets.line_images(16)
+    g.set_sizes([(48, 320)] * 16)
+    for i in range(16):
+        g.lane_input_mut(i)[:] = lines[i].reshape(-1)
+    g.upload()
+    ms, wall = time_model(g, steps, warmup)
+    rows = profile(g, 20)
+    g.close()
+    return plan, ms, wall, rows
+
+
+def bench_block(P, nets, steps, warmup):
+    plan = nets.fused_block_plan()
+    g = P.GpuModel.load(plan)
+    g.input_mut()[:] = np.random.default_rng(5).uniform(-1, 1, 160 * 160 * 96).astype(np.float32)
+    g.upload()
+    ms, _ = time_model(g, steps, warmup)
+    rows = profile(g, 20)
+    g.close()
+    flops = sum(r["flops"] for r in rows)
+    return {"workload": "fused dw3x3+SE+pw block 1x96x160x160", "ms": round(ms, 4),
+            "gflops_per_s": round(flops / (ms * 1e-3) / 1e9, 1),
+            "compulsory_gb_per_s": round(2 * 160 * 160 * 96 * 4 / (ms * 1e-3) / 1e9, 1),
+            "launches": by_kernel(rows)}
+
+
+def bench_micro(P, repeats: int = 20) -> dict:
+    from ppocr_native_amd.devmem import DeviceArray, Timer
+    rng = np.random.default_rng(0)
+    out = {}
+
+    def timeit(fn):
+        fn()
+        t = Timer()
+        t.start()
+        for _ in range(repeats):
+            fn()
+        return t.stop() / repeats
+
+    n = 240 * 240 * 256
+    a = DeviceArray.of(rng.uniform(-1, 1, n).astype(np.float32))
+    b = DeviceArray.of(rng.uniform(-1, 1, n).astype(np.float32))
+    y = DeviceArray(4 * n)
+    for name, fn, nbytes in [
+        ("add 1x256x240x240", lambda: P.hip_add(a.addr, b.addr, y.addr, n), 12 * n),
+        ("mul 1x256x240x240", lambda: P.hip_mul(a.addr, b.addr, y.addr, n), 12 * n),
+        ("hardswish 1x256x240x240", lambda: P.hip_activation(a.addr, y.addr, n, 7), 8 * n),
+    ]:
+        ms = timeit(fn)
+        out[name] = {"ms": round(ms, 4), "gb_per_s": round(nbytes / ms / 1e6, 1),
+                     "frac_hbm": round(nbytes / ms / 1e6 / PEAK_HBM_GBS, 3)}
+    px, c = 3600, 480
+    x = DeviceArray.of(rng.uniform(-1, 1, px * c).astype(np.float32))
+    g = DeviceArray.of(rng.uniform(-1, 1, c).astype(np.float32))
+    yy = DeviceArray(4 * px * c)
+    ms = timeit(lambda: P.hip_channel_mean(x.addr, yy.addr, px, c))
+    out["mean 1x480x60x60"] = {"ms": round(ms, 4), "gb_per_s": round(4 * px * c / ms / 1e6, 1)}
+    ms = timeit(lambda: P.hip_channel_mul(x.addr, g.addr, yy.addr, px, c))
+    out["channel_mul 1x480x60x60"] = {"ms": round(ms, 4), "gb_per_s": round(8 * px * c / ms / 1e6, 1)}
+    rows, cc = 1280, 120
+    xl = DeviceArray.of(rng.uniform(-1, 1, rows * cc).astype(np.float32))
+    wl = DeviceArray.of(np.concatenate([np.ones(cc), np.zeros(cc), [1e-6]]).astype(np.float32))
+    ms = timeit(lambda: P.hip_layer_norm(xl.addr, wl.addr, yy.addr, rows, cc))
+    out["layernorm 1280x120"] = {"ms": round(ms, 4), "gb_per_s": round(8 * rows * cc / ms / 1e6, 1)}
+    cols = 18385
+    xa = DeviceArray.of(rng.normal(0, 3, rows * cols).astype(np.float32))
+    ya = DeviceArray(8 * rows)
+    ms = timeit(lambda: P.hip_row_argmax(xa.addr, ya.addr, rows, cols))
+    nb = 4 * rows * cols
+    out["row_argmax 1280x18385"] = {"ms": round(ms, 4), "gb_per_s": round(nb / ms / 1e6, 1),
+                                    "frac_hbm": round(nb / ms / 1e6 / PEAK_HBM_GBS, 3)}
+    return out
+
+
+def cpu_baseline(nets, det_plan, rec_plan, budget_s: float) -> tuple[dict, dict]:
+    sys.path.insert(0, str(ROOT))
+    import oracle
+    threads = min(os.cpu_count() or 1, 16)
+    m = oracle.OracleModel(det_plan)
+    img = nets.page_image(960, 960)
+    m.run(img, threads)
+    n, t0 = 0, time.perf_counter()
+    while n < 2 or (time.perf_counter() - t0 < budget_s and n < 20):
+        m.run(img, threads)
+        n += 1
+    det = n / (time.perf_counter() - t0)
+    r = oracle.OracleModel(rec_plan)
+    lines = nets.line_images(16)
+    r.run(lines[0], threads)
+    k, t0 = 0, time.perf_counter()
+    while k < 16 or (time.perf_counter() - t0 < budget_s / 2 and k < 64):
+        r.run(lines[k % 16], threads)
+        k += 1
+    rec = k / (time.perf_counter() - t0)
+    return ({"value": round(det, 3), "unit": "img/s", "cores": threads, "kind": "port",
+             "sample": f"{n} detector forwards at 1x3x960x960 on the C oracle (tier-3 FMA order), "
+                       f"{threads} OpenMP threads"},
+            {"value": round(rec, 2), "unit": "lines/s", "cores": threads, "kind": "port",
+             "sample": f"{k} recogniser lines of 3x48x320 one at a time, {threads} threads"})
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--only", choices=["det", "rec", "all"], default="all")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: the GPU path shards by page and by line batch with "
+              f"no exchange, and no multi-GPU figure is asked for (got --gpus {args.gpus})",
+              file=sys.stderr)
+        return 2
+    P = package()
+    from ppocr_native_amd import nets
+
+    log("bench: detector 1x3x960x960")
+    det_plan, det_ms, det_wall, pcie_ms, det_rows = bench_detector(P, nets, args.steps, args.warmup)
+    dom = max(det_rows, key=lambda r: r["ms"])
+    result = {
+        "metric": "det img/s @960², rec lines/s @16×3×48×320; % of HBM / FP32-MFMA roofline",
+        "value": round(1e3 / det_ms, 2),
+        "unit": "img/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(det_ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "PP-OCR mobile-style DB detector forward, 1x3x960x960 synthetic "
+                               "page, seeded N(0,0.05) weights (synthetic PPOCRPL1 plan)",
+                   "batch": 1, "height": 960, "width": 960},
+        "roofline": {k: dom[k] for k in ("bound", "achieved", "peak", "unit", "frac")},
+        "wall_ms_per_step": round(det_wall, 4),
+        "with_host_copies_img_per_s": round(1e3 / pcie_ms, 2),
+    }
+    result["roofline"]["traffic"] = None
+    result["roofline"]["kernel"] = f"{dom['name']} (op {dom['op']})"
+    result["roofline"]["launch_ms"] = round(dom["ms"], 5)
+    result["det_kernels"] = by_kernel(det_rows)
+    if args.only in ("rec", "all"):
+        log("bench: recogniser 16x3x48x320")
+        rec_plan, rec_ms, rec_wall, rec_rows = bench_recognizer(P, nets, args.steps, args.warmup)
+        rdom = max(rec_rows, key=lambda r: r["ms"])
+        result["rec"] = {"metric": "rec lines/s @16x3x48x320", "value": round(16e3 / rec_ms, 1),
+                         "unit": "lines/s", "ms_per_batch": round(rec_ms, 4),
+                         "roofline": {k: rdom[k] for k in ("bound", "achieved", "peak", "unit", "frac")}
+                         | {"kernel": f"{rdom['name']} (op {rdom['op']})"},
+                         "kernels": by_kernel(rec_rows)}
+        log("bench: fused block, microkernels")
+        result["block"] = bench_block(P, nets, args.steps, args.warmup)
+        result["micro"] = bench_micro(P)
+    else:
+        rec_plan = nets.recognizer_plan(init="baseline")
+    if not args.no_cpu:
+        log("bench: CPU oracle baseline")
+        det_cpu, rec_cpu = cpu_baseline(nets, det_plan, rec_plan, args.cpu_seconds)
+        result["cpu_baseline"] = det_cpu
+        if "rec" in result:
+            result["rec"]["cpu_baseline"] = rec_cpu
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

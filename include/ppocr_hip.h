@@ -103,6 +103,11 @@ void *ppocr_gpu_stream(ppocr_gpu_model *model);
 size_t ppocr_gpu_launch_count(const ppocr_gpu_model *model);
 const char *ppocr_gpu_launch_name(const ppocr_gpu_model *model, size_t i, size_t *op);
 
+/* Launch `i`'s algorithmic work for the lanes of its batch: `*flops` the
+ * layer's floating-point operations, `*bytes` what it must move (inputs and
+ * weights read once, outputs written once). Returns 0, or 1 for a bad index. */
+int ppocr_gpu_launch_work(const ppocr_gpu_model *model, size_t i, double *flops, double *bytes);
+
 /* Time each launch of one run separately: `ms` receives launch_count values,
  * each the mean over `repeats` back-to-back repeats of that launch alone. */
 int ppocr_gpu_profile_launches(ppocr_gpu_model *model, int repeats, float *ms, char *err,

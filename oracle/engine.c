@@ -547,7 +547,11 @@ static int g_threads = 1;
 
 /* Pointwise layer: conv.rs:128-143 and kernels/pointwise.rs. Calls of
  * rows_per_group rows; within a call, outputs of a multiple-of-16 width
- * start from the bias except the last count % 4 pixels. */
+ * start from the bias except the last count % 4 pixels, every other output
+ * adds it last (pointwise.rs:46-130, 584-760). Columns below co / 8 * 8 sum
+ * with fused multiply-adds; the rest multiply and add separately (the
+ * scalar tail columns of pw_any and matvec_t, pointwise.rs:723-743,
+ * matvec.rs:84-90). */
 static void pointwise(const op_t *op, const float *x, float *y, const float *w, const float *b) {
     size_t ci = op->ic, co = op->oc;
     size_t rows = (48 + op->ow - 1) / op->ow;
@@ -560,12 +564,16 @@ static void pointwise(const op_t *op, const float *x, float *y, const float *w, 
         size_t nr = op->oh - first < rows ? op->oh - first : rows;
         size_t count = nr * op->ow;
         size_t bias_first = co % 16 == 0 ? count / 4 * 4 : 0;
+        size_t fused = co / 8 * 8;
         for (size_t p = 0; p < count; p++) {
             const float *xp = x + (first * op->ow + p) * ci;
             float *yp = y + (first * op->ow + p) * co;
             for (size_t j = 0; j < co; j++) {
                 float acc = (b && p < bias_first) ? b[j] : 0.0f;
-                for (size_t i = 0; i < ci; i++) acc = fmaf(w[i * co + j], xp[i], acc);
+                if (j < fused)
+                    for (size_t i = 0; i < ci; i++) acc = fmaf(w[i * co + j], xp[i], acc);
+                else
+                    for (size_t i = 0; i < ci; i++) acc = acc + xp[i] * w[i * co + j];
                 if (b && p >= bias_first) acc = acc + b[j];
                 yp[j] = oracle_act(acc, op->fused);
             }
@@ -573,17 +581,34 @@ static void pointwise(const op_t *op, const float *x, float *y, const float *w, 
     }
 }
 
-/* Windowed dense convolution over one or two sources: kernels/dense.rs:38-147
- * (bias first, taps [ky][kx], then the channels of x and of x2). */
+/* One tap's products into the accumulators: fused for the columns below
+ * `fused`, multiply then add for the rest. */
+static inline void tap_acc(float *acc, const float *tap, const float *px, size_t n, size_t co,
+                           size_t fused) {
+    for (size_t i = 0; i < n; i++)
+        for (size_t j = 0; j < co; j++)
+            acc[j] = j < fused ? fmaf(tap[i * co + j], px[i], acc[j]) : acc[j] + px[i] * tap[i * co + j];
+}
+
+/* Windowed dense convolution over one or two sources: kernels/dense.rs:38-147,
+ * taps [ky][kx], then the channels of x and of x2. The bias comes first for a
+ * multiple-of-16 width except the row's last ow % 4 pixels, else last;
+ * columns below co / 8 * 8 use fused multiply-adds. The RGB stem (three
+ * channels, one input, conv.rs:13-14, 146-236) starts every output from its
+ * bias. */
 static void conv_window(const op_t *op, const float *x, const float *x2, float *y, const float *w,
                         const float *b) {
     size_t ct = op->ic + op->n2, co = op->oc;
+    size_t fused = co / 8 * 8;
+    int stem = op->ic == 3 && op->n2 == 0;
+    size_t first_end = stem ? op->ow : (co % 16 == 0 ? op->ow - op->ow % 4 : 0);
     long oy;
 #pragma omp parallel for schedule(static) num_threads(g_threads)
     for (oy = 0; oy < (long)op->oh; oy++) {
         float *acc = (float *)malloc(co * sizeof(float));
         for (size_t ox = 0; ox < op->ow; ox++) {
-            for (size_t j = 0; j < co; j++) acc[j] = b ? b[j] : 0.0f;
+            int bias_first = ox < first_end;
+            for (size_t j = 0; j < co; j++) acc[j] = (b && bias_first) ? b[j] : 0.0f;
             for (size_t ky = 0; ky < op->kh; ky++) {
                 long iy = (long)oy * (long)op->sh + (long)ky - op->pt;
                 if (iy < 0 || iy >= (long)op->ih) continue;
@@ -592,18 +617,18 @@ static void conv_window(const op_t *op, const float *x, const float *x2, float *
                     if (ix < 0 || ix >= (long)op->iw) continue;
                     const float *tap = w + (ky * op->kw + kx) * ct * co;
                     const float *p1 = x + ((size_t)iy * op->iw + (size_t)ix) * op->ic;
-                    for (size_t i = 0; i < op->ic; i++)
-                        for (size_t j = 0; j < co; j++) acc[j] = fmaf(tap[i * co + j], p1[i], acc[j]);
+                    tap_acc(acc, tap, p1, op->ic, co, fused);
                     if (op->n2) {
                         const float *p2 = x2 + ((size_t)iy * op->iw + (size_t)ix) * op->n2;
-                        for (size_t i = 0; i < op->n2; i++)
-                            for (size_t j = 0; j < co; j++)
-                                acc[j] = fmaf(tap[(op->ic + i) * co + j], p2[i], acc[j]);
+                        tap_acc(acc, tap + op->ic * co, p2, op->n2, co, fused);
                     }
                 }
             }
             float *yp = y + ((size_t)oy * op->ow + ox) * co;
-            for (size_t j = 0; j < co; j++) yp[j] = oracle_act(acc[j], op->fused);
+            for (size_t j = 0; j < co; j++) {
+                float v = (b && !bias_first) ? acc[j] + b[j] : acc[j];
+                yp[j] = oracle_act(v, op->fused);
+            }
         }
         free(acc);
     }
@@ -730,9 +755,11 @@ static void softmax_row(float *y, size_t n) {
     for (size_t j = 0; j < n; j++) y[j] *= r;
 }
 
-/* layers.rs:494-522: per head, S = (Q * scale) K^T from zero with FMA over
- * the head's dimensions, softmax per row, then S V from zero with FMA over
- * the keys. */
+/* layers.rs:494-522: per head, S = (Q * scale) K^T from zero over the
+ * head's dimensions (a pointwise product whose columns are the keys: fused
+ * multiply-adds below t / 8 * 8 keys, multiply then add past them), softmax
+ * per row, then S V from zero with FMA over the keys (its columns, the head
+ * padded to a multiple of 8, are all fused). */
 static void attention(const op_t *op, const float *x, float *y, float scale) {
     size_t t = op->iw, c = op->oc, heads = op->n2, hd = c / heads;
     long h;
@@ -745,8 +772,11 @@ static void attention(const op_t *op, const float *x, float *y, float scale) {
         for (size_t s = 0; s < t; s++) {
             for (size_t j = 0; j < t; j++) {
                 float acc = 0.0f;
-                for (size_t d = 0; d < hd; d++)
-                    acc = fmaf(x[j * 3 * c + c + (size_t)h * hd + d], q[s * hd + d], acc);
+                const float *k = x + j * 3 * c + c + (size_t)h * hd;
+                if (j < t / 8 * 8)
+                    for (size_t d = 0; d < hd; d++) acc = fmaf(k[d], q[s * hd + d], acc);
+                else
+                    for (size_t d = 0; d < hd; d++) acc = acc + q[s * hd + d] * k[d];
                 scores[s * t + j] = acc;
             }
             softmax_row(scores + s * t, t);
@@ -850,7 +880,10 @@ static void conv_transpose(const op_t *op, const float *x, float *y, const float
             const float *xp = x + ((size_t)iy * op->iw + ix) * ci;
             for (size_t n = 0; n < cols; n++) {
                 float acc = (b && ix < bias_first) ? b[n] : 0.0f;
-                for (size_t i = 0; i < ci; i++) acc = fmaf(w[i * cols + n], xp[i], acc);
+                if (n < cols / 8 * 8)
+                    for (size_t i = 0; i < ci; i++) acc = fmaf(w[i * cols + n], xp[i], acc);
+                else
+                    for (size_t i = 0; i < ci; i++) acc = acc + xp[i] * w[i * cols + n];
                 if (b && ix >= bias_first) acc = acc + b[n];
                 size_t tap = n / op->oc, o = n % op->oc;
                 size_t ky = tap / op->kw, kx = tap % op->kw;

@@ -65,6 +65,7 @@ def lib() -> C.CDLL:
         "ppocr_gpu_launch_count": ([vp], sz),
         "ppocr_gpu_launch_name": ([vp, sz, szp], cp),
         "ppocr_gpu_profile_launches": ([vp, C.c_int, fp, cp, sz], C.c_int),
+        "ppocr_gpu_launch_work": ([vp, sz, C.POINTER(C.c_double), C.POINTER(C.c_double)], C.c_int),
         "ppocr_hip_add": ([vp, vp, vp, sz, C.c_int, vp], C.c_int),
         "ppocr_hip_mul": ([vp, vp, vp, sz, vp], C.c_int),
         "ppocr_hip_activation": ([vp, vp, sz, C.c_int, vp], C.c_int),
@@ -178,6 +179,15 @@ class GpuModel:
             op = C.c_size_t()
             name = lib().ppocr_gpu_launch_name(self._h, i, C.byref(op))
             out.append((name.decode(), op.value))
+        return out
+
+    def launch_work(self) -> list[tuple[float, float]]:
+        """(flops, bytes) of each launch: the layer's algorithmic work."""
+        out = []
+        for i in range(lib().ppocr_gpu_launch_count(self._h)):
+            f, b = C.c_double(), C.c_double()
+            lib().ppocr_gpu_launch_work(self._h, i, C.byref(f), C.byref(b))
+            out.append((f.value, b.value))
         return out
 
     def profile_launches(self, repeats: int = 10) -> list[float]:

@@ -198,7 +198,11 @@ __global__ __launch_bounds__(256) void eltwise_kernel(EltArgs a) {
 hipError_t launch_eltwise(const EltArgs &a, hipStream_t s) {
   long n = (long)a.lanes * a.oh * a.ow * a.c;
   bool vec = a.c % 4 == 0 && (a.mode != ELT_CONCAT || (a.ca % 4 == 0 && a.cb % 4 == 0));
-  if (a.mode == ELT_ADD || a.mode == ELT_MUL || a.mode == ELT_ACT) vec = n % 4 == 0;
+  // Flat modes need whole vectors inside each lane's tensor.
+  if (a.mode == ELT_ADD || a.mode == ELT_MUL || a.mode == ELT_ACT)
+    vec = ((long)a.oh * a.ow * a.c) % 4 == 0;
+  auto a16 = [](const void *p) { return p == nullptr || (uintptr_t(p) & 15) == 0; };
+  if (!a16(a.a) || !a16(a.b) || !a16(a.g) || !a16(a.y)) vec = false;
   if (vec && (a.a_lane_stride % 4 || a.b_lane_stride % 4 || a.y_lane_stride % 4)) vec = false;
   long nv = vec ? n / 4 : n;
   unsigned blocks = blocks_for(nv, 256);
@@ -283,38 +287,71 @@ __global__ __launch_bounds__(256) void mean_partial(const float *x, long x_lane_
   }
 }
 
-// Pass 2: one block per lane joins the partials in order and divides; with
-// an SE, then the two 1x1 layers of one pixel, each output from zero with a
-// fused multiply-add per input in order, then its bias, then its activation.
-__global__ __launch_bounds__(256) void mean_finish(const double *partial, int pixels, int c,
-                                                  int chunks, SeArgs se, int has_se, float *y,
-                                                  long y_lane_stride) {
+// Pass 2: one block per lane joins the partials and divides; with an SE,
+// then the two 1x1 layers of one pixel, each output from zero with a fused
+// multiply-add per input in order, then its bias, then its activation.
+// Each channel's partials are split between J threads (a fixed split, eight
+// independent loads in flight per thread), joined in LDS in thread order.
+__global__ __launch_bounds__(1024) void mean_finish(const double *partial, int pixels, int c,
+                                                   int chunks, SeArgs se, int has_se, float *y,
+                                                   long y_lane_stride) {
   extern __shared__ float smem[];
+  __shared__ double red[1024];
   float *mean = smem;         // c
   float *hid = smem + c;      // mid
-  int ln = blockIdx.x;
+  const int ln = blockIdx.x, t = threadIdx.x;
   const double *pl = partial + (long)ln * chunks * c;
-  for (int ch = threadIdx.x; ch < c; ch += blockDim.x) {
+  for (int c0 = 0; c0 < c; c0 += 1024) {
+    const int cw = min(1024, c - c0);
+    const int J = 1024 / cw;
+    const int ch = t % cw, j = t / cw;
     double s = 0.0;
-    for (int r = 0; r < chunks; r++) s += pl[(long)r * c + ch];
-    mean[ch] = (float)(s / (double)pixels);
+    if (j < J) {
+      const double *p = pl + c0 + ch;
+      int r = j;
+      for (; r + 7 * J < chunks; r += 8 * J) {
+        double v[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) v[k] = p[(long)(r + k * J) * c];
+#pragma unroll
+        for (int k = 0; k < 8; k++) s += v[k];
+      }
+      for (; r < chunks; r += J) s += p[(long)r * c];
+    }
+    red[t] = s;
+    __syncthreads();
+    if (t < cw) {
+      double tot = 0.0;
+      for (int k = 0; k < J; k++) tot += red[k * cw + t];
+      mean[c0 + t] = (float)(tot / (double)pixels);
+    }
+    __syncthreads();
   }
-  __syncthreads();
   float *yl = y + (long)ln * y_lane_stride;
   if (!has_se) {
     for (int ch = threadIdx.x; ch < c; ch += blockDim.x) yl[ch] = mean[ch];
     return;
   }
+  // Columns below co / 8 * 8 fuse their multiply-adds; the tail columns
+  // multiply and add separately (the engine's pointwise rule for one pixel).
   for (int j = threadIdx.x; j < se.mid; j += blockDim.x) {
     float acc = 0.0f;
-    for (int i = 0; i < c; i++) acc = fmaf(se.w1[(long)i * se.mid + j], mean[i], acc);
+    const float *w = se.w1 + j;
+    if (j < se.mid / 8 * 8)
+      for (int i = 0; i < c; i++) acc = fmaf(w[(long)i * se.mid], mean[i], acc);
+    else
+      for (int i = 0; i < c; i++) acc = acc + mean[i] * w[(long)i * se.mid];
     if (se.b1) acc = acc + se.b1[j];
     hid[j] = act(acc, se.act1);
   }
   __syncthreads();
   for (int j = threadIdx.x; j < se.cout; j += blockDim.x) {
     float acc = 0.0f;
-    for (int i = 0; i < se.mid; i++) acc = fmaf(se.w2[(long)i * se.cout + j], hid[i], acc);
+    const float *w = se.w2 + j;
+    if (j < se.cout / 8 * 8)
+      for (int i = 0; i < se.mid; i++) acc = fmaf(w[(long)i * se.cout], hid[i], acc);
+    else
+      for (int i = 0; i < se.mid; i++) acc = acc + hid[i] * w[(long)i * se.cout];
     if (se.b2) acc = acc + se.b2[j];
     yl[j] = act(acc, se.act2);
   }
@@ -342,7 +379,7 @@ hipError_t launch_mean(const float *x, long x_lane_stride, int pixels, int c, in
   if (e != hipSuccess) return e;
   SeArgs none{};
   size_t shm = (size_t)(c + (se ? se->mid : 0)) * sizeof(float);
-  hipLaunchKernelGGL(mean_finish, dim3(lanes), dim3(256), shm, s, partial, pixels, c, chunks,
+  hipLaunchKernelGGL(mean_finish, dim3(lanes), dim3(1024), shm, s, partial, pixels, c, chunks,
                      se ? *se : none, se ? 1 : 0, y, y_lane_stride);
   return hipGetLastError();
 }
@@ -391,9 +428,66 @@ __global__ __launch_bounds__(64) void layernorm_kernel(const float *x, long x_la
   }
 }
 
+// One thread per row with the row in registers (MAXV float4s): the loads of
+// a row are independent and all in flight at once; the sums then run in
+// sequence as the CPU's do.
+template <int MAXV>
+__global__ __launch_bounds__(64) void layernorm_rows(const float *x, long x_lane_stride,
+                                                    const float *w, int rows, int c, int lanes,
+                                                    float *y, long y_lane_stride) {
+  long row = (long)blockIdx.x * 64 + threadIdx.x;
+  if (row >= (long)rows * lanes) return;
+  int ln = (int)(row / rows);
+  long rl = row - (long)ln * rows;
+  const int nv = c / 4;
+  const f32x4 *xr = reinterpret_cast<const f32x4 *>(x + (long)ln * x_lane_stride + rl * c);
+  f32x4 v[MAXV];
+#pragma unroll
+  for (int k = 0; k < MAXV; k++)
+    if (k < nv) v[k] = xr[k];
+  float s = 0.0f;
+#pragma unroll
+  for (int k = 0; k < MAXV; k++)
+    if (k < nv) s = (((s + v[k].x) + v[k].y) + v[k].z) + v[k].w;
+  const float mean = s / (float)c;
+  float q = 0.0f;
+#pragma unroll
+  for (int k = 0; k < MAXV; k++) {
+    if (k < nv) {
+      float d0 = v[k].x - mean, d1 = v[k].y - mean, d2 = v[k].z - mean, d3 = v[k].w - mean;
+      q = q + d0 * d0;
+      q = q + d1 * d1;
+      q = q + d2 * d2;
+      q = q + d3 * d3;
+    }
+  }
+  const float r = sqrtf(q / (float)c + w[2 * c]);
+  const f32x4 *g4 = reinterpret_cast<const f32x4 *>(w);
+  const f32x4 *b4 = reinterpret_cast<const f32x4 *>(w + c);
+  f32x4 *yr = reinterpret_cast<f32x4 *>(y + (long)ln * y_lane_stride + rl * c);
+#pragma unroll
+  for (int k = 0; k < MAXV; k++) {
+    if (k < nv) {
+      f32x4 g = g4[k], b = b4[k], o;
+      o.x = (v[k].x - mean) / r * g.x + b.x;
+      o.y = (v[k].y - mean) / r * g.y + b.y;
+      o.z = (v[k].z - mean) / r * g.z + b.z;
+      o.w = (v[k].w - mean) / r * g.w + b.w;
+      yr[k] = o;
+    }
+  }
+}
+
 hipError_t launch_layernorm(const float *x, long x_lane_stride, const float *w, int rows, int c,
                             int lanes, float *y, long y_lane_stride, hipStream_t s) {
   long total = (long)rows * lanes;
+  auto a16 = [](const void *p) { return (uintptr_t(p) & 15) == 0; };
+  if (c % 4 == 0 && c <= 128 && a16(x) && a16(y) && a16(w) && a16(w + c) &&
+      x_lane_stride % 4 == 0 && y_lane_stride % 4 == 0) {
+    hipLaunchKernelGGL(layernorm_rows<32>, dim3(blocks_for(total, 64)), dim3(64), 0, s, x,
+                       x_lane_stride, w, rows, c, lanes, y, y_lane_stride);
+    return hipGetLastError();
+  }
   size_t shm = (size_t)64 * (c + 1) * sizeof(float);
   if (shm > 64 * 1024) return hipErrorInvalidValue;
   hipLaunchKernelGGL(layernorm_kernel, dim3(blocks_for(total, 64)), dim3(64), shm, s, x,
@@ -403,97 +497,147 @@ hipError_t launch_layernorm(const float *x, long x_lane_stride, const float *w, 
 
 // ------------------------------------------------------------ attention
 
-// One block per (lane, head): K and V of the head in LDS, one thread per
-// query (looping when t exceeds the block). Scores from zero with a fused
-// multiply-add per head dimension against the pre-scaled query, an 8-lane
-// softmax, then each output from zero with a fused multiply-add per key.
-__global__ __launch_bounds__(128) void attention_kernel(const float *x, long x_lane_stride,
+// One block of 256 threads per (lane, head), in three phases that keep the
+// engine's order for every value (src/engine/layers.rs:494-522, 273-294):
+//  1. each score from zero, a fused multiply-add per head dimension against
+//     the pre-scaled query; threads take (query, key) pairs;
+//  2. softmax per row in 8 lanes: thread (row, l) keeps lane l (keys j with
+//     j % 8 == l below the last whole group of 8); the row's maximum and sum
+//     then join the lanes in order, the tail one key at a time;
+//  3. each output from zero, a fused multiply-add per key in order against
+//     the rounded probability; threads take (query, dimension) pairs.
+// Q, K and V of the head sit in LDS; the t x t scores too, or for long lines
+// in global scratch.
+__global__ __launch_bounds__(256) void attention_kernel(const float *x, long x_lane_stride,
                                                        float scale, int t, int c, int heads,
                                                        float *y, long y_lane_stride,
                                                        float *gscores) {
   extern __shared__ float sm[];
   const int hd = c / heads;
   const int ln = blockIdx.x / heads, h = blockIdx.x % heads;
-  float *ks = sm;                 // t * hd
-  float *vs = ks + t * hd;        // t * hd
-  // blockDim.x score rows of t + 1: in LDS, or for long lines in global memory.
-  float *sc = gscores ? gscores + (long)blockIdx.x * blockDim.x * (t + 1) : vs + t * hd;
+  const int tid = threadIdx.x, nt = blockDim.x;
+  const int ts = t + 1;  // score row stride
+  float *qs = sm;                  // t * hd, pre-scaled
+  float *ks = qs + t * hd;         // t * hd
+  float *vs = ks + t * hd;         // t * hd
+  float *lane_max = vs + t * hd;   // t * 8
+  float *lane_sum = lane_max + t * 8;  // t * 8
+  float *rinv = lane_sum + t * 8;      // t: row maximum, then 1 / sum
+  float *rmax = rinv + t;              // t
+  float *sc = gscores ? gscores + (long)blockIdx.x * t * ts : rmax + t;
   const float *xl = x + (long)ln * x_lane_stride;
-  for (int e = threadIdx.x; e < t * hd; e += blockDim.x) {
+  for (int e = tid; e < t * hd; e += nt) {
     int j = e / hd, d = e - j * hd;
-    ks[e] = xl[(long)j * 3 * c + c + h * hd + d];
-    vs[e] = xl[(long)j * 3 * c + 2 * c + h * hd + d];
+    const float *px = xl + (long)j * 3 * c + h * hd + d;
+    qs[e] = px[0] * scale;
+    ks[e] = px[c];
+    vs[e] = px[2 * c];
   }
   __syncthreads();
-  float *row = sc + threadIdx.x * (t + 1);
-  for (int s = threadIdx.x; s < t; s += blockDim.x) {
-    float q[64];
-    for (int d = 0; d < hd; d++) q[d] = xl[(long)s * 3 * c + h * hd + d] * scale;
-    for (int j = 0; j < t; j++) {
-      float acc = 0.0f;
-      for (int d = 0; d < hd; d++) acc = fmaf(ks[j * hd + d], q[d], acc);
-      row[j] = acc;
-    }
-    // Softmax of the row in 8 lanes (src/engine/layers.rs:273-294).
-    int body = t / 8 * 8;
-    float lanes_[8];
-    for (int l = 0; l < 8; l++) lanes_[l] = -__builtin_inff();
-    for (int j = 0; j < body; j++) {
-      float v = row[j];
-      lanes_[j & 7] = v > lanes_[j & 7] ? v : lanes_[j & 7];
-    }
-    float mx = -__builtin_inff();
-    for (int l = 0; l < 8; l++) mx = fmaxf(mx, lanes_[l]);
-    for (int j = body; j < t; j++) mx = fmaxf(mx, row[j]);
-    float sums[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int j = 0; j < body; j++) {
-      float e = exp_neg(row[j] - mx);
-      row[j] = e;
-      sums[j & 7] = sums[j & 7] + e;
-    }
+  const int fused = t / 8 * 8;  // keys past it multiply and add separately
+  for (int e = tid; e < t * t; e += nt) {
+    int s = e / t, j = e - s * t;
+    const float *q = qs + s * hd, *k = ks + j * hd;
+    float acc = 0.0f;
+    if (j < fused)
+      for (int d = 0; d < hd; d++) acc = fmaf(k[d], q[d], acc);
+    else
+      for (int d = 0; d < hd; d++) acc = acc + q[d] * k[d];
+    sc[s * ts + j] = acc;
+  }
+  __syncthreads();
+  const int body = t / 8 * 8;
+  const float ninf = -__builtin_inff();
+  for (int e = tid; e < t * 8; e += nt) {
+    int s = e >> 3, l = e & 7;
+    const float *row = sc + s * ts;
+    float m = ninf;
+    for (int j = l; j < body; j += 8) m = row[j] > m ? row[j] : m;
+    lane_max[e] = m;
+  }
+  __syncthreads();
+  for (int s = tid; s < t; s += nt) {
+    const float *row = sc + s * ts;
+    float m = ninf;
+    for (int l = 0; l < 8; l++) m = fmaxf(m, lane_max[s * 8 + l]);
+    for (int j = body; j < t; j++) m = fmaxf(m, row[j]);
+    rmax[s] = m;
+  }
+  __syncthreads();
+  for (int e = tid; e < t * 8; e += nt) {
+    int s = e >> 3, l = e & 7;
+    float *row = sc + s * ts;
+    const float m = rmax[s];
     float sum = 0.0f;
-    for (int l = 0; l < 8; l++) sum = sum + sums[l];
+    for (int j = l; j < body; j += 8) {
+      float ex = exp_neg(row[j] - m);
+      row[j] = ex;
+      sum = sum + ex;
+    }
+    lane_sum[e] = sum;
+  }
+  __syncthreads();
+  for (int s = tid; s < t; s += nt) {
+    float *row = sc + s * ts;
+    const float m = rmax[s];
+    float sum = 0.0f;
+    for (int l = 0; l < 8; l++) sum = sum + lane_sum[s * 8 + l];
     for (int j = body; j < t; j++) {
-      float e = exp_neg(row[j] - mx);
-      row[j] = e;
-      sum = sum + e;
+      float ex = exp_neg(row[j] - m);
+      row[j] = ex;
+      sum = sum + ex;
     }
-    float r = 1.0f / sum;
-    for (int j = 0; j < t; j++) row[j] = row[j] * r;
-    float *out = y + (long)ln * y_lane_stride + (long)s * c + h * hd;
-    for (int d = 0; d < hd; d++) {
-      float acc = 0.0f;
-      for (int j = 0; j < t; j++) acc = fmaf(vs[j * hd + d], row[j], acc);
-      out[d] = acc;
-    }
+    rinv[s] = 1.0f / sum;
+  }
+  __syncthreads();
+  for (int e = tid; e < t * t; e += nt) {
+    int s = e / t, j = e - s * t;
+    sc[s * ts + j] = sc[s * ts + j] * rinv[s];
+  }
+  __syncthreads();
+  float *yl = y + (long)ln * y_lane_stride + h * hd;
+  for (int e = tid; e < t * hd; e += nt) {
+    int s = e / hd, d = e - s * hd;
+    const float *p = sc + s * ts;
+    float acc = 0.0f;
+    for (int j = 0; j < t; j++) acc = fmaf(vs[j * hd + d], p[j], acc);
+    yl[(long)s * c + d] = acc;
   }
 }
 
-static int attention_threads(int t) { return t < 128 ? ((t + 63) / 64) * 64 : 128; }
+static size_t attention_lds_floats(int t, int hd, bool scores) {
+  return (size_t)3 * t * hd + (size_t)t * 18 + (scores ? (size_t)t * (t + 1) : 0);
+}
+
+// gfx950 has 160 KiB of LDS per CU; a kernel may use it all once allowed to.
+static const size_t kMaxLds = 160 * 1024;
 
 static bool attention_in_lds(int t, int hd) {
-  size_t shm = ((size_t)2 * t * hd + (size_t)attention_threads(t) * (t + 1)) * sizeof(float);
-  return shm <= 64 * 1024;
+  return attention_lds_floats(t, hd, true) * sizeof(float) <= kMaxLds;
 }
 
 size_t attention_scratch_floats(int t, int c, int heads, int lanes) {
   int hd = c / heads;
   if (attention_in_lds(t, hd)) return 0;
-  return (size_t)lanes * heads * attention_threads(t) * (t + 1);
+  return (size_t)lanes * heads * t * (t + 1);
 }
 
 hipError_t launch_attention(const float *x, long x_lane_stride, float scale, int t, int c,
                             int heads, int lanes, float *y, long y_lane_stride, float *scratch,
                             hipStream_t s) {
+  if (heads <= 0 || c % heads) return hipErrorInvalidValue;
   int hd = c / heads;
-  if (hd > 64 || heads <= 0 || c % heads) return hipErrorInvalidValue;
-  int threads = attention_threads(t);
   bool lds = attention_in_lds(t, hd);
   if (!lds && !scratch) return hipErrorInvalidValue;
-  size_t shm = ((size_t)2 * t * hd + (lds ? (size_t)threads * (t + 1) : 0)) * sizeof(float);
-  if (shm > 64 * 1024) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(attention_kernel, dim3(lanes * heads), dim3(threads), shm, s, x,
-                     x_lane_stride, scale, t, c, heads, y, y_lane_stride, lds ? nullptr : scratch);
+  size_t shm = attention_lds_floats(t, hd, lds) * sizeof(float);
+  if (shm > kMaxLds) return hipErrorInvalidValue;
+  if (shm > 64 * 1024) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&attention_kernel),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, int(kMaxLds));
+    if (e != hipSuccess) return e;
+  }
+  hipLaunchKernelGGL(attention_kernel, dim3(lanes * heads), dim3(256), shm, s, x, x_lane_stride,
+                     scale, t, c, heads, y, y_lane_stride, lds ? nullptr : scratch);
   return hipGetLastError();
 }
 
@@ -588,11 +732,14 @@ __global__ __launch_bounds__(256) void convt_small_kernel(ConvtArgs a) {
   float acc[16];
 #pragma unroll
   for (int n = 0; n < 16; n++) acc[n] = first && n < cols ? a.bias[n] : 0.0f;
+  const int fused = cols / 8 * 8;  // tail columns multiply and add separately
   for (int i = 0; i < a.ic; i++) {
     float v = xp[i];
 #pragma unroll
-    for (int n = 0; n < 16; n++)
-      if (n < cols) acc[n] = fmaf(a.w[(long)i * cols + n], v, acc[n]);
+    for (int n = 0; n < 16; n++) {
+      if (n < fused) acc[n] = fmaf(a.w[(long)i * cols + n], v, acc[n]);
+      else if (n < cols) acc[n] = acc[n] + v * a.w[(long)i * cols + n];
+    }
   }
   float *yl = a.y + (long)ln * a.y_lane_stride;
   const long ow = (long)a.iw * a.kw;

@@ -90,6 +90,10 @@ struct Launch {
   std::string name;
   int op;
   std::function<hipError_t(hipStream_t)> fn;
+  // Algorithmic work of the launch: floating-point operations of the layer,
+  // and bytes it must move (each input and the weights read once, each
+  // output written once), for roofline fractions.
+  double flops = 0, bytes = 0;
 };
 
 // A batch of lanes of one size.
@@ -137,6 +141,7 @@ struct Model {
   bool set_sizes(const size_t *hw, size_t n, std::string &err);
   bool arrange(Batch &b, std::string &err);
   void build_launches(Batch &b);
+  void account(Batch &b) const;
   bool run(bool copy_in, bool copy_out, std::string &err);
   std::vector<size_t> step_reads(const Step &s) const;
   size_t step_writes(const Step &s) const;
@@ -551,6 +556,7 @@ bool Model::arrange(Batch &b, std::string &err) {
     }
   }
   build_launches(b);
+  account(b);
   return true;
 }
 
@@ -734,6 +740,86 @@ void Model::build_launches(Batch &b) {
         b.launches.push_back({"convt_small", s.op, [a](hipStream_t st) { return launch_convt_small(a, st); }});
         break;
       }
+    }
+  }
+}
+
+// Each launch's algorithmic work, in the order build_launches made them.
+void Model::account(Batch &b) const {
+  const Plan &p = b.plan;
+  const double L = double(b.lanes.size()), F = 4.0;
+  size_t li = 0;
+  for (const Step &s : steps) {
+    const Op &op = p.ops[s.op];
+    const double in_px = double(op.ih) * op.iw, out_px = double(op.oh) * op.ow;
+    Launch &l = b.launches[li++];
+    switch (s.kind) {
+      case S_GEMM: {
+        double M, K = 0, N = s.gemm_n, in = 0;
+        if (op.kind == K_CONVTRANSPOSE) {
+          M = L * in_px, K = double(op.ic), in = M * K;
+        } else {
+          M = L * out_px;
+          for (const Source &src : s.sources) {
+            K += double(op.kh * op.kw) * src.c;
+            in += L * double(op.ih >> src.shift) * double(op.iw >> src.shift) * src.c;
+          }
+          if (s.gate >= 0) in += L * op.ic;
+          if (s.add >= 0) in += M * N;
+        }
+        l.flops = 2.0 * M * N * K;
+        l.bytes = F * (in + M * N + K * N + (op.b1 ? N : 0));
+        break;
+      }
+      case S_CTC: {
+        double M = L * op.iw, K = double(op.ic), N = double(op.n2);
+        double ntn = double((s.gemm_n + s.tile.bn - 1) / s.tile.bn);
+        l.flops = 2.0 * M * N * K;
+        l.bytes = F * (M * K + K * N + N + 2 * M);
+        Launch &merge = b.launches[li++];
+        merge.bytes = F * (M * ntn * 4 + 2 * M);
+        break;
+      }
+      case S_DW:
+        l.flops = 2.0 * L * out_px * op.oc * op.kh * op.kw;
+        l.bytes = F * (L * in_px * op.ic + L * out_px * op.oc + double(op.kh * op.kw + 1) * op.oc);
+        break;
+      case S_ELT: {
+        double out = L * out_px * op.oc, src = L * in_px * op.ic;
+        switch (s.elt) {
+          case ELT_ADD: l.bytes = F * 3 * out; break;
+          case ELT_CHANNELMUL: case ELT_RESGATE: l.bytes = F * (2 * out + L * op.oc); break;
+          case ELT_UPSAMPLE: l.bytes = F * (src + out); break;
+          case ELT_UPSAMPLEADD: l.bytes = F * (src + 2 * out); break;
+          case ELT_UPSAMPLEADD_RESGATE: l.bytes = F * (src + 2 * out + L * op.oc); break;
+          default: l.bytes = F * 2 * out;
+        }
+        break;
+      }
+      case S_POOL:
+        l.bytes = F * L * (in_px * op.ic + out_px * op.oc);
+        break;
+      case S_MEAN:
+        l.bytes = F * L * (in_px * op.ic + op.oc);
+        if (s.fc1 >= 0) {
+          const Op &f1 = p.ops[s.fc1], &f2 = p.ops[s.fc2];
+          l.flops = 2.0 * L * (double(f1.ic) * f1.oc + double(f2.ic) * f2.oc);
+          l.bytes += F * (double(f1.w1 + f1.b1 + f2.w1 + f2.b1));
+        }
+        break;
+      case S_LN:
+        l.bytes = F * (2 * L * out_px * op.oc + op.w1);
+        break;
+      case S_ATTN: {
+        double t = double(op.iw), hd = double(op.oc / op.n2);
+        l.flops = L * op.n2 * t * t * hd * 4;
+        l.bytes = F * L * t * (op.ic + op.oc);
+        break;
+      }
+      case S_CONVT:
+        l.flops = 2.0 * L * in_px * op.ic * op.kh * op.kw * op.oc;
+        l.bytes = F * (L * in_px * op.ic + L * out_px * op.oc + op.w1 + op.b1);
+        break;
     }
   }
 }
@@ -998,6 +1084,15 @@ const char *ppocr_gpu_launch_name(const ppocr_gpu_model *model, size_t i, size_t
   if (!l) return nullptr;
   if (op) *op = size_t(l->op);
   return l->name.c_str();
+}
+
+int ppocr_gpu_launch_work(const ppocr_gpu_model *model, size_t i, double *flops, double *bytes) {
+  if (!model) return 1;
+  const ppocr::Launch *l = launch_at(model, i);
+  if (!l) return 1;
+  if (flops) *flops = l->flops;
+  if (bytes) *bytes = l->bytes;
+  return 0;
 }
 
 int ppocr_gpu_profile_launches(ppocr_gpu_model *model, int repeats, float *ms, char *err, size_t err_len) {

@@ -189,6 +189,17 @@ def test_layernorm_attention_exact(oracle):
         assert np.array_equal(gl[2], m.run(q)[0])
 
 
+@pytest.mark.parametrize("t,heads,hd", [(80, 8, 15), (41, 8, 15), (9, 2, 3), (160, 4, 32),
+                                        (320, 8, 15)])
+def test_attention_exact(oracle, t, heads, hd):
+    # Keys past t // 8 * 8 use separate products and sums; 320 steps keep
+    # the scores in global scratch instead of LDS.
+    c = heads * hd
+    got, want = both(lambda b, x: b.attention(x, heads, float(np.float32(hd ** -0.5))),
+                     (1, t, 3 * c), oracle, lanes=2)
+    exact(got, want)
+
+
 @pytest.mark.parametrize("oc", [1, 4])
 def test_narrow_convtranspose_exact(oracle, oc):
     w = RNG.normal(0, 0.3, (24, 2, 2, oc)).astype(np.float32)

@@ -114,7 +114,10 @@ def test_pointwise_bias_rules(oracle, co):
         for j in range(0, co, 5):
             acc = np.float32(bias[j]) if first else np.float32(0)
             for i in range(9):
-                acc = np.float32(np.float64(w[0, 0, i, j]) * np.float64(xf[p, i]) + np.float64(acc))
+                if j < co // 8 * 8:  # fused multiply-add
+                    acc = np.float32(np.float64(w[0, 0, i, j]) * np.float64(xf[p, i]) + np.float64(acc))
+                else:                # the tail columns: product, then sum
+                    acc = np.float32(acc + np.float32(xf[p, i] * w[0, 0, i, j]))
             if not first:
                 acc = np.float32(acc + bias[j])
             assert y[p, j] == acc, (p, j)
