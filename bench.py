@@ -95,6 +95,9 @@ def bench_detector(P, nets, steps, warmup):
     g.input_mut()[:] = nets.page_image(960, 960).reshape(-1)
     g.upload()
     ms, wall = time_model(g, steps, warmup)
+    g.set_graphs(False)
+    eager_ms, _ = time_model(g, steps, warmup)
+    g.set_graphs(True)
     # With the host copies of run() (pinned memory, PCIe), for reference.
     g.run()
     t0 = time.perf_counter()
@@ -104,7 +107,7 @@ def bench_detector(P, nets, steps, warmup):
     pcie_ms = (time.perf_counter() - t0) * 1e3 / n
     rows = profile(g, 20)
     g.close()
-    return plan, ms, wall, pcie_ms, rows
+    return plan, ms, wall, pcie_ms, rows, eager_ms
 
 
 def bench_recognizer(P, nets, steps, warmup):
@@ -116,9 +119,11 @@ def bench_recognizer(P, nets, steps, warmup):
         g.lane_input_mut(i)[:] = lines[i].reshape(-1)
     g.upload()
     ms, wall = time_model(g, steps, warmup)
+    g.set_graphs(False)
+    eager_ms, _ = time_model(g, steps, warmup)
     rows = profile(g, 20)
     g.close()
-    return plan, ms, wall, rows
+    return plan, ms, wall, rows, eager_ms
 
 
 def bench_block(P, nets, steps, warmup):
@@ -154,6 +159,8 @@ def bench_micro(P, repeats: int = 20) -> dict:
     b = DeviceArray.of(rng.uniform(-1, 1, n).astype(np.float32))
     y = DeviceArray(4 * n)
     for name, fn, nbytes in [
+        # A plain copy (activation code 0): the reference for HBM counters.
+        ("copy 1x256x240x240", lambda: P.hip_activation(a.addr, y.addr, n, 0), 8 * n),
         ("add 1x256x240x240", lambda: P.hip_add(a.addr, b.addr, y.addr, n), 12 * n),
         ("mul 1x256x240x240", lambda: P.hip_mul(a.addr, b.addr, y.addr, n), 12 * n),
         ("hardswish 1x256x240x240", lambda: P.hip_activation(a.addr, y.addr, n, 7), 8 * n),
@@ -229,7 +236,8 @@ def main() -> int:
     from ppocr_native_amd import nets
 
     log("bench: detector 1x3x960x960")
-    det_plan, det_ms, det_wall, pcie_ms, det_rows = bench_detector(P, nets, args.steps, args.warmup)
+    det_plan, det_ms, det_wall, pcie_ms, det_rows, det_eager = bench_detector(P, nets, args.steps,
+                                                                              args.warmup)
     dom = max(det_rows, key=lambda r: r["ms"])
     result = {
         "metric": "det img/s @960², rec lines/s @16×3×48×320; % of HBM / FP32-MFMA roofline",
@@ -249,21 +257,27 @@ def main() -> int:
                    "batch": 1, "height": 960, "width": 960},
         "roofline": {k: dom[k] for k in ("bound", "achieved", "peak", "unit", "frac")},
         "wall_ms_per_step": round(det_wall, 4),
+        "eager_ms_per_step": round(det_eager, 4),
         "with_host_copies_img_per_s": round(1e3 / pcie_ms, 2),
     }
     result["roofline"]["traffic"] = None
     result["roofline"]["kernel"] = f"{dom['name']} (op {dom['op']})"
     result["roofline"]["launch_ms"] = round(dom["ms"], 5)
     result["det_kernels"] = by_kernel(det_rows)
+    result["det_launches"] = [[r["name"], r["op"], round(r["ms"] * 1e3, 1), r["frac"]] for r in det_rows]
     if args.only in ("rec", "all"):
         log("bench: recogniser 16x3x48x320")
-        rec_plan, rec_ms, rec_wall, rec_rows = bench_recognizer(P, nets, args.steps, args.warmup)
+        rec_plan, rec_ms, rec_wall, rec_rows, rec_eager = bench_recognizer(P, nets, args.steps,
+                                                                           args.warmup)
         rdom = max(rec_rows, key=lambda r: r["ms"])
         result["rec"] = {"metric": "rec lines/s @16x3x48x320", "value": round(16e3 / rec_ms, 1),
                          "unit": "lines/s", "ms_per_batch": round(rec_ms, 4),
+                         "eager_ms_per_batch": round(rec_eager, 4),
                          "roofline": {k: rdom[k] for k in ("bound", "achieved", "peak", "unit", "frac")}
                          | {"kernel": f"{rdom['name']} (op {rdom['op']})"},
-                         "kernels": by_kernel(rec_rows)}
+                         "kernels": by_kernel(rec_rows),
+                         "launches": [[r["name"], r["op"], round(r["ms"] * 1e3, 1), r["frac"]]
+                                      for r in rec_rows]}
         log("bench: fused block, microkernels")
         result["block"] = bench_block(P, nets, args.steps, args.warmup)
         result["micro"] = bench_micro(P)

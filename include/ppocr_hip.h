@@ -98,6 +98,11 @@ int ppocr_gpu_download(ppocr_gpu_model *model, char *err, size_t err_len);
 /* The model's HIP stream, as a hipStream_t. */
 void *ppocr_gpu_stream(ppocr_gpu_model *model);
 
+/* Runs record their launches in a HIP graph from the second run after the
+ * lanes were set, and replay it (default, `enable` 1); with 0 every run
+ * launches each kernel itself. Returns 0, or 1 for a NULL model. */
+int ppocr_gpu_set_graphs(ppocr_gpu_model *model, int enable);
+
 /* Kernel launches one run makes, and launch `i`'s kernel name (valid for the
  * model's lifetime) and the plan operation it starts from. */
 size_t ppocr_gpu_launch_count(const ppocr_gpu_model *model);

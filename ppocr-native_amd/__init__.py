@@ -62,6 +62,7 @@ def lib() -> C.CDLL:
         "ppocr_gpu_run_resident": ([vp, C.c_int, fp, cp, sz], C.c_int),
         "ppocr_gpu_download": ([vp, cp, sz], C.c_int),
         "ppocr_gpu_stream": ([vp], vp),
+        "ppocr_gpu_set_graphs": ([vp, C.c_int], C.c_int),
         "ppocr_gpu_launch_count": ([vp], sz),
         "ppocr_gpu_launch_name": ([vp, sz, szp], cp),
         "ppocr_gpu_profile_launches": ([vp, C.c_int, fp, cp, sz], C.c_int),
@@ -172,6 +173,10 @@ class GpuModel:
 
     def stream(self) -> int:
         return lib().ppocr_gpu_stream(self._h) or 0
+
+    def set_graphs(self, enable: bool) -> None:
+        """Replay runs from a captured HIP graph (default) or launch eagerly."""
+        lib().ppocr_gpu_set_graphs(self._h, int(enable))
 
     def launches(self) -> list[tuple[str, int]]:
         out = []

@@ -1,21 +1,26 @@
 // Dense convolution as an implicit matrix product on FP32 MFMA (gfx950).
 //
 // Row m of the product is an output pixel of some lane (lanes stacked along
-// M), column n an output channel. The reduction runs over chunks of BK: for
-// each tap (ky, kx) of the window, each source's channels in steps of BK,
-// zero past the source's channels or outside the image. This is the plan's
-// weight order [kh][kw][ic + n2][oc] (src/engine/plan.rs:83-86,
-// shaders/gemm.comp:2-18), with each source padded to whole chunks; the host
-// packs the weights in that padded order, one row of the reduction per output
-// column, so a chunk of weights is one contiguous 16-byte-aligned run.
+// M), column n an output channel. The reduction follows the plan's weight
+// order [kh][kw][ic + n2][oc] (src/engine/plan.rs:83-86, shaders/gemm.comp:
+// 2-18): taps in [ky][kx] order, in each tap the channels of every source in
+// turn (up to four sources, each possibly a nearest upsampling by 2^shift
+// folded in), zero outside the image. It runs in chunks of BK:
+//  - channel layout (all sources' channels a multiple of 4): each tap's
+//    channels padded to whole chunks, read four channels at a time;
+//  - flat layout (other channel counts, e.g. an RGB stem): the whole
+//    reduction taps * channels padded to whole chunks, read one at a time.
+// The host packs the weights in the same padded order, one row of the
+// reduction per output column, so a chunk of weights is one aligned run.
 //
 // A workgroup is four waves over a BM x BN tile (BM = 4 * WM); each wave owns
 // WM rows and all BN columns as (WM/16) x (BN/16) tiles of
 // v_mfma_f32_16x16x4_f32. Within a chunk, lane l (group g = l / 16) supplies
 // reduction indices g*BK/4 .. g*BK/4 + BK/4 - 1, one per MFMA step, so each
-// lane reads its A and B values with one LDS vector load per tile. Operands
-// are staged in LDS rows of BK + 4 floats (conflict-free for these reads);
-// the next chunk's global loads are issued before the current chunk's MFMAs.
+// lane reads its operands with vector LDS loads. Operands sit in two LDS
+// buffers of rows of BK + 4 floats: while the MFMAs consume one chunk, the
+// next chunk's global loads are in flight and then stored to the other
+// buffer, one barrier per chunk.
 //
 // Epilogues: bias, activation, then optionally a residual add and a second
 // activation (an Add folded in); a transposed convolution's spread store; or
@@ -63,11 +68,22 @@ __device__ __forceinline__ CtcState ctc_join(CtcState x, CtcState y) {
   return r;
 }
 
+// The source holding channel c of a tap's concatenation.
+__device__ __forceinline__ ConvSrc pick_src(const ConvArgs &a, int c) {
+  ConvSrc s = a.src[0];
+  if (a.nsrc > 1 && c >= a.src[1].coff) s = a.src[1];
+  if (a.nsrc > 2 && c >= a.src[2].coff) s = a.src[2];
+  if (a.nsrc > 3 && c >= a.src[3].coff) s = a.src[3];
+  return s;
+}
+
 template <int WM, int BN, int BK, bool VEC, bool PW, bool CTC>
 __global__ __launch_bounds__(256) void conv_mfma(ConvArgs a) {
   constexpr int BM = 4 * WM;
   constexpr int S = BK + 4;
   constexpr int KS = BK / 4;
+  constexpr int KW = KS >= 4 ? 4 : KS;  // floats per LDS operand read
+  constexpr int KR = KS / KW;           // operand reads per chunk
   constexpr int MT = WM / 16, NT = BN / 16;
   constexpr int AV = VEC ? 4 : 1;
   constexpr int A_KV = BK / AV;
@@ -77,10 +93,10 @@ __global__ __launch_bounds__(256) void conv_mfma(ConvArgs a) {
   constexpr int B_ELEMS = BN * B_KV;
   constexpr int B_PER = (B_ELEMS + 255) / 256;
   typedef typename VecT<AV>::T AT;
-  typedef typename VecT<KS>::T KT;
+  typedef typename VecT<KW>::T KT;
 
-  __shared__ __attribute__((aligned(16))) float As[BM * S];
-  __shared__ __attribute__((aligned(16))) float Bs[BN * S];
+  __shared__ __attribute__((aligned(16))) float As[2][BM * S];
+  __shared__ __attribute__((aligned(16))) float Bs[2][BN * S];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int per_lane = a.oh * a.ow;
@@ -124,45 +140,47 @@ __global__ __launch_bounds__(256) void conv_mfma(ConvArgs a) {
     b_ptr[i] = a.wt + (long)(n0 + (b_ok[i] ? nn : 0)) * a.wt_k + kv * 4;
   }
 
-  const int taps = a.kh * a.kw;
-  const int cpt = a.chunks / taps;
-
   AT ra[A_PER];
   f32x4 rb[B_PER];
 
   auto load = [&](int q) {
-    int tap = q / cpt, r = q - tap * cpt, s = 0;
-    ConvSrc src = a.src[0];
-    if (!PW) {
-      // Unrolled so the sources stay in kernel-argument registers.
-      if (a.nsrc > 1 && r >= src.chunks) { r -= src.chunks; s = 1; src = a.src[1]; }
-      if (a.nsrc > 2 && s == 1 && r >= src.chunks) { r -= src.chunks; s = 2; src = a.src[2]; }
-      if (a.nsrc > 3 && s == 2 && r >= src.chunks) { r -= src.chunks; s = 3; src = a.src[3]; }
+    int tap = 0, cbase = 0;
+    if (VEC) {
+      tap = q / a.cpt;
+      cbase = (q - tap * a.cpt) * BK;
     }
-    const int c0 = r * BK;
-    const int ky = tap / a.kw, kx = tap - ky * a.kw;
-    const int sw_ = a.iw >> src.shift;
 #pragma unroll
     for (int i = 0; i < A_PER; i++) {
-      const int c = c0 + a_kv[i] * AV;
+      int t = tap, c;
+      if (VEC) {
+        c = cbase + a_kv[i] * AV;
+      } else {
+        int k = q * BK + a_kv[i];
+        t = k / a.ctot;
+        c = k - t * a.ctot;
+      }
       AT v;
       if constexpr (AV == 4) v = f32x4{0.f, 0.f, 0.f, 0.f};
       else v = 0.0f;
-      bool live = a_ok[i] && c < src.c;
-      long pix = 0;
+      bool live = a_ok[i] && c < a.ctot && t < a.kh * a.kw;
       if (PW) {
-        pix = a_y[i];
+        if (live) {
+          const ConvSrc &src = a.src[0];
+          v = *reinterpret_cast<const AT *>(src.p + (long)a_lane[i] * src.lane_stride +
+                                            (long)a_y[i] * src.c + c);
+          if (a.gate) v = v * *reinterpret_cast<const AT *>(a.gate + (long)a_lane[i] * a.gate_lane_stride + c);
+        }
       } else {
+        int ky = t / a.kw, kx = t - ky * a.kw;
         int iy = a_y[i] + ky, ix = a_x[i] + kx;
         live = live && iy >= 0 && iy < a.ih && ix >= 0 && ix < a.iw;
-        pix = (long)(iy >> src.shift) * sw_ + (ix >> src.shift);
-      }
-      if (live) {
-        const float *p = src.p + (long)a_lane[i] * src.lane_stride + pix * src.c + c;
-        v = *reinterpret_cast<const AT *>(p);
-        if (s == 0 && a.gate) {
-          const float *g = a.gate + (long)a_lane[i] * a.gate_lane_stride + c;
-          v = v * *reinterpret_cast<const AT *>(g);
+        if (live) {
+          const ConvSrc src = pick_src(a, c);
+          int cl = c - src.coff;
+          long pix = (long)(iy >> src.shift) * (a.iw >> src.shift) + (ix >> src.shift);
+          v = *reinterpret_cast<const AT *>(src.p + (long)a_lane[i] * src.lane_stride + pix * src.c + cl);
+          if (a.gate && src.coff == 0)
+            v = v * *reinterpret_cast<const AT *>(a.gate + (long)a_lane[i] * a.gate_lane_stride + cl);
         }
       }
       ra[i] = v;
@@ -171,6 +189,14 @@ __global__ __launch_bounds__(256) void conv_mfma(ConvArgs a) {
     for (int i = 0; i < B_PER; i++) {
       if (b_ok[i]) rb[i] = *reinterpret_cast<const f32x4 *>(b_ptr[i] + (long)q * BK);
     }
+  };
+  auto store = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < A_PER; i++)
+      if (tid + 256 * i < A_ELEMS) *reinterpret_cast<AT *>(&As[buf][a_row[i] * S + a_kv[i] * AV]) = ra[i];
+#pragma unroll
+    for (int i = 0; i < B_PER; i++)
+      if (b_ok[i]) *reinterpret_cast<f32x4 *>(&Bs[buf][b_off[i]]) = rb[i];
   };
 
   f32x4 acc[MT][NT];
@@ -181,40 +207,40 @@ __global__ __launch_bounds__(256) void conv_mfma(ConvArgs a) {
 
   const int li = lane & 15, lg = lane >> 4;
   load(0);
+  store(0);
+  __syncthreads();
   for (int q = 0; q < a.chunks; q++) {
-#pragma unroll
-    for (int i = 0; i < A_PER; i++)
-      if (tid + 256 * i < A_ELEMS) *reinterpret_cast<AT *>(&As[a_row[i] * S + a_kv[i] * AV]) = ra[i];
-#pragma unroll
-    for (int i = 0; i < B_PER; i++)
-      if (b_ok[i]) *reinterpret_cast<f32x4 *>(&Bs[b_off[i]]) = rb[i];
-    __syncthreads();
+    const int cur = q & 1;
     if (q + 1 < a.chunks) load(q + 1);
-    KT av[MT], bv[NT];
 #pragma unroll
-    for (int i = 0; i < MT; i++)
-      av[i] = *reinterpret_cast<const KT *>(&As[(wave * WM + i * 16 + li) * S + lg * KS]);
+    for (int r = 0; r < KR; r++) {
+      KT av[MT], bv[NT];
 #pragma unroll
-    for (int j = 0; j < NT; j++)
-      bv[j] = *reinterpret_cast<const KT *>(&Bs[(j * 16 + li) * S + lg * KS]);
+      for (int i = 0; i < MT; i++)
+        av[i] = *reinterpret_cast<const KT *>(&As[cur][(wave * WM + i * 16 + li) * S + lg * KS + r * KW]);
 #pragma unroll
-    for (int k = 0; k < KS; k++) {
+      for (int j = 0; j < NT; j++)
+        bv[j] = *reinterpret_cast<const KT *>(&Bs[cur][(j * 16 + li) * S + lg * KS + r * KW]);
 #pragma unroll
-      for (int i = 0; i < MT; i++) {
+      for (int k = 0; k < KW; k++) {
 #pragma unroll
-        for (int j = 0; j < NT; j++) {
-          float x, w;
-          if constexpr (KS == 1) {
-            x = av[i];
-            w = bv[j];
-          } else {
-            x = av[i][k];
-            w = bv[j][k];
+        for (int i = 0; i < MT; i++) {
+#pragma unroll
+          for (int j = 0; j < NT; j++) {
+            float x, w;
+            if constexpr (KW == 1) {
+              x = av[i];
+              w = bv[j];
+            } else {
+              x = av[i][k];
+              w = bv[j][k];
+            }
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(x, w, acc[i][j], 0, 0, 0);
           }
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(x, w, acc[i][j], 0, 0, 0);
         }
       }
     }
+    if (q + 1 < a.chunks) store(cur ^ 1);
     __syncthreads();
   }
 
@@ -317,31 +343,48 @@ static hipError_t go(const ConvArgs &a, hipStream_t s) {
   return hipGetLastError();
 }
 
-#define PPOCR_TILES(BK, VEC, PW)                                         \
+#define PPOCR_TILES(BK, VEC, PW)                                              \
   if (t.wm == 32 && t.bn == 64) return go<32, 64, BK, VEC, PW, false>(a, s); \
   if (t.wm == 32 && t.bn == 32) return go<32, 32, BK, VEC, PW, false>(a, s); \
   if (t.wm == 32 && t.bn == 16) return go<32, 16, BK, VEC, PW, false>(a, s); \
   if (t.wm == 16 && t.bn == 64) return go<16, 64, BK, VEC, PW, false>(a, s);
 
+#define PPOCR_TILES_SMALL(BK, VEC, PW)                                        \
+  if (t.wm == 16 && t.bn == 64) return go<16, 64, BK, VEC, PW, false>(a, s); \
+  if (t.wm == 16 && t.bn == 32) return go<16, 32, BK, VEC, PW, false>(a, s); \
+  if (t.wm == 16 && t.bn == 16) return go<16, 16, BK, VEC, PW, false>(a, s);
+
+bool gemm_tile_supported(const GemmTile &t) {
+  if (t.bk == 64) return t.vec && t.wm == 16 && (t.bn == 16 || t.bn == 32 || t.bn == 64);
+  bool tile = (t.wm == 32 && (t.bn == 16 || t.bn == 32 || t.bn == 64)) || (t.wm == 16 && t.bn == 64);
+  if (!tile) return false;
+  if (t.vec) return t.bk == 8 || t.bk == 16 || t.bk == 32;
+  return !t.pointwise && (t.bk == 8 || t.bk == 16 || t.bk == 32);
+}
+
 hipError_t launch_conv(const ConvArgs &a, const GemmTile &t, hipStream_t s) {
   if (a.mode == GEMM_CTC) {
-    if (!t.pointwise || !t.vec) return hipErrorInvalidValue;
-    if (t.wm == 32 && t.bn == 64 && t.bk == 16) return go<32, 64, 16, true, true, true>(a, s);
-    if (t.wm == 32 && t.bn == 64 && t.bk == 8) return go<32, 64, 8, true, true, true>(a, s);
+    if (!t.pointwise || !t.vec || t.bn != 64) return hipErrorInvalidValue;
+    if (t.wm == 32 && t.bk == 8) return go<32, 64, 8, true, true, true>(a, s);
+    if (t.wm == 32 && t.bk == 16) return go<32, 64, 16, true, true, true>(a, s);
     return hipErrorInvalidValue;
   }
-  if (t.pointwise) {
-    if (!t.vec) return hipErrorInvalidValue;
+  if (!gemm_tile_supported(t)) return hipErrorInvalidValue;
+  if (t.vec && t.pointwise) {
+    if (t.bk == 64) { PPOCR_TILES_SMALL(64, true, true) }
+    if (t.bk == 32) { PPOCR_TILES(32, true, true) }
     if (t.bk == 16) { PPOCR_TILES(16, true, true) }
     if (t.bk == 8) { PPOCR_TILES(8, true, true) }
-    return hipErrorInvalidValue;
-  }
-  if (t.vec) {
+  } else if (t.vec) {
+    if (t.bk == 64) { PPOCR_TILES_SMALL(64, true, false) }
+    if (t.bk == 32) { PPOCR_TILES(32, true, false) }
     if (t.bk == 16) { PPOCR_TILES(16, true, false) }
     if (t.bk == 8) { PPOCR_TILES(8, true, false) }
-    return hipErrorInvalidValue;
+  } else {
+    if (t.bk == 32) { PPOCR_TILES(32, false, false) }
+    if (t.bk == 16) { PPOCR_TILES(16, false, false) }
+    if (t.bk == 8) { PPOCR_TILES(8, false, false) }
   }
-  if (t.bk == 4) { PPOCR_TILES(4, false, false) }
   return hipErrorInvalidValue;
 }
 

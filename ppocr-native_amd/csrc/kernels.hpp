@@ -13,14 +13,15 @@ namespace ppocr {
 
 // ---------------------------------------------------------------- GEMM conv
 
-// One input of an implicit-GEMM convolution: `c` channels, `shift` > 0 when it
-// is read as nearest-upsampled by 2^shift (an upsampling folded in).
+// One input of an implicit-GEMM convolution: `c` channels starting at channel
+// `coff` of each tap's concatenation, `shift` > 0 when it is read as
+// nearest-upsampled by 2^shift (an upsampling folded in).
 struct ConvSrc {
   const float *p;
   long lane_stride;
   int c;
   int shift;
-  int chunks;  // ceil(c / BK): reduction chunks this source gives each tap
+  int coff;
 };
 
 enum GemmMode : int { GEMM_STORE = 0, GEMM_SPREAD = 1, GEMM_CTC = 2 };
@@ -32,7 +33,9 @@ struct ConvArgs {
   int kh, kw, sh, sw, pt, pl;
   int nsrc;
   ConvSrc src[4];
-  int chunks;           // total reduction chunks: kh * kw * sum of src chunks
+  int ctot;             // channels of a tap: the sources' sum
+  int cpt;              // channel layout: chunks per tap, ceil(ctot / BK)
+  int chunks;           // reduction chunks: kh * kw * cpt, or ceil(kh * kw * ctot / BK)
   const float *wt;      // packed weights [n_pad][chunks * BK], zero padded
   long wt_k;            // floats per packed weight row (chunks * BK)
   const float *bias;    // n values or null
@@ -51,10 +54,13 @@ struct ConvArgs {
 
 struct GemmTile {
   int wm, bn, bk;  // wave rows (4 waves per tile), tile columns, reduction chunk
-  bool vec;        // channels read 4 at a time
+  bool vec;        // channel layout, four channels at a time (else flat layout)
   bool pointwise;  // 1x1, stride 1, no padding, one source
 };
 
+// Tiles launch_conv has compiled: BK 8, 16, 32 with WM 32 (BN 16, 32, 64) or
+// WM 16 (BN 64); BK 64 (channel layout) with WM 16 and BN 16, 32, 64.
+bool gemm_tile_supported(const GemmTile &t);
 hipError_t launch_conv(const ConvArgs &a, const GemmTile &t, hipStream_t s);
 
 // CTC choice from the GEMM's per-tile partials: y[2m] = best, y[2m+1] = 1/sum.

@@ -92,6 +92,80 @@ __global__ __launch_bounds__(256) void dwconv_kernel(DwArgs a) {
   }
 }
 
+// The same arithmetic with the window's size K and stride S known at compile
+// time: each kernel row's input segment ((DX - 1) * S + K pixels of four
+// channels) is loaded once, every load of the row issued before the first
+// multiply-add; taps outside the image are skipped, as in the engine.
+template <int K, int S, int DX>
+__global__ __launch_bounds__(256) void dwconv_fixed(DwArgs a) {
+  constexpr int SPAN = (DX - 1) * S + K;
+  const int cv = a.c / 4;
+  const int runs = (a.ow + DX - 1) / DX;
+  long g = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  long total = (long)a.lanes * a.oh * runs * cv;
+  if (g >= total) return;
+  int ch = (int)(g % cv) * 4;
+  long t = g / cv;
+  int run = (int)(t % runs);
+  t /= runs;
+  int oy = (int)(t % a.oh);
+  int ln = (int)(t / a.oh);
+  int ox0 = run * DX;
+  const float *x = a.x + (long)ln * a.x_lane_stride + ch;
+  const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+  f32x4 acc[DX];
+  f32x4 bias = a.bias ? *reinterpret_cast<const f32x4 *>(a.bias + ch) : zero;
+#pragma unroll
+  for (int o = 0; o < DX; o++) acc[o] = bias;
+  const int left = ox0 * S - a.pl;
+#pragma unroll
+  for (int ky = 0; ky < K; ky++) {
+    const int iy = oy * a.sh + ky - a.pt;
+    if (iy < 0 || iy >= a.ih) continue;
+    const float *row = x + (long)iy * a.iw * a.c;
+    f32x4 seg[SPAN], wk[K];
+    bool in[SPAN];
+#pragma unroll
+    for (int i = 0; i < SPAN; i++) {
+      const int ix = left + i;
+      in[i] = ix >= 0 && ix < a.iw;
+      seg[i] = in[i] ? *reinterpret_cast<const f32x4 *>(row + (long)ix * a.c) : zero;
+    }
+#pragma unroll
+    for (int kx = 0; kx < K; kx++) wk[kx] = *reinterpret_cast<const f32x4 *>(a.w + (long)(ky * K + kx) * a.c + ch);
+#pragma unroll
+    for (int kx = 0; kx < K; kx++) {
+#pragma unroll
+      for (int o = 0; o < DX; o++) {
+        const int i = o * S + kx;
+        if (in[i]) {
+          acc[o].x = fmaf(wk[kx].x, seg[i].x, acc[o].x);
+          acc[o].y = fmaf(wk[kx].y, seg[i].y, acc[o].y);
+          acc[o].z = fmaf(wk[kx].z, seg[i].z, acc[o].z);
+          acc[o].w = fmaf(wk[kx].w, seg[i].w, acc[o].w);
+        }
+      }
+    }
+  }
+  float *y = a.y + (long)ln * a.y_lane_stride + ((long)oy * a.ow) * a.c + ch;
+#pragma unroll
+  for (int o = 0; o < DX; o++) {
+    if (ox0 + o >= a.ow) break;
+    f32x4 v = acc[o];
+    v.x = act(v.x, a.act);
+    v.y = act(v.y, a.act);
+    v.z = act(v.z, a.act);
+    v.w = act(v.w, a.act);
+    *reinterpret_cast<f32x4 *>(y + (long)(ox0 + o) * a.c) = v;
+  }
+}
+
+template <typename F>
+static hipError_t launch_fixed(F kernel, dim3 grid, dim3 block, const DwArgs &a, hipStream_t s) {
+  hipLaunchKernelGGL(kernel, grid, block, 0, s, a);
+  return hipGetLastError();
+}
+
 hipError_t launch_dwconv(const DwArgs &a, hipStream_t s) {
   constexpr int DX = 4;
   auto aligned = [](const void *p) { return p == nullptr || (uintptr_t(p) & 15) == 0; };
@@ -99,10 +173,25 @@ hipError_t launch_dwconv(const DwArgs &a, hipStream_t s) {
              a.x_lane_stride % 4 == 0 && a.y_lane_stride % 4 == 0;
   long runs = (a.ow + DX - 1) / DX;
   long total = (long)a.lanes * a.oh * runs * (vec ? a.c / 4 : a.c);
+  dim3 grid(blocks_for(total, 256)), block(256);
+  if (vec && a.kh == a.kw && a.sh == a.sw) {
+    const int k = a.kh, st = a.sw;
+    if (k == 3 && st == 1) return launch_fixed(dwconv_fixed<3, 1, DX>, grid, block, a, s);
+    if (k == 3 && st == 2) return launch_fixed(dwconv_fixed<3, 2, DX>, grid, block, a, s);
+    if (k == 5 && st == 1) return launch_fixed(dwconv_fixed<5, 1, DX>, grid, block, a, s);
+    if (k == 5 && st == 2) return launch_fixed(dwconv_fixed<5, 2, DX>, grid, block, a, s);
+    if (k == 7 && st == 1) return launch_fixed(dwconv_fixed<7, 1, DX>, grid, block, a, s);
+  }
+  if (vec && a.kh == a.kw && a.sh != a.sw && a.sw == 1) {
+    // Height-only strides (the recogniser's (2, 1) stages).
+    const int k = a.kh;
+    if (k == 3) return launch_fixed(dwconv_fixed<3, 1, DX>, grid, block, a, s);
+    if (k == 5) return launch_fixed(dwconv_fixed<5, 1, DX>, grid, block, a, s);
+  }
   if (vec)
-    hipLaunchKernelGGL((dwconv_kernel<4, DX>), dim3(blocks_for(total, 256)), dim3(256), 0, s, a);
+    hipLaunchKernelGGL((dwconv_kernel<4, DX>), grid, block, 0, s, a);
   else
-    hipLaunchKernelGGL((dwconv_kernel<1, DX>), dim3(blocks_for(total, 256)), dim3(256), 0, s, a);
+    hipLaunchKernelGGL((dwconv_kernel<1, DX>), grid, block, 0, s, a);
   return hipGetLastError();
 }
 
@@ -508,10 +597,11 @@ hipError_t launch_layernorm(const float *x, long x_lane_stride, const float *w, 
 //     the rounded probability; threads take (query, dimension) pairs.
 // Q, K and V of the head sit in LDS; the t x t scores too, or for long lines
 // in global scratch.
-__global__ __launch_bounds__(256) void attention_kernel(const float *x, long x_lane_stride,
-                                                       float scale, int t, int c, int heads,
-                                                       float *y, long y_lane_stride,
-                                                       float *gscores) {
+template <int HDV, int NT>
+__global__ __launch_bounds__(NT) void attention_kernel(const float *x, long x_lane_stride,
+                                                      float scale, int t, int c, int heads,
+                                                      float *y, long y_lane_stride,
+                                                      float *gscores) {
   extern __shared__ float sm[];
   const int hd = c / heads;
   const int ln = blockIdx.x / heads, h = blockIdx.x % heads;
@@ -538,11 +628,22 @@ __global__ __launch_bounds__(256) void attention_kernel(const float *x, long x_l
   for (int e = tid; e < t * t; e += nt) {
     int s = e / t, j = e - s * t;
     const float *q = qs + s * hd, *k = ks + j * hd;
+    float qv[HDV], kv[HDV];
+#pragma unroll
+    for (int d = 0; d < HDV; d++) {
+      qv[d] = d < hd ? q[d] : 0.0f;
+      kv[d] = d < hd ? k[d] : 0.0f;
+    }
     float acc = 0.0f;
-    if (j < fused)
-      for (int d = 0; d < hd; d++) acc = fmaf(k[d], q[d], acc);
-    else
-      for (int d = 0; d < hd; d++) acc = acc + q[d] * k[d];
+    if (j < fused) {
+#pragma unroll
+      for (int d = 0; d < HDV; d++)
+        if (d < hd) acc = fmaf(kv[d], qv[d], acc);
+    } else {
+#pragma unroll
+      for (int d = 0; d < HDV; d++)
+        if (d < hd) acc = acc + qv[d] * kv[d];
+    }
     sc[s * ts + j] = acc;
   }
   __syncthreads();
@@ -599,8 +700,17 @@ __global__ __launch_bounds__(256) void attention_kernel(const float *x, long x_l
   for (int e = tid; e < t * hd; e += nt) {
     int s = e / hd, d = e - s * hd;
     const float *p = sc + s * ts;
+    const float *v = vs + d;
     float acc = 0.0f;
-    for (int j = 0; j < t; j++) acc = fmaf(vs[j * hd + d], p[j], acc);
+    int j = 0;
+    for (; j + 8 <= t; j += 8) {
+      float vv[8], pp[8];
+#pragma unroll
+      for (int u = 0; u < 8; u++) vv[u] = v[(j + u) * hd], pp[u] = p[j + u];
+#pragma unroll
+      for (int u = 0; u < 8; u++) acc = fmaf(vv[u], pp[u], acc);
+    }
+    for (; j < t; j++) acc = fmaf(v[j * hd], p[j], acc);
     yl[(long)s * c + d] = acc;
   }
 }
@@ -627,18 +737,30 @@ hipError_t launch_attention(const float *x, long x_lane_stride, float scale, int
                             hipStream_t s) {
   if (heads <= 0 || c % heads) return hipErrorInvalidValue;
   int hd = c / heads;
+  if (hd > 64) return hipErrorInvalidValue;
   bool lds = attention_in_lds(t, hd);
   if (!lds && !scratch) return hipErrorInvalidValue;
   size_t shm = attention_lds_floats(t, hd, lds) * sizeof(float);
   if (shm > kMaxLds) return hipErrorInvalidValue;
-  if (shm > 64 * 1024) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&attention_kernel),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, int(kMaxLds));
-    if (e != hipSuccess) return e;
-  }
-  hipLaunchKernelGGL(attention_kernel, dim3(lanes * heads), dim3(256), shm, s, x, x_lane_stride,
-                     scale, t, c, heads, y, y_lane_stride, lds ? nullptr : scratch);
-  return hipGetLastError();
+  float *g = lds ? nullptr : scratch;
+  auto go = [&](auto kernel, int nt) {
+    // Allowed once per kernel, before any use beyond 64 KiB (and so before a
+    // graph capture records such a launch).
+    static bool allowed[3] = {false, false, false};
+    bool &done = allowed[nt == 1024 ? 0 : (nt == 512 ? 1 : 2)];
+    if (shm > 64 * 1024 && !done) {
+      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, int(kMaxLds));
+      if (e != hipSuccess) return e;
+      done = true;
+    }
+    hipLaunchKernelGGL(kernel, dim3(lanes * heads), dim3(nt), shm, s, x, x_lane_stride, scale, t,
+                       c, heads, y, y_lane_stride, g);
+    return hipGetLastError();
+  };
+  if (hd <= 16) return go(attention_kernel<16, 1024>, 1024);
+  if (hd <= 32) return go(attention_kernel<32, 512>, 512);
+  return go(attention_kernel<64, 256>, 256);
 }
 
 // ------------------------------------------------------------ CTC choice

@@ -81,9 +81,8 @@ struct Step {
   std::vector<Source> sources;
   // Implicit-GEMM steps
   GemmTile tile{};
-  int gemm_n = 0, chunks = 0;
+  int gemm_n = 0, chunks = 0, ctot = 0, cpt = 0;
   size_t wt_off = 0, wt_k = 0;
-  std::vector<int> src_chunks;
 };
 
 struct Launch {
@@ -133,8 +132,17 @@ struct Model {
   std::vector<std::pair<size_t, size_t>> lane_at;  // lane -> (batch, index in batch)
   std::vector<std::pair<size_t, size_t>> sizes;
   size_t active_batches = 0;
+  // The launches of one run over every batch, captured as a HIP graph on the
+  // second run after the lanes were arranged (the first runs them eagerly,
+  // which also sets any kernel attribute outside the capture).
+  bool use_graphs = true;
+  int eager_runs = 0;
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t graph_exec = nullptr;
 
   ~Model();
+  void drop_graph();
+  bool enqueue(std::string &err);
   bool load(const uint8_t *bytes, size_t len, std::string &err);
   bool build_steps(std::string &err);
   bool pack(std::string &err);
@@ -149,6 +157,7 @@ struct Model {
 
 Model::~Model() {
   if (stream) hipStreamSynchronize(stream);
+  drop_graph();
   for (auto &b : batches) {
     if (b->arena) hipFree(b->arena);
     if (b->host_in) hipHostFree(b->host_in);
@@ -366,16 +375,22 @@ bool Model::build_steps(std::string &err) {
   return true;
 }
 
-// Choose each GEMM step's tile and repack its weights: row n of the packed
-// matrix holds column n's reduction in the kernel's chunk order (tap, source,
-// channel chunk), zero where a source's channels do not fill a chunk.
+// Choose each GEMM step's reduction chunk and tile, and repack its weights:
+// row n of the packed matrix holds column n's reduction in the kernel's chunk
+// order, zero where the padding of a chunk lies.
+//  - channel layout (every source's channels a multiple of 4): per tap, the
+//    tap's concatenated channels padded to cpt * BK;
+//  - flat layout: taps * channels as one run padded to whole chunks.
+// BK: the largest of 64, 32, 16, 8 that pads a tap's channels by at most an
+// eighth, else the one that pads least: fewer chunks mean fewer load
+// latencies in sequence, which is what small layers wait on.
 bool Model::pack(std::string &err) {
   std::vector<float> packed;
   const auto &ops = plan.ops;
   for (Step &s : steps) {
     if (s.kind != S_GEMM && s.kind != S_CTC) continue;
     const Op &op = ops[s.op];
-    int K_taps = 1, N;
+    int taps = 1, N;
     std::vector<Source> srcs = s.sources;
     if (s.kind == S_CTC) {
       srcs = {{op.x, int(op.ic), 0}};
@@ -383,31 +398,45 @@ bool Model::pack(std::string &err) {
     } else if (op.kind == K_CONVTRANSPOSE) {
       N = int(op.kh * op.kw * op.oc);
     } else {
-      K_taps = int(op.kh * op.kw);
+      taps = int(op.kh * op.kw);
       N = int(op.oc);
     }
     bool vec = true;
-    for (auto &x : srcs) vec = vec && x.c % 4 == 0;
+    int ctot = 0;
+    for (auto &x : srcs) vec = vec && x.c % 4 == 0, ctot += x.c;
     bool pw = (op.kind != K_CONV || op.is_pointwise()) && srcs.size() == 1 && srcs[0].shift == 0 && vec;
-    int bk = 4;
+    int bk, cpt = 0;
     if (vec) {
-      long k16 = 0, k8 = 0;
-      for (auto &x : srcs) k16 += (x.c + 15) / 16 * 16, k8 += (x.c + 7) / 8 * 8;
-      bk = k8 < k16 ? 8 : 16;
+      int best = 0;
+      double best_waste = 1e9;
+      for (int cand : {64, 32, 16, 8}) {
+        double waste = double((ctot + cand - 1) / cand * cand) / ctot - 1.0;
+        if (waste <= 0.125) {
+          best = cand;
+          break;
+        }
+        if (waste < best_waste - 1e-12) best = cand, best_waste = waste;
+      }
+      bk = best;
+      // The CTC head has thousands of tiles and is throughput-bound: small
+      // chunks keep the LDS footprint small and the occupancy high.
+      if (s.kind == S_CTC) bk = 8;
+      cpt = (ctot + bk - 1) / bk;
+      s.chunks = taps * cpt;
+    } else {
+      int K = taps * ctot;
+      bk = K <= 8 ? 8 : (K <= 16 ? 16 : 32);
+      s.chunks = (K + bk - 1) / bk;
     }
     int bn = N <= 16 ? 16 : (N <= 32 ? 32 : 64);
-    int wm = 32;
     if (s.kind == S_CTC) bn = 64;
+    int wm = bk == 64 ? 16 : 32;
     s.tile = GemmTile{wm, bn, bk, vec, pw};
+    if (!gemm_tile_supported(s.tile) && s.kind != S_CTC)
+      return err = fmt("operation %d: no GEMM tile for this shape", s.op), false;
     s.gemm_n = N;
-    s.src_chunks.clear();
-    int cpt = 0;
-    for (auto &x : srcs) {
-      int ch = (x.c + bk - 1) / bk;
-      s.src_chunks.push_back(ch);
-      cpt += ch;
-    }
-    s.chunks = K_taps * cpt;
+    s.ctot = ctot;
+    s.cpt = cpt;
     s.wt_k = size_t(s.chunks) * bk;
     int n_pad = (N + bn - 1) / bn * bn;
     size_t start = round_up(packed.size(), 64);
@@ -415,24 +444,14 @@ bool Model::pack(std::string &err) {
     s.wt_off = start;
     float *dst = packed.data() + start;
     const float *w = weights.data() + op.w0;
-    int ctot = 0;
-    for (auto &x : srcs) ctot += x.c;
     for (int nn = 0; nn < N; nn++) {
       float *row = dst + size_t(nn) * s.wt_k;
-      size_t k = 0;
-      for (int tap = 0; tap < K_taps; tap++) {
-        int coff = 0;
-        for (size_t si = 0; si < srcs.size(); si++) {
-          int c = srcs[si].c;
-          for (int cc = 0; cc < s.src_chunks[si] * bk; cc++, k++) {
-            if (cc >= c) continue;
-            size_t kk = size_t(tap) * ctot + coff + cc;  // plan reduction index
-            float v;
-            if (s.kind == S_CTC) v = w[(size_t(nn) / 16) * op.ic * 16 + kk * 16 + nn % 16];
-            else v = w[kk * N + nn];
-            row[k] = v;
-          }
-          coff += c;
+      for (int tap = 0; tap < taps; tap++) {
+        for (int c = 0; c < ctot; c++) {
+          size_t kk = size_t(tap) * ctot + c;  // the plan's reduction index
+          size_t k = vec ? size_t(tap) * cpt * bk + c : kk;
+          row[k] = s.kind == S_CTC ? w[(size_t(nn) / 16) * op.ic * 16 + kk * 16 + nn % 16]
+                                   : w[kk * N + nn];
         }
       }
     }
@@ -588,10 +607,13 @@ void Model::build_launches(Batch &b) {
           a.mode = GEMM_STORE;
         }
         a.nsrc = int(s.sources.size());
+        int coff = 0;
         for (size_t k = 0; k < s.sources.size(); k++) {
           const Source &src = s.sources[k];
-          a.src[k] = ConvSrc{b.dev(src.slot), b.stride(src.slot), src.c, src.shift, s.src_chunks[k]};
+          a.src[k] = ConvSrc{b.dev(src.slot), b.stride(src.slot), src.c, src.shift, coff};
+          coff += src.c;
         }
+        a.ctot = s.ctot, a.cpt = s.cpt;
         a.chunks = s.chunks;
         a.wt = dpacked + s.wt_off;
         a.wt_k = long(s.wt_k);
@@ -611,6 +633,7 @@ void Model::build_launches(Batch &b) {
         GemmTile t = s.tile;
         long M = long(L) * a.oh * a.ow;
         long tiles = (M + 127) / 128 * ((a.n + t.bn - 1) / t.bn);
+        // Fewer than four tiles per CU of 128 rows: take 64-row tiles.
         if (t.bn == 64 && tiles < 1024) t.wm = 16;
         const char *nm = op.kind == K_CONVTRANSPOSE ? "convt_gemm" : (t.pointwise ? "pointwise_gemm" : "conv_gemm");
         b.launches.push_back({nm, s.op, [a, t](hipStream_t st) { return launch_conv(a, t, st); }});
@@ -623,7 +646,8 @@ void Model::build_launches(Batch &b) {
         a.n = s.gemm_n;
         a.kh = a.kw = a.sh = a.sw = 1;
         a.nsrc = 1;
-        a.src[0] = ConvSrc{b.dev(op.x), b.stride(op.x), int(op.ic), 0, s.src_chunks[0]};
+        a.src[0] = ConvSrc{b.dev(op.x), b.stride(op.x), int(op.ic), 0, 0};
+        a.ctot = s.ctot, a.cpt = s.cpt;
         a.chunks = s.chunks;
         a.wt = dpacked + s.wt_off;
         a.wt_k = long(s.wt_k);
@@ -852,6 +876,7 @@ bool Model::set_sizes(const size_t *hw, size_t n, std::string &err) {
     at[i] = {g, members[g].size()};
     members[g].push_back(i);
   }
+  drop_graph();  // the lanes' memory moves: record the run again
   while (batches.size() < order.size()) batches.emplace_back(new Batch());
   lane_at.clear();
   sizes.clear();
@@ -872,28 +897,73 @@ bool Model::set_sizes(const size_t *hw, size_t n, std::string &err) {
   return true;
 }
 
+void Model::drop_graph() {
+  if (graph_exec) hipGraphExecDestroy(graph_exec);
+  if (graph) hipGraphDestroy(graph);
+  graph_exec = nullptr;
+  graph = nullptr;
+  eager_runs = 0;
+}
+
+// Enqueue every batch's launches once on the stream: eagerly the first time
+// after the lanes were arranged, from the captured graph afterwards. A
+// capture that fails leaves the model running eagerly.
+bool Model::enqueue(std::string &err) {
+  if (use_graphs && !graph_exec && eager_runs >= 1) {
+    bool ok = hipStreamBeginCapture(stream, hipStreamCaptureModeRelaxed) == hipSuccess;
+    for (size_t g = 0; ok && g < active_batches; g++)
+      for (const Launch &l : batches[g]->launches) ok = ok && l.fn(stream) == hipSuccess;
+    hipGraph_t captured = nullptr;
+    hipError_t end = hipStreamEndCapture(stream, &captured);
+    ok = ok && end == hipSuccess && captured;
+    if (ok && hipGraphInstantiate(&graph_exec, captured, nullptr, nullptr, 0) == hipSuccess) {
+      graph = captured;
+    } else {
+      if (captured) hipGraphDestroy(captured);
+      graph_exec = nullptr;
+      use_graphs = false;
+      (void)hipGetLastError();
+    }
+  }
+  if (graph_exec) {
+    HIPTRY(hipGraphLaunch(graph_exec, stream), "launching the run's graph");
+    return true;
+  }
+  for (size_t g = 0; g < active_batches; g++) {
+    for (const Launch &l : batches[g]->launches) {
+      hipError_t e = l.fn(stream);
+      if (e != hipSuccess)
+        return err = fmt("launching %s (operation %d): %s", l.name.c_str(), l.op, hipGetErrorString(e)), false;
+    }
+  }
+  eager_runs++;
+  return true;
+}
+
 bool Model::run(bool copy_in, bool copy_out, std::string &err) {
   HIPTRY(hipSetDevice(device), "selecting the GPU");
   if (lane_at.empty()) return err = "no lanes are set", false;
-  for (size_t g = 0; g < active_batches; g++) {
-    Batch &b = *batches[g];
-    const size_t L = b.lanes.size();
-    const Plan &p = b.plan;
-    if (copy_in)
+  if (copy_in) {
+    for (size_t g = 0; g < active_batches; g++) {
+      Batch &b = *batches[g];
+      const Plan &p = b.plan;
       HIPTRY(hipMemcpy2DAsync(b.dev(p.in_slot), b.stride(p.in_slot) * sizeof(float), b.host_in,
-                              b.in_len * sizeof(float), b.in_len * sizeof(float), L,
+                              b.in_len * sizeof(float), b.in_len * sizeof(float), b.lanes.size(),
                               hipMemcpyHostToDevice, stream),
              "copying the input");
-    for (const Launch &l : b.launches) {
-      hipError_t e = l.fn(stream);
-      if (e != hipSuccess) return err = fmt("launching %s (operation %d): %s", l.name.c_str(), l.op, hipGetErrorString(e)), false;
     }
-    if (copy_out)
+  }
+  if (!enqueue(err)) return false;
+  if (copy_out) {
+    for (size_t g = 0; g < active_batches; g++) {
+      Batch &b = *batches[g];
+      const Plan &p = b.plan;
       for (size_t k = 0; k < p.out_slot.size(); k++)
         HIPTRY(hipMemcpy2DAsync(b.host_out[k], p.out_n[k] * sizeof(float), b.dev(p.out_slot[k]),
-                                b.stride(p.out_slot[k]) * sizeof(float), p.out_n[k] * sizeof(float), L,
-                                hipMemcpyDeviceToHost, stream),
+                                b.stride(p.out_slot[k]) * sizeof(float), p.out_n[k] * sizeof(float),
+                                b.lanes.size(), hipMemcpyDeviceToHost, stream),
                "copying the results");
+    }
   }
   HIPTRY(hipStreamSynchronize(stream), "running the plan");
   return true;
@@ -1037,14 +1107,10 @@ int ppocr_gpu_run_resident(ppocr_gpu_model *model, int repeats, float *ms, char 
     hipEventRecord(t0, m.stream);
   }
   for (int r = 0; r < repeats; r++) {
-    for (size_t g = 0; g < m.active_batches; g++) {
-      for (const ppocr::Launch &l : m.batches[g]->launches) {
-        hipError_t e = l.fn(m.stream);
-        if (e != hipSuccess) {
-          if (t0) hipEventDestroy(t0), hipEventDestroy(t1);
-          return put_err(ppocr::fmt("launching %s (operation %d): %s", l.name.c_str(), l.op, hipGetErrorString(e)), err, err_len), 1;
-        }
-      }
+    std::string e;
+    if (!m.enqueue(e)) {
+      if (t0) hipEventDestroy(t0), hipEventDestroy(t1);
+      return put_err(e, err, err_len), 1;
     }
   }
   hipError_t e = hipSuccess;
@@ -1061,6 +1127,13 @@ int ppocr_gpu_run_resident(ppocr_gpu_model *model, int repeats, float *ms, char 
 }
 
 void *ppocr_gpu_stream(ppocr_gpu_model *model) { return model ? (void *)model->m.stream : nullptr; }
+
+int ppocr_gpu_set_graphs(ppocr_gpu_model *model, int enable) {
+  if (!model) return 1;
+  model->m.drop_graph();
+  model->m.use_graphs = enable != 0;
+  return 0;
+}
 
 size_t ppocr_gpu_launch_count(const ppocr_gpu_model *model) {
   if (!model) return 0;

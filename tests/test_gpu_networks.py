@@ -92,6 +92,40 @@ def test_same_width_lane_alone_matches_batch():
         assert np.array_equal(alone.view(np.uint32), batch[i].view(np.uint32))
 
 
+def test_graph_replays_match_eager_run(oracle):
+    # The first run launches eagerly; later runs replay the captured graph.
+    # Every replay, with host work and synchronisation between them, must
+    # give the eager run's bits; a resize records the graph again.
+    plan = nets.recognizer_plan(init="scaled", vocab=6625)
+    lines = nets.line_images(4, seed=31)
+    g = GpuModel.load(plan)
+    g.set_sizes([(48, 320)] * 4)
+    for i in range(4):
+        g.lane_input_mut(i)[:] = lines[i].reshape(-1)
+    g.run()
+    eager = [g.lane_output(i) for i in range(4)]
+    m = oracle.OracleModel(plan)
+    for i in range(4):
+        check_rec(eager[i], m.run(lines[i])[0])
+    for _ in range(4):
+        g.lane_input_mut(0)[:] = lines[0].reshape(-1)  # host work between replays
+        g.run()
+        for i in range(4):
+            assert np.array_equal(g.lane_output(i).view(np.uint32), eager[i].view(np.uint32))
+    g.set_sizes([(48, 160)] * 2)
+    for i in range(2):
+        g.lane_input_mut(i)[:] = lines[i][:, :160].reshape(-1)
+    outs = []
+    for _ in range(3):
+        g.run()
+        outs.append([g.lane_output(i) for i in range(2)])
+    m.set_size(48, 160)
+    for i in range(2):
+        check_rec(outs[0][i], m.run(np.ascontiguousarray(lines[i][:, :160]))[0])
+        assert np.array_equal(outs[1][i], outs[0][i]) and np.array_equal(outs[2][i], outs[0][i])
+    g.close()
+
+
 def test_resize_between_runs(oracle):
     # set_sizes up, down and back on one model (src/engine/mod.rs:1496-1507).
     plan = nets.detector_plan(h=64, w=64, init="scaled")
