@@ -77,8 +77,34 @@ __device__ __forceinline__ ConvSrc pick_src(const ConvArgs &a, int c) {
   return s;
 }
 
-template <int WM, int BN, int BK, bool VEC, bool PW, bool CTC>
+// Workgroup i of a launch runs on XCD i % 8 (the dispatcher deals them round
+// robin) and each XCD has its own L2. Renumber so that each XCD takes one
+// contiguous run of tiles: neighbouring row tiles, which share input rows of
+// a window (and, with several column tiles, the same A rows), then meet in
+// the same L2 instead of each XCD fetching them from HBM. A bijection on
+// [0, groups): the first groups % 8 XCDs take one tile more.
+__device__ __forceinline__ int xcd_tile(int i, int groups) {
+  const int per = (groups + 7) >> 3;
+  const int tall = (groups & 7) ? (groups & 7) : 8;
+  const int xcd = i & 7, local = i >> 3;
+  return xcd < tall ? xcd * per + local : tall * per + (xcd - tall) * (per - 1) + local;
+}
+
+// How a tile's A operand (the input patch of each row) is read.
+//  L_FLAT: any channel count, one float at a time over taps * channels.
+//  L_SOURCES: up to four sources (upsampled by 2^shift), four channels at a
+//    time; the source of each channel is looked up per chunk.
+//  L_WINDOW: one source at full resolution, kh, kw <= 8: each staged element
+//    keeps a base pointer at its window's corner and a mask of the window rows
+//    and columns inside the image; a chunk adds a uniform offset.
+//  L_POINTWISE: 1x1 over one source (also the transposed conv's and the CTC
+//    head's input): base pointer plus a uniform channel offset.
+enum { L_FLAT = 0, L_SOURCES = 1, L_WINDOW = 2, L_POINTWISE = 3 };
+
+template <int WM, int BN, int BK, int LAY, bool CTC>
 __global__ __launch_bounds__(256) void conv_mfma(ConvArgs a) {
+  constexpr bool VEC = LAY != L_FLAT;
+  constexpr bool FAST = LAY == L_WINDOW || LAY == L_POINTWISE;
   constexpr int BM = 4 * WM;
   constexpr int S = BK + 4;
   constexpr int KS = BK / 4;
@@ -102,13 +128,17 @@ __global__ __launch_bounds__(256) void conv_mfma(ConvArgs a) {
   const int per_lane = a.oh * a.ow;
   const int M = a.lanes * per_lane;
   const int ntn = (a.n + BN - 1) / BN;
-  const int tn = blockIdx.x % ntn, tm = blockIdx.x / ntn;
+  const int tile = a.xcd_rows ? xcd_tile(blockIdx.x, gridDim.x) : blockIdx.x;
+  const int tn = tile % ntn, tm = tile / ntn;
   const int m0 = tm * BM, n0 = tn * BN;
   if (m0 >= M) return;
 
   // Rows this thread stages, decomposed once.
   int a_row[A_PER], a_kv[A_PER], a_lane[A_PER], a_y[A_PER], a_x[A_PER];
   bool a_ok[A_PER];
+  const float *a_base[FAST ? A_PER : 1];
+  const float *g_base[FAST ? A_PER : 1];
+  unsigned a_mask[LAY == L_WINDOW ? A_PER : 1];
 #pragma unroll
   for (int i = 0; i < A_PER; i++) {
     int e = tid + 256 * i;
@@ -119,13 +149,25 @@ __global__ __launch_bounds__(256) void conv_mfma(ConvArgs a) {
     int mm = a_ok[i] ? m : 0;
     a_lane[i] = mm / per_lane;
     int rem = mm - a_lane[i] * per_lane;
-    if (PW) {
+    if (LAY == L_POINTWISE) {
       a_y[i] = rem;
       a_x[i] = 0;
     } else {
       int oy = rem / a.ow, ox = rem - oy * a.ow;
       a_y[i] = oy * a.sh - a.pt;
       a_x[i] = ox * a.sw - a.pl;
+    }
+    if constexpr (FAST) {
+      const ConvSrc &src = a.src[0];
+      long pix = LAY == L_POINTWISE ? (long)a_y[i] : (long)a_y[i] * a.iw + a_x[i];
+      a_base[i] = src.p + (long)a_lane[i] * src.lane_stride + pix * src.c + a_kv[i] * 4;
+      g_base[i] = a.gate ? a.gate + (long)a_lane[i] * a.gate_lane_stride + a_kv[i] * 4 : nullptr;
+    }
+    if constexpr (LAY == L_WINDOW) {
+      unsigned ym = 0, xm = 0;
+      for (int k = 0; k < a.kh; k++) ym |= (unsigned)(a_y[i] + k >= 0 && a_y[i] + k < a.ih) << k;
+      for (int k = 0; k < a.kw; k++) xm |= (unsigned)(a_x[i] + k >= 0 && a_x[i] + k < a.iw) << k;
+      a_mask[i] = a_ok[i] ? ym | xm << 8 : 0u;
     }
   }
   const float *b_ptr[B_PER];
@@ -143,36 +185,54 @@ __global__ __launch_bounds__(256) void conv_mfma(ConvArgs a) {
   AT ra[A_PER];
   f32x4 rb[B_PER];
 
-  auto load = [&](int q) {
-    int tap = 0, cbase = 0;
-    if (VEC) {
-      tap = q / a.cpt;
-      cbase = (q - tap * a.cpt) * BK;
+  // The chunk being loaded: tap (ky, kx), channel chunk cc of that tap.
+  int ky = 0, kx = 0, cc = 0;
+  auto advance = [&]() {
+    if (++cc == a.cpt) {
+      cc = 0;
+      if (++kx == a.kw) kx = 0, ++ky;
     }
+  };
+
+  auto load = [&](int q) {
+    if constexpr (FAST) {
+      const int cb = cc * BK;
+      const long off = LAY == L_WINDOW ? (long)(ky * a.iw + kx) * a.src[0].c + cb : (long)cb;
+      const int climit = a.ctot - cb;  // staged channel offsets below this are real
 #pragma unroll
-    for (int i = 0; i < A_PER; i++) {
-      int t = tap, c;
-      if (VEC) {
-        c = cbase + a_kv[i] * AV;
-      } else {
-        int k = q * BK + a_kv[i];
-        t = k / a.ctot;
-        c = k - t * a.ctot;
-      }
-      AT v;
-      if constexpr (AV == 4) v = f32x4{0.f, 0.f, 0.f, 0.f};
-      else v = 0.0f;
-      bool live = a_ok[i] && c < a.ctot && t < a.kh * a.kw;
-      if (PW) {
+      for (int i = 0; i < A_PER; i++) {
+        bool live = a_kv[i] * 4 < climit;
+        if (LAY == L_WINDOW) live = live && ((a_mask[i] >> ky) & (a_mask[i] >> (8 + kx)) & 1u);
+        else live = live && a_ok[i];
+        f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
         if (live) {
-          const ConvSrc &src = a.src[0];
-          v = *reinterpret_cast<const AT *>(src.p + (long)a_lane[i] * src.lane_stride +
-                                            (long)a_y[i] * src.c + c);
-          if (a.gate) v = v * *reinterpret_cast<const AT *>(a.gate + (long)a_lane[i] * a.gate_lane_stride + c);
+          v = *reinterpret_cast<const f32x4 *>(a_base[i] + off);
+          if (a.gate) v = v * *reinterpret_cast<const f32x4 *>(g_base[i] + cb);
         }
-      } else {
-        int ky = t / a.kw, kx = t - ky * a.kw;
-        int iy = a_y[i] + ky, ix = a_x[i] + kx;
+        ra[i] = v;
+      }
+    } else {
+      int tap = 0, cbase = 0;
+      if (VEC) {
+        tap = q / a.cpt;
+        cbase = (q - tap * a.cpt) * BK;
+      }
+#pragma unroll
+      for (int i = 0; i < A_PER; i++) {
+        int t = tap, c;
+        if (VEC) {
+          c = cbase + a_kv[i] * AV;
+        } else {
+          int k = q * BK + a_kv[i];
+          t = k / a.ctot;
+          c = k - t * a.ctot;
+        }
+        AT v;
+        if constexpr (AV == 4) v = f32x4{0.f, 0.f, 0.f, 0.f};
+        else v = 0.0f;
+        bool live = a_ok[i] && c < a.ctot && t < a.kh * a.kw;
+        int tky = t / a.kw, tkx = t - tky * a.kw;
+        int iy = a_y[i] + tky, ix = a_x[i] + tkx;
         live = live && iy >= 0 && iy < a.ih && ix >= 0 && ix < a.iw;
         if (live) {
           const ConvSrc src = pick_src(a, c);
@@ -182,8 +242,8 @@ __global__ __launch_bounds__(256) void conv_mfma(ConvArgs a) {
           if (a.gate && src.coff == 0)
             v = v * *reinterpret_cast<const AT *>(a.gate + (long)a_lane[i] * a.gate_lane_stride + cl);
         }
+        ra[i] = v;
       }
-      ra[i] = v;
     }
 #pragma unroll
     for (int i = 0; i < B_PER; i++) {
@@ -207,11 +267,15 @@ __global__ __launch_bounds__(256) void conv_mfma(ConvArgs a) {
 
   const int li = lane & 15, lg = lane >> 4;
   load(0);
+  advance();
   store(0);
   __syncthreads();
   for (int q = 0; q < a.chunks; q++) {
     const int cur = q & 1;
-    if (q + 1 < a.chunks) load(q + 1);
+    if (q + 1 < a.chunks) {
+      load(q + 1);
+      advance();
+    }
 #pragma unroll
     for (int r = 0; r < KR; r++) {
       KT av[MT], bv[NT];
@@ -333,30 +397,38 @@ __global__ __launch_bounds__(256) void ctc_merge(const float4 *part, int rows, i
   }
 }
 
-template <int WM, int BN, int BK, bool VEC, bool PW, bool CTC>
+template <int WM, int BN, int BK, int LAY, bool CTC>
 static hipError_t go(const ConvArgs &a, hipStream_t s) {
   long M = (long)a.lanes * a.oh * a.ow;
   long tiles = (M + 4 * WM - 1) / (4 * WM) * ((a.n + BN - 1) / BN);
   if (tiles <= 0 || tiles > 0x7fffffffL) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((conv_mfma<WM, BN, BK, VEC, PW, CTC>), dim3((unsigned)tiles), dim3(256), 0, s,
+  hipLaunchKernelGGL((conv_mfma<WM, BN, BK, LAY, CTC>), dim3((unsigned)tiles), dim3(256), 0, s,
                      a);
   return hipGetLastError();
 }
 
-#define PPOCR_TILES(BK, VEC, PW)                                              \
-  if (t.wm == 32 && t.bn == 64) return go<32, 64, BK, VEC, PW, false>(a, s); \
-  if (t.wm == 32 && t.bn == 32) return go<32, 32, BK, VEC, PW, false>(a, s); \
-  if (t.wm == 32 && t.bn == 16) return go<32, 16, BK, VEC, PW, false>(a, s); \
-  if (t.wm == 16 && t.bn == 64) return go<16, 64, BK, VEC, PW, false>(a, s);
+#define PPOCR_TILES(BK, LAY)                                               \
+  if (t.wm == 32 && t.bn == 64) return go<32, 64, BK, LAY, false>(a, s); \
+  if (t.wm == 32 && t.bn == 32) return go<32, 32, BK, LAY, false>(a, s); \
+  if (t.wm == 32 && t.bn == 16) return go<32, 16, BK, LAY, false>(a, s); \
+  if (t.wm == 16 && t.bn == 64) return go<16, 64, BK, LAY, false>(a, s); \
+  if (t.wm == 16 && t.bn == 32) return go<16, 32, BK, LAY, false>(a, s); \
+  if (t.wm == 16 && t.bn == 16) return go<16, 16, BK, LAY, false>(a, s);
 
-#define PPOCR_TILES_SMALL(BK, VEC, PW)                                        \
-  if (t.wm == 16 && t.bn == 64) return go<16, 64, BK, VEC, PW, false>(a, s); \
-  if (t.wm == 16 && t.bn == 32) return go<16, 32, BK, VEC, PW, false>(a, s); \
-  if (t.wm == 16 && t.bn == 16) return go<16, 16, BK, VEC, PW, false>(a, s);
+#define PPOCR_TILES_SMALL(BK, LAY)                                         \
+  if (t.wm == 16 && t.bn == 64) return go<16, 64, BK, LAY, false>(a, s); \
+  if (t.wm == 16 && t.bn == 32) return go<16, 32, BK, LAY, false>(a, s); \
+  if (t.wm == 16 && t.bn == 16) return go<16, 16, BK, LAY, false>(a, s);
+
+#define PPOCR_CHUNKS(LAY)                               \
+  if (t.bk == 64) { PPOCR_TILES_SMALL(64, LAY) }        \
+  if (t.bk == 32) { PPOCR_TILES(32, LAY) }              \
+  if (t.bk == 16) { PPOCR_TILES(16, LAY) }              \
+  if (t.bk == 8) { PPOCR_TILES(8, LAY) }
 
 bool gemm_tile_supported(const GemmTile &t) {
   if (t.bk == 64) return t.vec && t.wm == 16 && (t.bn == 16 || t.bn == 32 || t.bn == 64);
-  bool tile = (t.wm == 32 && (t.bn == 16 || t.bn == 32 || t.bn == 64)) || (t.wm == 16 && t.bn == 64);
+  bool tile = (t.wm == 32 || t.wm == 16) && (t.bn == 16 || t.bn == 32 || t.bn == 64);
   if (!tile) return false;
   if (t.vec) return t.bk == 8 || t.bk == 16 || t.bk == 32;
   return !t.pointwise && (t.bk == 8 || t.bk == 16 || t.bk == 32);
@@ -365,25 +437,22 @@ bool gemm_tile_supported(const GemmTile &t) {
 hipError_t launch_conv(const ConvArgs &a, const GemmTile &t, hipStream_t s) {
   if (a.mode == GEMM_CTC) {
     if (!t.pointwise || !t.vec || t.bn != 64) return hipErrorInvalidValue;
-    if (t.wm == 32 && t.bk == 8) return go<32, 64, 8, true, true, true>(a, s);
-    if (t.wm == 32 && t.bk == 16) return go<32, 64, 16, true, true, true>(a, s);
+    if (t.wm == 32 && t.bk == 8) return go<32, 64, 8, L_POINTWISE, true>(a, s);
+    if (t.wm == 32 && t.bk == 16) return go<32, 64, 16, L_POINTWISE, true>(a, s);
     return hipErrorInvalidValue;
   }
   if (!gemm_tile_supported(t)) return hipErrorInvalidValue;
-  if (t.vec && t.pointwise) {
-    if (t.bk == 64) { PPOCR_TILES_SMALL(64, true, true) }
-    if (t.bk == 32) { PPOCR_TILES(32, true, true) }
-    if (t.bk == 16) { PPOCR_TILES(16, true, true) }
-    if (t.bk == 8) { PPOCR_TILES(8, true, true) }
-  } else if (t.vec) {
-    if (t.bk == 64) { PPOCR_TILES_SMALL(64, true, false) }
-    if (t.bk == 32) { PPOCR_TILES(32, true, false) }
-    if (t.bk == 16) { PPOCR_TILES(16, true, false) }
-    if (t.bk == 8) { PPOCR_TILES(8, true, false) }
+  if (!t.vec) {
+    if (t.bk == 32) { PPOCR_TILES(32, L_FLAT) }
+    if (t.bk == 16) { PPOCR_TILES(16, L_FLAT) }
+    if (t.bk == 8) { PPOCR_TILES(8, L_FLAT) }
+  } else if (t.pointwise) {
+    if (a.nsrc != 1 || a.src[0].shift != 0 || a.ctot != a.src[0].c) return hipErrorInvalidValue;
+    PPOCR_CHUNKS(L_POINTWISE)
+  } else if (a.nsrc == 1 && a.src[0].shift == 0 && a.kh <= 8 && a.kw <= 8) {
+    PPOCR_CHUNKS(L_WINDOW)
   } else {
-    if (t.bk == 32) { PPOCR_TILES(32, false, false) }
-    if (t.bk == 16) { PPOCR_TILES(16, false, false) }
-    if (t.bk == 8) { PPOCR_TILES(8, false, false) }
+    PPOCR_CHUNKS(L_SOURCES)
   }
   return hipErrorInvalidValue;
 }

@@ -50,6 +50,7 @@ struct ConvArgs {
   int spread_kw, spread_oc;  // GEMM_SPREAD: non-overlapping transposed conv
   float *part;          // GEMM_CTC: per row and column tile (max, sum, best)
   int vocab;
+  int xcd_rows;         // 1: give each XCD a contiguous run of tiles (see xcd_tile)
 };
 
 struct GemmTile {

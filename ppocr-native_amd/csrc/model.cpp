@@ -634,7 +634,8 @@ void Model::build_launches(Batch &b) {
         long M = long(L) * a.oh * a.ow;
         long tiles = (M + 127) / 128 * ((a.n + t.bn - 1) / t.bn);
         // Fewer than four tiles per CU of 128 rows: take 64-row tiles.
-        if (t.bn == 64 && tiles < 1024) t.wm = 16;
+        if (tiles < 1024) t.wm = 16;
+        a.xcd_rows = 1;
         const char *nm = op.kind == K_CONVTRANSPOSE ? "convt_gemm" : (t.pointwise ? "pointwise_gemm" : "conv_gemm");
         b.launches.push_back({nm, s.op, [a, t](hipStream_t st) { return launch_conv(a, t, st); }});
         break;
