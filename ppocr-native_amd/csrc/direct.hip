@@ -1,0 +1,230 @@
+// Layers computed directly on the vector ALUs, each output in the CPU
+// engine's own summation order, so the results are bit-identical to it:
+//  - conv_direct: a windowed convolution over few input channels (the RGB
+//    stem), where an implicit GEMM would spend its time on index arithmetic;
+//  - db_head: the detector head's two 2x2 stride-2 transposed convolutions,
+//    the second narrow, in one pass, so the wide intermediate map never
+//    reaches memory.
+#include "act.hpp"
+#include "kernels.hpp"
+
+namespace ppocr {
+
+// Thread = one output pixel of one lane; block row blockIdx.y = a group of
+// eight output channels, whose weights the block stages in LDS first (every
+// thread of the block reads the same ones). Order per output
+// (src/engine/kernels/dense.rs:38-147, conv.rs:146-236): the bias first
+// (always for the RGB stem; otherwise for a multiple-of-16 width except the
+// row's last ow % 4 pixels), taps [ky][kx], channels in order, a fused
+// multiply-add for columns below oc / 8 * 8 and a separate multiply and add
+// above; a bias not taken first is added last.
+constexpr int kDirectTaps = 64;  // kh * kw * ic at most
+
+// KH, KW, IC > 0: the window and channel count fixed at compile time, so the
+// thread issues all of its patch's loads before the first multiply (the
+// loads of a runtime loop would each wait for the previous sum). 0: any.
+template <int KH, int KW, int IC>
+__global__ __launch_bounds__(256) void conv_direct_kernel(DirectArgs a) {
+  __shared__ __attribute__((aligned(16))) float ws[kDirectTaps * 8];
+  constexpr bool FIXED = KH > 0;
+  const int kh = FIXED ? KH : a.kh, kw = FIXED ? KW : a.kw, ic = FIXED ? IC : a.ic;
+  const int j0 = blockIdx.y * 8;
+  const int K = kh * kw * ic;
+  for (int e = threadIdx.x; e < K * 8; e += 256) {
+    const int r = e >> 3, k = e & 7;
+    ws[e] = j0 + k < a.oc ? a.w[(long)r * a.oc + j0 + k] : 0.0f;
+  }
+  __syncthreads();
+  const int per = a.oh * a.ow;
+  const int g = blockIdx.x * 256 + threadIdx.x;
+  if (g >= a.lanes * per) return;
+  const int ln = g / per;
+  const int rem = g - ln * per;
+  const int oy = rem / a.ow, ox = rem - oy * a.ow;
+  const float *x = a.x + (long)ln * a.x_lane_stride;
+  const bool first = ox < a.first_end;
+  float acc[8];
+#pragma unroll
+  for (int k = 0; k < 8; k++) acc[k] = (a.bias && first && j0 + k < a.oc) ? a.bias[j0 + k] : 0.0f;
+  auto tap_sum = [&](const float *tap, float v, int i) {
+    const float4 w0 = *reinterpret_cast<const float4 *>(tap + i * 8);
+    const float4 w1 = *reinterpret_cast<const float4 *>(tap + i * 8 + 4);
+    const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+    for (int k = 0; k < 8; k++) acc[k] = j0 + k < a.fused ? fmaf(wv[k], v, acc[k]) : acc[k] + v * wv[k];
+  };
+  if constexpr (FIXED) {
+    // Gather the patch (zeros where the window leaves the image, which are
+    // then skipped, as the engine skips them), then sum in tap order.
+    float patch[KH * KW * IC];
+    bool in[KH * KW];
+#pragma unroll
+    for (int ky = 0; ky < KH; ky++) {
+#pragma unroll
+      for (int kx = 0; kx < KW; kx++) {
+        const int iy = oy * a.sh + ky - a.pt, ix = ox * a.sw + kx - a.pl;
+        const bool ok = iy >= 0 && iy < a.ih && ix >= 0 && ix < a.iw;
+        in[ky * KW + kx] = ok;
+        const float *px = x + ((long)iy * a.iw + ix) * IC;
+#pragma unroll
+        for (int i = 0; i < IC; i++) patch[(ky * KW + kx) * IC + i] = ok ? px[i] : 0.0f;
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < KH * KW; t++) {
+      if (!in[t]) continue;
+#pragma unroll
+      for (int i = 0; i < IC; i++) tap_sum(ws + t * IC * 8, patch[t * IC + i], i);
+    }
+  } else {
+    for (int ky = 0; ky < kh; ky++) {
+      const int iy = oy * a.sh + ky - a.pt;
+      if (iy < 0 || iy >= a.ih) continue;
+      for (int kx = 0; kx < kw; kx++) {
+        const int ix = ox * a.sw + kx - a.pl;
+        if (ix < 0 || ix >= a.iw) continue;
+        const float *px = x + ((long)iy * a.iw + ix) * ic;
+        for (int i = 0; i < ic; i++) tap_sum(ws + (ky * kw + kx) * ic * 8, px[i], i);
+      }
+    }
+  }
+  float *y = a.y + (long)ln * a.y_lane_stride + (long)rem * a.oc + j0;
+#pragma unroll
+  for (int k = 0; k < 8; k++) {
+    if (j0 + k >= a.oc) break;
+    float v = acc[k];
+    if (a.bias && !first) v = v + a.bias[j0 + k];
+    y[k] = act(v, a.act);
+  }
+}
+
+bool direct_supported(int kh, int kw, int ic) { return kh * kw * ic <= kDirectTaps; }
+
+hipError_t launch_conv_direct(const DirectArgs &a, hipStream_t s) {
+  const long n = (long)a.lanes * a.oh * a.ow;
+  if (n <= 0 || a.oc <= 0) return hipSuccess;
+  if (!direct_supported(a.kh, a.kw, a.ic) || n > 0x7fffff00L || (a.oc + 7) / 8 > 65535)
+    return hipErrorInvalidValue;
+  dim3 grid((unsigned)((n + 255) / 256), (a.oc + 7) / 8), block(256);
+  if (a.kh == 3 && a.kw == 3 && a.ic == 3)
+    hipLaunchKernelGGL((conv_direct_kernel<3, 3, 3>), grid, block, 0, s, a);
+  else if (a.kh == 2 && a.kw == 2 && a.ic == 3)
+    hipLaunchKernelGGL((conv_direct_kernel<2, 2, 3>), grid, block, 0, s, a);
+  else if (a.kh == 3 && a.kw == 3 && a.ic == 1)
+    hipLaunchKernelGGL((conv_direct_kernel<3, 3, 1>), grid, block, 0, s, a);
+  else
+    hipLaunchKernelGGL((conv_direct_kernel<0, 0, 0>), grid, block, 0, s, a);
+  return hipGetLastError();
+}
+
+// Thread = one input pixel (iy, ix) of the first transposed convolution and
+// one of its two output rows ky (blockIdx.y, so the weights a wave reads are
+// uniform). It forms the 2 x OC1 values of intermediate pixels
+// (2iy+ky, 2ix+kx), kx = 0, 1, as the engine's pointwise call over one input
+// row does (src/engine/layers.rs:600-680): the bias first for a
+// multiple-of-16 column count except the row's last iw % 4 pixels, else
+// last; fused multiply-adds below cols / 8 * 8. After the first activation,
+// each intermediate pixel gives its 2 x 2 outputs of the second convolution
+// (four columns: bias last, separate multiply and add), then the second
+// activation; the thread writes 2 rows x 4 columns of the final map.
+constexpr int kHeadMaxIc = 128;
+
+template <int OC1>
+__global__ __launch_bounds__(256) void db_head_kernel(HeadArgs a) {
+  constexpr int COLS1 = 4 * OC1;
+  constexpr int FUSED1 = COLS1 / 8 * 8;
+  constexpr int T = 2 * OC1;  // the thread's first-layer columns
+  __shared__ __attribute__((aligned(16))) float w1s[kHeadMaxIc * T];
+  __shared__ __attribute__((aligned(16))) float w2s[OC1 * 4];
+  const int ky = blockIdx.y;
+  const int n0 = ky * T;  // columns of taps (ky, 0) and (ky, 1)
+  for (int e = threadIdx.x; e < a.ic * T; e += 256) w1s[e] = a.w1[(long)(e / T) * COLS1 + n0 + e % T];
+  for (int e = threadIdx.x; e < OC1 * 4; e += 256) w2s[e] = a.w2[e];
+  __syncthreads();
+  const int per = a.ih * a.iw;
+  const int g = blockIdx.x * 256 + threadIdx.x;
+  if (g >= a.lanes * per) return;
+  const int ln = g / per;
+  const int pix = g - ln * per;
+  const int iy = pix / a.iw, ix = pix - iy * a.iw;
+  const bool first = COLS1 % 16 == 0 && ix < a.iw / 4 * 4;
+  const float *xp = a.x + (long)ln * a.x_lane_stride + (long)pix * a.ic;
+  float t[T];
+#pragma unroll
+  for (int n = 0; n < T; n++) t[n] = (a.b1 && first) ? a.b1[n0 + n] : 0.0f;
+  // Channels in runs of eight: the next run's loads are issued before this
+  // run's sums, so a thread waits for memory once per run, not per channel.
+  float4 cur0 = *reinterpret_cast<const float4 *>(xp), cur1 = *reinterpret_cast<const float4 *>(xp + 4);
+  for (int i0 = 0; i0 < a.ic; i0 += 8) {
+    float4 nx0 = cur0, nx1 = cur1;
+    if (i0 + 8 < a.ic) {
+      nx0 = *reinterpret_cast<const float4 *>(xp + i0 + 8);
+      nx1 = *reinterpret_cast<const float4 *>(xp + i0 + 12);
+    }
+    const float xv[8] = {cur0.x, cur0.y, cur0.z, cur0.w, cur1.x, cur1.y, cur1.z, cur1.w};
+#pragma unroll
+    for (int ii = 0; ii < 8; ii++) {
+      const float v = xv[ii];
+      const float *wr = w1s + (i0 + ii) * T;
+#pragma unroll
+      for (int n = 0; n < T; n += 4) {
+        const float4 w = *reinterpret_cast<const float4 *>(wr + n);
+        const float wv[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+          t[n + k] = n0 + n + k < FUSED1 ? fmaf(wv[k], v, t[n + k]) : t[n + k] + v * wv[k];
+      }
+    }
+    cur0 = nx0, cur1 = nx1;
+  }
+#pragma unroll
+  for (int n = 0; n < T; n++) {
+    float v = t[n];
+    if (a.b1 && !first) v = v + a.b1[n0 + n];
+    t[n] = act(v, a.act1);
+  }
+  // Second convolution, oc 1: four columns per intermediate pixel, tap
+  // (ky2, kx2) = column ky2 * 2 + kx2.
+  float out[2][4];
+#pragma unroll
+  for (int kx = 0; kx < 2; kx++) {
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int o = 0; o < OC1; o++) acc = acc + t[kx * OC1 + o] * w2s[o * 4 + c];
+      if (a.b2) acc = acc + a.b2[c];
+      out[c >> 1][kx * 2 + (c & 1)] = act(acc, a.act2);
+    }
+  }
+  const long ow = 4L * a.iw;
+  const long row = 4L * iy + 2L * ky;
+  float *y = a.y + (long)ln * a.y_lane_stride + row * ow + 4L * ix;
+#pragma unroll
+  for (int r = 0; r < 2; r++)
+    *reinterpret_cast<float4 *>(y + r * ow) = make_float4(out[r][0], out[r][1], out[r][2], out[r][3]);
+}
+
+bool head_supported(int ic, int oc1) {
+  return ic > 0 && ic % 8 == 0 && ic <= kHeadMaxIc && (oc1 == 8 || oc1 == 16 || oc1 == 24 || oc1 == 32);
+}
+
+hipError_t launch_db_head(const HeadArgs &a, hipStream_t s) {
+  const long n = (long)a.lanes * a.ih * a.iw;
+  if (n <= 0) return hipSuccess;
+  // The float4 loads and stores need 16-byte aligned pixels.
+  if (!head_supported(a.ic, a.oc1) || (reinterpret_cast<uintptr_t>(a.y) & 15) || (a.y_lane_stride & 3) ||
+      (reinterpret_cast<uintptr_t>(a.x) & 15) || (a.x_lane_stride & 3) || n > 0x7fffff00L)
+    return hipErrorInvalidValue;
+  dim3 grid((unsigned)((n + 255) / 256), 2), block(256);
+  switch (a.oc1) {
+    case 8: hipLaunchKernelGGL(db_head_kernel<8>, grid, block, 0, s, a); break;
+    case 16: hipLaunchKernelGGL(db_head_kernel<16>, grid, block, 0, s, a); break;
+    case 24: hipLaunchKernelGGL(db_head_kernel<24>, grid, block, 0, s, a); break;
+    case 32: hipLaunchKernelGGL(db_head_kernel<32>, grid, block, 0, s, a); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace ppocr

@@ -156,4 +156,34 @@ struct ConvtArgs {
 };
 hipError_t launch_convt_small(const ConvtArgs &a, hipStream_t s);
 
+// ------------------------------------------------------- direct (VALU) layers
+
+// A windowed convolution over one source, in the CPU engine's order: bias
+// first for outputs ox < first_end, fused multiply-adds for channels below
+// `fused`.
+struct DirectArgs {
+  int lanes, ih, iw, ic, oh, ow, oc, kh, kw, sh, sw, pt, pl;
+  const float *x; long x_lane_stride;
+  const float *w;     // [kh][kw][ic][oc]
+  const float *bias;  // oc or null
+  int act, first_end, fused;
+  float *y; long y_lane_stride;
+};
+bool direct_supported(int kh, int kw, int ic);
+hipError_t launch_conv_direct(const DirectArgs &a, hipStream_t s);
+
+// Two 2x2 stride-2 transposed convolutions in a row: ic -> oc1 (act1), then
+// oc1 -> 1 (act2); y is the final map, (4 ih) x (4 iw).
+struct HeadArgs {
+  int lanes, ih, iw, ic, oc1;
+  const float *x; long x_lane_stride;
+  const float *w1, *b1;  // [ic][2][2][oc1], 4 * oc1 or null
+  int act1;
+  const float *w2, *b2;  // [oc1][2][2][1], 4 or null
+  int act2;
+  float *y; long y_lane_stride;
+};
+bool head_supported(int ic, int oc1);
+hipError_t launch_db_head(const HeadArgs &a, hipStream_t s);
+
 }  // namespace ppocr

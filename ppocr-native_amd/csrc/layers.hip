@@ -307,17 +307,21 @@ hipError_t launch_eltwise(const EltArgs &a, hipStream_t s) {
 // tap, each later tap kept only when greater (src/engine/conv.rs:404-440).
 // Average: whole windows, taps summed from zero in row-major order, then
 // divided (src/engine/layers.rs:443-463).
+template <int V>
 __global__ __launch_bounds__(256) void pool_kernel(PoolArgs a) {
-  long per = (long)a.oh * a.ow * a.c;
+  const int cv = a.c / V;
+  long per = (long)a.oh * a.ow * cv;
   long g = (long)blockIdx.x * blockDim.x + threadIdx.x;
   if (g >= (long)a.lanes * per) return;
   int ln = (int)(g / per);
   long off = g - (long)ln * per;
-  int ch = (int)(off % a.c);
-  long pix = off / a.c;
+  int ch = (int)(off % cv) * V;
+  long pix = off / cv;
   int oy = (int)(pix / a.ow), ox = (int)(pix - (long)oy * a.ow);
   const float *x = a.x + (long)ln * a.x_lane_stride;
-  float accv = 0.0f;
+  float accv[V];
+#pragma unroll
+  for (int k = 0; k < V; k++) accv[k] = 0.0f;
   bool seeded = false;
   for (int ky = 0; ky < a.kh; ky++) {
     int iy = oy * a.sh + ky;
@@ -325,22 +329,34 @@ __global__ __launch_bounds__(256) void pool_kernel(PoolArgs a) {
     for (int kx = 0; kx < a.kw; kx++) {
       int ix = ox * a.sw + kx;
       if (ix >= a.iw) continue;
-      float v = x[((long)iy * a.iw + ix) * a.c + ch];
-      if (a.avg) {
-        accv = accv + v;
-      } else if (!seeded || v > accv) {
-        accv = v;
+      float v[V];
+      vload<V>(v, x + ((long)iy * a.iw + ix) * a.c + ch);
+#pragma unroll
+      for (int k = 0; k < V; k++) {
+        if (a.avg) {
+          accv[k] = accv[k] + v[k];
+        } else if (!seeded || v[k] > accv[k]) {
+          accv[k] = v[k];
+        }
       }
       seeded = true;
     }
   }
-  if (a.avg) accv = accv / (float)(a.kh * a.kw);
-  a.y[(long)ln * a.y_lane_stride + off] = accv;
+  if (a.avg) {
+#pragma unroll
+    for (int k = 0; k < V; k++) accv[k] = accv[k] / (float)(a.kh * a.kw);
+  }
+  vstore<V>(a.y + (long)ln * a.y_lane_stride + pix * a.c + ch, accv);
 }
 
 hipError_t launch_pool(const PoolArgs &a, hipStream_t s) {
-  long n = (long)a.lanes * a.oh * a.ow * a.c;
-  hipLaunchKernelGGL(pool_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, s, a);
+  const bool v4 = a.c % 4 == 0 && a.x_lane_stride % 4 == 0 && a.y_lane_stride % 4 == 0 &&
+                  (reinterpret_cast<uintptr_t>(a.x) & 15) == 0 && (reinterpret_cast<uintptr_t>(a.y) & 15) == 0;
+  long n = (long)a.lanes * a.oh * a.ow * (v4 ? a.c / 4 : a.c);
+  if (v4)
+    hipLaunchKernelGGL(pool_kernel<4>, dim3(blocks_for(n, 256)), dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL(pool_kernel<1>, dim3(blocks_for(n, 256)), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 
@@ -363,7 +379,16 @@ __global__ __launch_bounds__(256) void mean_partial(const float *x, long x_lane_
     int ch = t % cw, r = t / cw;
     double s = 0.0;
     if (r < rows) {
-      for (int p = p0 + r; p < p1; p += rows) s += (double)xl[(long)p * c + c0 + ch];
+      // Eight loads in flight, then their sums in pixel order.
+      int p = p0 + r;
+      for (; p + 7 * rows < p1; p += 8 * rows) {
+        float v[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) v[k] = xl[(long)(p + k * rows) * c + c0 + ch];
+#pragma unroll
+        for (int k = 0; k < 8; k++) s += (double)v[k];
+      }
+      for (; p < p1; p += rows) s += (double)xl[(long)p * c + c0 + ch];
     }
     sums[t] = s;
     __syncthreads();
@@ -374,6 +399,27 @@ __global__ __launch_bounds__(256) void mean_partial(const float *x, long x_lane_
     }
     __syncthreads();
   }
+}
+
+// One output column of a 1x1 layer over one pixel: from zero, inputs in
+// order, fused multiply-adds or separate products and sums. Weights are
+// fetched eight at a time ahead of their sums.
+__device__ __forceinline__ float se_column(const float *w, int stride, const float *in, int n,
+                                           bool fused) {
+  float acc = 0.0f;
+  int i = 0;
+  for (; i + 8 <= n; i += 8) {
+    float wv[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) wv[k] = w[(long)(i + k) * stride];
+#pragma unroll
+    for (int k = 0; k < 8; k++) acc = fused ? fmaf(wv[k], in[i + k], acc) : acc + in[i + k] * wv[k];
+  }
+  for (; i < n; i++) {
+    float wv = w[(long)i * stride];
+    acc = fused ? fmaf(wv, in[i], acc) : acc + in[i] * wv;
+  }
+  return acc;
 }
 
 // Pass 2: one block per lane joins the partials and divides; with an SE,
@@ -424,23 +470,13 @@ __global__ __launch_bounds__(1024) void mean_finish(const double *partial, int p
   // Columns below co / 8 * 8 fuse their multiply-adds; the tail columns
   // multiply and add separately (the engine's pointwise rule for one pixel).
   for (int j = threadIdx.x; j < se.mid; j += blockDim.x) {
-    float acc = 0.0f;
-    const float *w = se.w1 + j;
-    if (j < se.mid / 8 * 8)
-      for (int i = 0; i < c; i++) acc = fmaf(w[(long)i * se.mid], mean[i], acc);
-    else
-      for (int i = 0; i < c; i++) acc = acc + mean[i] * w[(long)i * se.mid];
+    float acc = se_column(se.w1 + j, se.mid, mean, c, j < se.mid / 8 * 8);
     if (se.b1) acc = acc + se.b1[j];
     hid[j] = act(acc, se.act1);
   }
   __syncthreads();
   for (int j = threadIdx.x; j < se.cout; j += blockDim.x) {
-    float acc = 0.0f;
-    const float *w = se.w2 + j;
-    if (j < se.cout / 8 * 8)
-      for (int i = 0; i < se.mid; i++) acc = fmaf(w[(long)i * se.cout], hid[i], acc);
-    else
-      for (int i = 0; i < se.mid; i++) acc = acc + hid[i] * w[(long)i * se.cout];
+    float acc = se_column(se.w2 + j, se.cout, hid, se.mid, j < se.cout / 8 * 8);
     if (se.b2) acc = acc + se.b2[j];
     yl[j] = act(acc, se.act2);
   }

@@ -63,7 +63,7 @@ void put_err(const std::string &m, char *err, size_t len) {
 
 size_t round_up(size_t v, size_t m) { return (v + m - 1) / m * m; }
 
-enum StepKind { S_GEMM, S_DW, S_ELT, S_POOL, S_MEAN, S_LN, S_ATTN, S_CTC, S_CONVT };
+enum StepKind { S_GEMM, S_DW, S_ELT, S_POOL, S_MEAN, S_LN, S_ATTN, S_CTC, S_CONVT, S_DIRECT, S_HEAD };
 
 struct Source {
   size_t slot;
@@ -77,6 +77,7 @@ struct Step {
   int add = -1;      // Add folded into a convolution's output / of a residual gate
   int resgate = -1;  // Channelmul of a residual gate, x + x * g
   int fc1 = -1, fc2 = -1;  // squeeze-and-excite 1x1 layers after a Mean
+  int head2 = -1;          // the narrow transposed convolution folded into S_HEAD
   int elt = 0;             // EltMode
   std::vector<Source> sources;
   // Implicit-GEMM steps
@@ -201,6 +202,7 @@ std::vector<size_t> Model::step_reads(const Step &s) const {
 }
 
 size_t Model::step_writes(const Step &s) const {
+  if (s.kind == S_HEAD) return plan.ops[s.head2].y;
   if (s.kind == S_MEAN && s.fc2 >= 0) return plan.ops[s.fc2].y;
   if (s.kind == S_ELT && s.elt == ELT_UPSAMPLEADD_RESGATE) return plan.ops[s.op].y;
   if (s.add >= 0) return plan.ops[s.add].y;
@@ -338,6 +340,11 @@ bool Model::build_steps(std::string &err) {
           s.add = int(i + 1);
           folded[i + 1] = true;
         }
+        // A windowed convolution over a few channels that are not a multiple
+        // of four (the RGB stem): computed directly.
+        if (s.gate < 0 && s.add < 0 && op.n2 == 0 && s.sources.size() == 1 && s.sources[0].shift == 0 &&
+            !op.is_pointwise() && op.ic % 4 != 0 && direct_supported(int(op.kh), int(op.kw), int(op.ic)))
+          s.kind = S_DIRECT;
         break;
       }
       case K_DWCONV: s.kind = S_DW; break;
@@ -358,10 +365,24 @@ bool Model::build_steps(std::string &err) {
       case K_LAYERNORM: s.kind = S_LN; break;
       case K_ATTENTION: s.kind = S_ATTN; break;
       case K_CTCARGMAX: s.kind = S_CTC; break;
-      case K_CONVTRANSPOSE:
+      case K_CONVTRANSPOSE: {
         s.kind = op.kh * op.kw * op.oc <= 16 ? S_CONVT : S_GEMM;
+        // The DB head: a 2x2 stride-2 transposed convolution whose output only
+        // a second one to a single channel reads: one step, the intermediate
+        // map never stored.
+        auto two = [](const Op &o) { return o.kh == 2 && o.kw == 2 && o.sh == 2 && o.sw == 2; };
+        if (s.kind == S_GEMM && i + 1 < n && readers[op.y] == 1) {
+          const Op &o2 = ops[i + 1];
+          if (o2.kind == K_CONVTRANSPOSE && o2.x == op.y && two(op) && two(o2) && o2.oc == 1 &&
+              o2.ic == op.oc && head_supported(int(op.ic), int(op.oc))) {
+            s.kind = S_HEAD;
+            s.head2 = int(i + 1);
+            folded[i + 1] = true;
+          }
+        }
         if (s.kind == S_GEMM) s.sources.push_back({op.x, int(op.ic), 0});
         break;
+      }
       default:
         return err = fmt("operation %zu: %s is not supported on the GPU", i, kind_name(op.kind)), false;
     }
@@ -765,6 +786,37 @@ void Model::build_launches(Batch &b) {
         b.launches.push_back({"convt_small", s.op, [a](hipStream_t st) { return launch_convt_small(a, st); }});
         break;
       }
+      case S_DIRECT: {
+        DirectArgs a{};
+        a.lanes = L;
+        a.ih = int(op.ih), a.iw = int(op.iw), a.ic = int(op.ic);
+        a.oh = int(op.oh), a.ow = int(op.ow), a.oc = int(op.oc);
+        a.kh = int(op.kh), a.kw = int(op.kw), a.sh = int(op.sh), a.sw = int(op.sw);
+        a.pt = int(op.pt), a.pl = int(op.pl);
+        a.x = b.dev(op.x), a.x_lane_stride = b.stride(op.x);
+        a.w = W + op.w0, a.bias = bias, a.act = op.fused;
+        // kernels/dense.rs:38-147 and conv.rs:146-236: the RGB stem always
+        // starts from the bias; otherwise a multiple-of-16 width does, except
+        // for the row's last ow % 4 pixels.
+        const bool stem = op.ic == 3 && op.n2 == 0;
+        a.first_end = stem ? a.ow : (op.oc % 16 == 0 ? a.ow - a.ow % 4 : 0);
+        a.fused = int(op.oc / 8 * 8);
+        a.y = Y, a.y_lane_stride = ys;
+        b.launches.push_back({"conv_direct", s.op, [a](hipStream_t st) { return launch_conv_direct(a, st); }});
+        break;
+      }
+      case S_HEAD: {
+        const Op &o2 = p.ops[s.head2];
+        HeadArgs a{};
+        a.lanes = L;
+        a.ih = int(op.ih), a.iw = int(op.iw), a.ic = int(op.ic), a.oc1 = int(op.oc);
+        a.x = b.dev(op.x), a.x_lane_stride = b.stride(op.x);
+        a.w1 = W + op.w0, a.b1 = bias, a.act1 = op.fused;
+        a.w2 = W + o2.w0, a.b2 = o2.b1 ? W + o2.b0 : nullptr, a.act2 = o2.fused;
+        a.y = Y, a.y_lane_stride = ys;
+        b.launches.push_back({"db_head", s.op, [a](hipStream_t st) { return launch_db_head(a, st); }});
+        break;
+      }
     }
   }
 }
@@ -845,6 +897,17 @@ void Model::account(Batch &b) const {
         l.flops = 2.0 * L * in_px * op.ic * op.kh * op.kw * op.oc;
         l.bytes = F * (L * in_px * op.ic + L * out_px * op.oc + op.w1 + op.b1);
         break;
+      case S_DIRECT:
+        l.flops = 2.0 * L * out_px * op.oc * op.kh * op.kw * op.ic;
+        l.bytes = F * (L * in_px * op.ic + L * out_px * op.oc + op.w1 + op.b1);
+        break;
+      case S_HEAD: {
+        const Op &o2 = p.ops[s.head2];
+        const double mid_px = out_px, fin_px = double(o2.oh) * o2.ow;
+        l.flops = 2.0 * L * (in_px * op.ic * 4 * op.oc + mid_px * o2.ic * 4 * o2.oc);
+        l.bytes = F * (L * in_px * op.ic + L * fin_px * o2.oc + op.w1 + op.b1 + o2.w1 + o2.b1);
+        break;
+      }
     }
   }
 }

@@ -158,11 +158,44 @@ def test_elementwise_exact(oracle, mode):
     exact(got, want)
 
 
-def test_pools_exact(oracle):
+@pytest.mark.parametrize("c", [20, 6])
+def test_pools_exact(oracle, c):
+    # Four channels at a time when c % 4 == 0, else one.
     def build(b, t):
         return [b.maxpool(t), b.avgpool(t, (3, 1), (3, 1))]
 
-    got, want = both(build, (6, 11, 20), oracle)
+    got, want = both(build, (6, 11, c), oracle)
+    exact(got, want)
+
+
+@pytest.mark.parametrize("ci,co,k,s,pad,hw", [
+    (3, 24, 3, 2, 1, (19, 30)),   # RGB stem: every output from its bias
+    (3, 48, 3, 2, 1, (16, 22)),
+    (3, 24, 2, 2, 0, (12, 14)),
+    (6, 16, 3, 1, 1, (7, 14)),    # bias first except the row's last ow % 4 pixels
+    (5, 12, 3, 1, 1, (8, 13)),    # bias last; columns 8..11 multiply and add apart
+])
+def test_direct_conv_exact(oracle, ci, co, k, s, pad, hw):
+    w = RNG.normal(0, 0.3, (k, k, ci, co)).astype(np.float32)
+    bias = RNG.normal(0, 0.3, co).astype(np.float32)
+    got, want = both(lambda b, t: b.conv(t, w, bias, k=(k, k), s=(s, s), pad=(pad,) * 4,
+                                         fused="hardswish"), (*hw, ci), oracle)
+    exact(got, want)
+
+
+@pytest.mark.parametrize("oc1,hw", [(24, (9, 13)), (16, (6, 8))])
+def test_db_head_exact(oracle, oc1, hw):
+    # A wide 2x2 transposed conv read only by a narrow one: one fused step.
+    w1 = RNG.normal(0, 0.3, (24, 2, 2, oc1)).astype(np.float32)
+    b1 = RNG.normal(0, 0.3, oc1).astype(np.float32)
+    w2 = RNG.normal(0, 0.3, (oc1, 2, 2, 1)).astype(np.float32)
+    b2 = RNG.normal(0, 0.3, 1).astype(np.float32)
+
+    def build(b, t):
+        m = b.convtranspose(t, w1, b1, k=(2, 2), fused="relu")
+        return b.convtranspose(m, w2, b2, k=(2, 2), fused="sigmoid")
+
+    got, want = both(build, (*hw, 24), oracle)
     exact(got, want)
 
 
