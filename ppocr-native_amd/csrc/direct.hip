@@ -46,12 +46,20 @@ __global__ __launch_bounds__(256) void conv_direct_kernel(DirectArgs a) {
   float acc[8];
 #pragma unroll
   for (int k = 0; k < 8; k++) acc[k] = (a.bias && first && j0 + k < a.oc) ? a.bias[j0 + k] : 0.0f;
+  // Whether the group's eight columns all fuse is the same for the whole
+  // block: branch once rather than select per column.
+  const bool all_fused = j0 + 8 <= a.fused;
   auto tap_sum = [&](const float *tap, float v, int i) {
     const float4 w0 = *reinterpret_cast<const float4 *>(tap + i * 8);
     const float4 w1 = *reinterpret_cast<const float4 *>(tap + i * 8 + 4);
     const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+    if (all_fused) {
 #pragma unroll
-    for (int k = 0; k < 8; k++) acc[k] = j0 + k < a.fused ? fmaf(wv[k], v, acc[k]) : acc[k] + v * wv[k];
+      for (int k = 0; k < 8; k++) acc[k] = fmaf(wv[k], v, acc[k]);
+    } else {
+#pragma unroll
+      for (int k = 0; k < 8; k++) acc[k] = j0 + k < a.fused ? fmaf(wv[k], v, acc[k]) : acc[k] + v * wv[k];
+    }
   };
   if constexpr (FIXED) {
     // Gather the patch (zeros where the window leaves the image, which are
@@ -100,12 +108,104 @@ __global__ __launch_bounds__(256) void conv_direct_kernel(DirectArgs a) {
 
 bool direct_supported(int kh, int kw, int ic) { return kh * kw * ic <= kDirectTaps; }
 
+// The RGB stem, 3x3 over 3 channels to OC (a multiple of 8): every output
+// from its bias, every column fused (the stem rule, src/engine/conv.rs:
+// 146-236). Thread = one output pixel and all OC channels; the block's 256
+// pixels x OC outputs are one run of memory (within a lane), written back
+// from LDS as whole float4 rows instead of OC scattered floats per thread.
+template <int OC>
+__global__ __launch_bounds__(256) void conv_stem_kernel(DirectArgs a) {
+  constexpr int K = 27;
+  __shared__ __attribute__((aligned(16))) float ws[K * OC];
+  __shared__ __attribute__((aligned(16))) float out[256 * OC];
+  for (int e = threadIdx.x; e < K * OC; e += 256) ws[e] = a.w[e];
+  __syncthreads();
+  const int per = a.oh * a.ow, total = a.lanes * per;
+  const int g0 = blockIdx.x * 256, g = g0 + threadIdx.x;
+  if (g < total) {
+    const int ln = g / per, rem = g - ln * per;
+    const int oy = rem / a.ow, ox = rem - oy * a.ow;
+    const float *x = a.x + (long)ln * a.x_lane_stride;
+    float patch[K];
+    bool in[9];
+#pragma unroll
+    for (int ky = 0; ky < 3; ky++) {
+#pragma unroll
+      for (int kx = 0; kx < 3; kx++) {
+        const int iy = oy * a.sh + ky - a.pt, ix = ox * a.sw + kx - a.pl;
+        const bool ok = iy >= 0 && iy < a.ih && ix >= 0 && ix < a.iw;
+        in[ky * 3 + kx] = ok;
+        const float *px = x + ((long)iy * a.iw + ix) * 3;
+#pragma unroll
+        for (int i = 0; i < 3; i++) patch[(ky * 3 + kx) * 3 + i] = ok ? px[i] : 0.0f;
+      }
+    }
+    float acc[OC];
+#pragma unroll
+    for (int j = 0; j < OC; j++) acc[j] = a.bias ? a.bias[j] : 0.0f;
+#pragma unroll
+    for (int t = 0; t < 9; t++) {
+      if (!in[t]) continue;
+#pragma unroll
+      for (int i = 0; i < 3; i++) {
+        const float v = patch[t * 3 + i];
+        const float *wr = ws + (t * 3 + i) * OC;
+#pragma unroll
+        for (int j = 0; j < OC; j += 4) {
+          const float4 w = *reinterpret_cast<const float4 *>(wr + j);
+          acc[j] = fmaf(w.x, v, acc[j]);
+          acc[j + 1] = fmaf(w.y, v, acc[j + 1]);
+          acc[j + 2] = fmaf(w.z, v, acc[j + 2]);
+          acc[j + 3] = fmaf(w.w, v, acc[j + 3]);
+        }
+      }
+    }
+    float *o = out + threadIdx.x * OC;
+#pragma unroll
+    for (int j = 0; j < OC; j += 4)
+      *reinterpret_cast<float4 *>(o + j) =
+          make_float4(act(acc[j], a.act), act(acc[j + 1], a.act), act(acc[j + 2], a.act), act(acc[j + 3], a.act));
+  }
+  __syncthreads();
+  const int n = min(256, total - g0);
+  const int l0 = g0 / per, l1 = (g0 + n - 1) / per;
+  if (l0 == l1) {
+    float4 *dst = reinterpret_cast<float4 *>(a.y + (long)l0 * a.y_lane_stride + (long)(g0 - l0 * per) * OC);
+    const float4 *src = reinterpret_cast<const float4 *>(out);
+    for (int e = threadIdx.x; e < n * OC / 4; e += 256) dst[e] = src[e];
+  } else {
+    for (int e = threadIdx.x; e < n * OC; e += 256) {
+      const int p = g0 + e / OC, ln = p / per, rem = p - ln * per;
+      a.y[(long)ln * a.y_lane_stride + (long)rem * OC + e % OC] = out[e];
+    }
+  }
+}
+
 hipError_t launch_conv_direct(const DirectArgs &a, hipStream_t s) {
   const long n = (long)a.lanes * a.oh * a.ow;
   if (n <= 0 || a.oc <= 0) return hipSuccess;
   if (!direct_supported(a.kh, a.kw, a.ic) || n > 0x7fffff00L || (a.oc + 7) / 8 > 65535)
     return hipErrorInvalidValue;
-  dim3 grid((unsigned)((n + 255) / 256), (a.oc + 7) / 8), block(256);
+  const bool stem = a.kh == 3 && a.kw == 3 && a.ic == 3 && a.first_end >= a.ow && a.fused >= a.oc &&
+                    (reinterpret_cast<uintptr_t>(a.y) & 15) == 0 && a.y_lane_stride % 4 == 0;
+  const unsigned blocks = (unsigned)((n + 255) / 256);
+  if (stem && a.oc == 16) {
+    hipLaunchKernelGGL(conv_stem_kernel<16>, dim3(blocks), dim3(256), 0, s, a);
+    return hipGetLastError();
+  }
+  if (stem && a.oc == 24) {
+    hipLaunchKernelGGL(conv_stem_kernel<24>, dim3(blocks), dim3(256), 0, s, a);
+    return hipGetLastError();
+  }
+  if (stem && a.oc == 32) {
+    hipLaunchKernelGGL(conv_stem_kernel<32>, dim3(blocks), dim3(256), 0, s, a);
+    return hipGetLastError();
+  }
+  if (stem && a.oc == 48) {
+    hipLaunchKernelGGL(conv_stem_kernel<48>, dim3(blocks), dim3(256), 0, s, a);
+    return hipGetLastError();
+  }
+  dim3 grid(blocks, (a.oc + 7) / 8), block(256);
   if (a.kh == 3 && a.kw == 3 && a.ic == 3)
     hipLaunchKernelGGL((conv_direct_kernel<3, 3, 3>), grid, block, 0, s, a);
   else if (a.kh == 2 && a.kw == 2 && a.ic == 3)
@@ -132,7 +232,9 @@ constexpr int kHeadMaxIc = 128;
 template <int OC1>
 __global__ __launch_bounds__(256) void db_head_kernel(HeadArgs a) {
   constexpr int COLS1 = 4 * OC1;
-  constexpr int FUSED1 = COLS1 / 8 * 8;
+  // 4 * OC1 columns, a multiple of 8 for every supported OC1: all of them
+  // fuse their multiply-adds (columns below cols / 8 * 8 do).
+  static_assert(COLS1 % 8 == 0, "every first-layer column fuses");
   constexpr int T = 2 * OC1;  // the thread's first-layer columns
   __shared__ __attribute__((aligned(16))) float w1s[kHeadMaxIc * T];
   __shared__ __attribute__((aligned(16))) float w2s[OC1 * 4];
@@ -171,8 +273,7 @@ __global__ __launch_bounds__(256) void db_head_kernel(HeadArgs a) {
         const float4 w = *reinterpret_cast<const float4 *>(wr + n);
         const float wv[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
-        for (int k = 0; k < 4; k++)
-          t[n + k] = n0 + n + k < FUSED1 ? fmaf(wv[k], v, t[n + k]) : t[n + k] + v * wv[k];
+        for (int k = 0; k < 4; k++) t[n + k] = fmaf(wv[k], v, t[n + k]);
       }
     }
     cur0 = nx0, cur1 = nx1;

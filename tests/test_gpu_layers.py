@@ -170,6 +170,7 @@ def test_pools_exact(oracle, c):
 
 @pytest.mark.parametrize("ci,co,k,s,pad,hw", [
     (3, 24, 3, 2, 1, (19, 30)),   # RGB stem: every output from its bias
+    (3, 24, 3, 2, 1, (64, 70)),   # blocks of 256 pixels inside one lane and across two
     (3, 48, 3, 2, 1, (16, 22)),
     (3, 24, 2, 2, 0, (12, 14)),
     (6, 16, 3, 1, 1, (7, 14)),    # bias first except the row's last ow % 4 pixels
