@@ -79,8 +79,14 @@ struct DwArgs {
   int act;
   float *y;
   long y_lane_stride;
+  // When set: also the f64 sums of y per channel, one row of c per block,
+  // dw_mean_blocks(a) blocks per lane ([lane][block][c]), for the channel
+  // mean that reads y (joined by launch_mean_finish).
+  double *mean_part;
 };
 hipError_t launch_dwconv(const DwArgs &a, hipStream_t s);
+bool dw_mean_supported(const DwArgs &a);
+int dw_mean_blocks(const DwArgs &a);
 
 // ---------------------------------------------------------------- elementwise
 
@@ -130,6 +136,9 @@ size_t mean_partial_doubles(int pixels, int c, int lanes);
 hipError_t launch_mean(const float *x, long x_lane_stride, int pixels, int c, int lanes,
                        double *partial, const SeArgs *se, float *y, long y_lane_stride,
                        hipStream_t s);
+// The second pass alone, over `chunks` partial rows of c per lane.
+hipError_t launch_mean_finish(const double *partial, int pixels, int c, int chunks, int lanes,
+                              const SeArgs *se, float *y, long y_lane_stride, hipStream_t s);
 
 hipError_t launch_layernorm(const float *x, long x_lane_stride, const float *w, int rows, int c,
                             int lanes, float *y, long y_lane_stride, hipStream_t s);

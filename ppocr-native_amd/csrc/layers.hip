@@ -19,6 +19,9 @@ namespace ppocr {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
+// LDS a workgroup may use on gfx950 (kernels above 64 KiB raise their limit).
+static const size_t kMaxLds = 160 * 1024;
+
 static inline unsigned blocks_for(long n, int per) {
   long b = (n + per - 1) / per;
   return (unsigned)(b < 1 ? 1 : b);
@@ -96,67 +99,112 @@ __global__ __launch_bounds__(256) void dwconv_kernel(DwArgs a) {
 // time: each kernel row's input segment ((DX - 1) * S + K pixels of four
 // channels) is loaded once, every load of the row issued before the first
 // multiply-add; taps outside the image are skipped, as in the engine.
-template <int K, int S, int DX>
-__global__ __launch_bounds__(256) void dwconv_fixed(DwArgs a) {
+// Threads of a block of the depthwise kernel that also sums its outputs.
+constexpr int kDwMeanThreads = 256;
+
+template <int K, int S, int DX, bool MEAN>
+__global__ __launch_bounds__(MEAN ? kDwMeanThreads : 256) void dwconv_fixed(DwArgs a) {
   constexpr int SPAN = (DX - 1) * S + K;
   const int cv = a.c / 4;
   const int runs = (a.ow + DX - 1) / DX;
-  long g = (long)blockIdx.x * blockDim.x + threadIdx.x;
-  long total = (long)a.lanes * a.oh * runs * cv;
-  if (g >= total) return;
-  int ch = (int)(g % cv) * 4;
-  long t = g / cv;
-  int run = (int)(t % runs);
-  t /= runs;
-  int oy = (int)(t % a.oh);
-  int ln = (int)(t / a.oh);
-  int ox0 = run * DX;
-  const float *x = a.x + (long)ln * a.x_lane_stride + ch;
-  const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-  f32x4 acc[DX];
-  f32x4 bias = a.bias ? *reinterpret_cast<const f32x4 *>(a.bias + ch) : zero;
+  int ch, run, oy, ln;
+  bool live;
+  if constexpr (MEAN) {
+    // Block = R runs of one lane x every channel group, so that the block
+    // can sum its outputs per channel (dw_mean_blocks blocks per lane).
+    const int R = kDwMeanThreads / cv;
+    const int r = threadIdx.x / cv;
+    ch = (threadIdx.x - r * cv) * 4;
+    const int rg = blockIdx.x * R + r;
+    ln = blockIdx.y;
+    live = r < R && rg < a.oh * runs;
+    oy = rg / runs;
+    run = rg - oy * runs;
+  } else {
+    const long g = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    const long total = (long)a.lanes * a.oh * runs * cv;
+    if (g >= total) return;
+    ch = (int)(g % cv) * 4;
+    long t = g / cv;
+    run = (int)(t % runs);
+    t /= runs;
+    oy = (int)(t % a.oh);
+    ln = (int)(t / a.oh);
+    live = true;
+  }
+  double sum[4] = {0.0, 0.0, 0.0, 0.0};
+  if (live) {
+    const int ox0 = run * DX;
+    const float *x = a.x + (long)ln * a.x_lane_stride + ch;
+    const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+    f32x4 acc[DX];
+    f32x4 bias = a.bias ? *reinterpret_cast<const f32x4 *>(a.bias + ch) : zero;
 #pragma unroll
-  for (int o = 0; o < DX; o++) acc[o] = bias;
-  const int left = ox0 * S - a.pl;
+    for (int o = 0; o < DX; o++) acc[o] = bias;
+    const int left = ox0 * S - a.pl;
 #pragma unroll
-  for (int ky = 0; ky < K; ky++) {
-    const int iy = oy * a.sh + ky - a.pt;
-    if (iy < 0 || iy >= a.ih) continue;
-    const float *row = x + (long)iy * a.iw * a.c;
-    f32x4 seg[SPAN], wk[K];
-    bool in[SPAN];
+    for (int ky = 0; ky < K; ky++) {
+      const int iy = oy * a.sh + ky - a.pt;
+      if (iy < 0 || iy >= a.ih) continue;
+      const float *row = x + (long)iy * a.iw * a.c;
+      f32x4 seg[SPAN], wk[K];
+      bool in[SPAN];
 #pragma unroll
-    for (int i = 0; i < SPAN; i++) {
-      const int ix = left + i;
-      in[i] = ix >= 0 && ix < a.iw;
-      seg[i] = in[i] ? *reinterpret_cast<const f32x4 *>(row + (long)ix * a.c) : zero;
-    }
+      for (int i = 0; i < SPAN; i++) {
+        const int ix = left + i;
+        in[i] = ix >= 0 && ix < a.iw;
+        seg[i] = in[i] ? *reinterpret_cast<const f32x4 *>(row + (long)ix * a.c) : zero;
+      }
 #pragma unroll
-    for (int kx = 0; kx < K; kx++) wk[kx] = *reinterpret_cast<const f32x4 *>(a.w + (long)(ky * K + kx) * a.c + ch);
+      for (int kx = 0; kx < K; kx++) wk[kx] = *reinterpret_cast<const f32x4 *>(a.w + (long)(ky * K + kx) * a.c + ch);
 #pragma unroll
-    for (int kx = 0; kx < K; kx++) {
+      for (int kx = 0; kx < K; kx++) {
 #pragma unroll
-      for (int o = 0; o < DX; o++) {
-        const int i = o * S + kx;
-        if (in[i]) {
-          acc[o].x = fmaf(wk[kx].x, seg[i].x, acc[o].x);
-          acc[o].y = fmaf(wk[kx].y, seg[i].y, acc[o].y);
-          acc[o].z = fmaf(wk[kx].z, seg[i].z, acc[o].z);
-          acc[o].w = fmaf(wk[kx].w, seg[i].w, acc[o].w);
+        for (int o = 0; o < DX; o++) {
+          const int i = o * S + kx;
+          if (in[i]) {
+            acc[o].x = fmaf(wk[kx].x, seg[i].x, acc[o].x);
+            acc[o].y = fmaf(wk[kx].y, seg[i].y, acc[o].y);
+            acc[o].z = fmaf(wk[kx].z, seg[i].z, acc[o].z);
+            acc[o].w = fmaf(wk[kx].w, seg[i].w, acc[o].w);
+          }
         }
       }
     }
-  }
-  float *y = a.y + (long)ln * a.y_lane_stride + ((long)oy * a.ow) * a.c + ch;
+    float *y = a.y + (long)ln * a.y_lane_stride + ((long)oy * a.ow) * a.c + ch;
 #pragma unroll
-  for (int o = 0; o < DX; o++) {
-    if (ox0 + o >= a.ow) break;
-    f32x4 v = acc[o];
-    v.x = act(v.x, a.act);
-    v.y = act(v.y, a.act);
-    v.z = act(v.z, a.act);
-    v.w = act(v.w, a.act);
-    *reinterpret_cast<f32x4 *>(y + (long)(ox0 + o) * a.c) = v;
+    for (int o = 0; o < DX; o++) {
+      if (ox0 + o >= a.ow) break;
+      f32x4 v = acc[o];
+      v.x = act(v.x, a.act);
+      v.y = act(v.y, a.act);
+      v.z = act(v.z, a.act);
+      v.w = act(v.w, a.act);
+      *reinterpret_cast<f32x4 *>(y + (long)(ox0 + o) * a.c) = v;
+      if constexpr (MEAN) {
+        sum[0] += (double)v.x;
+        sum[1] += (double)v.y;
+        sum[2] += (double)v.z;
+        sum[3] += (double)v.w;
+      }
+    }
+  }
+  if constexpr (MEAN) {
+    // The block's f64 sums per channel, its runs joined in order.
+    __shared__ double red[kDwMeanThreads * 4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) red[threadIdx.x * 4 + k] = sum[k];
+    __syncthreads();
+    const int R = kDwMeanThreads / cv;
+    if ((int)threadIdx.x < cv) {
+      double tot[4] = {0.0, 0.0, 0.0, 0.0};
+      for (int r = 0; r < R; r++)
+#pragma unroll
+        for (int k = 0; k < 4; k++) tot[k] += red[(r * cv + threadIdx.x) * 4 + k];
+      double *out = a.mean_part + ((long)ln * gridDim.x + blockIdx.x) * a.c + threadIdx.x * 4;
+#pragma unroll
+      for (int k = 0; k < 4; k++) out[k] = tot[k];
+    }
   }
 }
 
@@ -166,32 +214,67 @@ static hipError_t launch_fixed(F kernel, dim3 grid, dim3 block, const DwArgs &a,
   return hipGetLastError();
 }
 
+static constexpr int kDwRun = 4;  // outputs per thread along a row
+
+// The fixed-window variants: (kernel, stride) pairs with a template, the
+// height-only strides (the recogniser's (2, 1) stages) run as stride 1.
+static int dw_fixed_kind(const DwArgs &a) {
+  if (a.kh != a.kw) return 0;
+  const int k = a.kh;
+  if (a.sh == a.sw) {
+    if (k == 3 && a.sw == 1) return 31;
+    if (k == 3 && a.sw == 2) return 32;
+    if (k == 5 && a.sw == 1) return 51;
+    if (k == 5 && a.sw == 2) return 52;
+    if (k == 7 && a.sw == 1) return 71;
+  } else if (a.sw == 1) {
+    if (k == 3) return 31;
+    if (k == 5) return 51;
+  }
+  return 0;
+}
+
+bool dw_mean_supported(const DwArgs &a) { return a.c % 4 == 0 && a.c <= 1024 && dw_fixed_kind(a) != 0; }
+
+int dw_mean_blocks(const DwArgs &a) {
+  const int cv = a.c / 4, R = kDwMeanThreads / cv;
+  const int runs = (a.ow + kDwRun - 1) / kDwRun;
+  return (a.oh * runs + R - 1) / R;
+}
+
+template <bool MEAN>
+static hipError_t launch_dw_fixed(int kind, dim3 grid, const DwArgs &a, hipStream_t s) {
+  constexpr int DX = kDwRun;
+  const dim3 block(MEAN ? kDwMeanThreads : 256);
+  switch (kind) {
+    case 31: return launch_fixed(dwconv_fixed<3, 1, DX, MEAN>, grid, block, a, s);
+    case 32: return launch_fixed(dwconv_fixed<3, 2, DX, MEAN>, grid, block, a, s);
+    case 51: return launch_fixed(dwconv_fixed<5, 1, DX, MEAN>, grid, block, a, s);
+    case 52: return launch_fixed(dwconv_fixed<5, 2, DX, MEAN>, grid, block, a, s);
+    case 71: return launch_fixed(dwconv_fixed<7, 1, DX, MEAN>, grid, block, a, s);
+  }
+  return hipErrorInvalidValue;
+}
+
 hipError_t launch_dwconv(const DwArgs &a, hipStream_t s) {
-  constexpr int DX = 4;
+  constexpr int DX = kDwRun;
   auto aligned = [](const void *p) { return p == nullptr || (uintptr_t(p) & 15) == 0; };
   bool vec = a.c % 4 == 0 && aligned(a.x) && aligned(a.y) && aligned(a.w) && aligned(a.bias) &&
              a.x_lane_stride % 4 == 0 && a.y_lane_stride % 4 == 0;
+  const int kind = dw_fixed_kind(a);
+  if (a.mean_part) {
+    // With the channel sums: only the fixed variants, one grid row per lane.
+    if (!vec || !dw_mean_supported(a) || a.lanes > 65535) return hipErrorInvalidValue;
+    return launch_dw_fixed<true>(kind, dim3(dw_mean_blocks(a), a.lanes), a, s);
+  }
   long runs = (a.ow + DX - 1) / DX;
   long total = (long)a.lanes * a.oh * runs * (vec ? a.c / 4 : a.c);
-  dim3 grid(blocks_for(total, 256)), block(256);
-  if (vec && a.kh == a.kw && a.sh == a.sw) {
-    const int k = a.kh, st = a.sw;
-    if (k == 3 && st == 1) return launch_fixed(dwconv_fixed<3, 1, DX>, grid, block, a, s);
-    if (k == 3 && st == 2) return launch_fixed(dwconv_fixed<3, 2, DX>, grid, block, a, s);
-    if (k == 5 && st == 1) return launch_fixed(dwconv_fixed<5, 1, DX>, grid, block, a, s);
-    if (k == 5 && st == 2) return launch_fixed(dwconv_fixed<5, 2, DX>, grid, block, a, s);
-    if (k == 7 && st == 1) return launch_fixed(dwconv_fixed<7, 1, DX>, grid, block, a, s);
-  }
-  if (vec && a.kh == a.kw && a.sh != a.sw && a.sw == 1) {
-    // Height-only strides (the recogniser's (2, 1) stages).
-    const int k = a.kh;
-    if (k == 3) return launch_fixed(dwconv_fixed<3, 1, DX>, grid, block, a, s);
-    if (k == 5) return launch_fixed(dwconv_fixed<5, 1, DX>, grid, block, a, s);
-  }
+  dim3 grid(blocks_for(total, 256));
+  if (vec && kind) return launch_dw_fixed<false>(kind, grid, a, s);
   if (vec)
-    hipLaunchKernelGGL((dwconv_kernel<4, DX>), grid, block, 0, s, a);
+    hipLaunchKernelGGL((dwconv_kernel<4, DX>), grid, dim3(256), 0, s, a);
   else
-    hipLaunchKernelGGL((dwconv_kernel<1, DX>), grid, block, 0, s, a);
+    hipLaunchKernelGGL((dwconv_kernel<1, DX>), grid, dim3(256), 0, s, a);
   return hipGetLastError();
 }
 
@@ -427,14 +510,32 @@ __device__ __forceinline__ float se_column(const float *w, int stride, const flo
 // multiply-add per input in order, then its bias, then its activation.
 // Each channel's partials are split between J threads (a fixed split, eight
 // independent loads in flight per thread), joined in LDS in thread order.
+// Floats of each 1x1 layer's weights that mean_finish stages in LDS; a
+// larger layer reads its weights from global memory.
+constexpr int kSeStage = 16384;
+
 __global__ __launch_bounds__(1024) void mean_finish(const double *partial, int pixels, int c,
                                                    int chunks, SeArgs se, int has_se, float *y,
                                                    long y_lane_stride) {
   extern __shared__ float smem[];
   __shared__ double red[1024];
-  float *mean = smem;         // c
-  float *hid = smem + c;      // mid
+  float *mean = smem;             // c
+  float *hid = smem + c;          // mid
+  float *w1s = hid + se.mid;      // c * mid when staged
+  float *w2s = w1s + kSeStage;    // mid * cout when staged
   const int ln = blockIdx.x, t = threadIdx.x;
+  // Both layers' weights are requested first, so that their loads overlap
+  // the partial sums' instead of following them.
+  constexpr int PER = kSeStage / 1024;
+  const int n1 = has_se ? c * se.mid : 0, n2 = has_se ? se.mid * se.cout : 0;
+  const bool st1 = n1 > 0 && n1 <= kSeStage, st2 = n2 > 0 && n2 <= kSeStage;
+  float r1[PER], r2[PER];
+#pragma unroll
+  for (int k = 0; k < PER; k++) {
+    const int e = t + k * 1024;
+    r1[k] = st1 && e < n1 ? se.w1[e] : 0.0f;
+    r2[k] = st2 && e < n2 ? se.w2[e] : 0.0f;
+  }
   const double *pl = partial + (long)ln * chunks * c;
   for (int c0 = 0; c0 < c; c0 += 1024) {
     const int cw = min(1024, c - c0);
@@ -467,16 +568,25 @@ __global__ __launch_bounds__(1024) void mean_finish(const double *partial, int p
     for (int ch = threadIdx.x; ch < c; ch += blockDim.x) yl[ch] = mean[ch];
     return;
   }
+#pragma unroll
+  for (int k = 0; k < PER; k++) {
+    const int e = t + k * 1024;
+    if (st1 && e < n1) w1s[e] = r1[k];
+    if (st2 && e < n2) w2s[e] = r2[k];
+  }
+  __syncthreads();
   // Columns below co / 8 * 8 fuse their multiply-adds; the tail columns
   // multiply and add separately (the engine's pointwise rule for one pixel).
   for (int j = threadIdx.x; j < se.mid; j += blockDim.x) {
-    float acc = se_column(se.w1 + j, se.mid, mean, c, j < se.mid / 8 * 8);
+    const bool f = j < se.mid / 8 * 8;
+    float acc = st1 ? se_column(w1s + j, se.mid, mean, c, f) : se_column(se.w1 + j, se.mid, mean, c, f);
     if (se.b1) acc = acc + se.b1[j];
     hid[j] = act(acc, se.act1);
   }
   __syncthreads();
   for (int j = threadIdx.x; j < se.cout; j += blockDim.x) {
-    float acc = se_column(se.w2 + j, se.cout, hid, se.mid, j < se.cout / 8 * 8);
+    const bool f = j < se.cout / 8 * 8;
+    float acc = st2 ? se_column(w2s + j, se.cout, hid, se.mid, f) : se_column(se.w2 + j, se.cout, hid, se.mid, f);
     if (se.b2) acc = acc + se.b2[j];
     yl[j] = act(acc, se.act2);
   }
@@ -502,8 +612,22 @@ hipError_t launch_mean(const float *x, long x_lane_stride, int pixels, int c, in
                      c, chunk, chunks, partial);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
+  return launch_mean_finish(partial, pixels, c, chunks, lanes, se, y, y_lane_stride, s);
+}
+
+hipError_t launch_mean_finish(const double *partial, int pixels, int c, int chunks, int lanes,
+                              const SeArgs *se, float *y, long y_lane_stride, hipStream_t s) {
   SeArgs none{};
-  size_t shm = (size_t)(c + (se ? se->mid : 0)) * sizeof(float);
+  size_t shm = (size_t)(c + (se ? se->mid + 2 * kSeStage : 0)) * sizeof(float);
+  if (shm > (size_t)kMaxLds - 1024 * sizeof(double)) return hipErrorInvalidValue;
+  static bool raised = false;  // once per process: the limit is a property of the kernel
+  if (!raised) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(mean_finish),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       (int)(kMaxLds - 1024 * sizeof(double)));
+    if (e != hipSuccess) return e;
+    raised = true;
+  }
   hipLaunchKernelGGL(mean_finish, dim3(lanes), dim3(1024), shm, s, partial, pixels, c, chunks,
                      se ? *se : none, se ? 1 : 0, y, y_lane_stride);
   return hipGetLastError();
@@ -756,7 +880,6 @@ static size_t attention_lds_floats(int t, int hd, bool scores) {
 }
 
 // gfx950 has 160 KiB of LDS per CU; a kernel may use it all once allowed to.
-static const size_t kMaxLds = 160 * 1024;
 
 static bool attention_in_lds(int t, int hd) {
   return attention_lds_floats(t, hd, true) * sizeof(float) <= kMaxLds;

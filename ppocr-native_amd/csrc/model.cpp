@@ -78,6 +78,8 @@ struct Step {
   int resgate = -1;  // Channelmul of a residual gate, x + x * g
   int fc1 = -1, fc2 = -1;  // squeeze-and-excite 1x1 layers after a Mean
   int head2 = -1;          // the narrow transposed convolution folded into S_HEAD
+  bool dw_sums = false;    // S_DW: also sum its output per channel for the next step's mean
+  int mean_of_dw = -1;     // S_MEAN: the depthwise operation whose sums it joins
   int elt = 0;             // EltMode
   std::vector<Source> sources;
   // Implicit-GEMM steps
@@ -222,6 +224,16 @@ size_t Model::step_writes(const Step &s) const {
 //    535-605).
 //  - An Add that is the only reader of a convolution's output: the
 //    convolution's epilogue (gpu/mod.rs:522-526).
+// The depthwise launch shape of an operation (pointers unset).
+static DwArgs dw_shape(const Op &op) {
+  DwArgs a{};
+  a.lanes = 1;
+  a.ih = int(op.ih), a.iw = int(op.iw), a.c = int(op.oc), a.oh = int(op.oh), a.ow = int(op.ow);
+  a.kh = int(op.kh), a.kw = int(op.kw), a.sh = int(op.sh), a.sw = int(op.sw);
+  a.pt = int(op.pt), a.pl = int(op.pl);
+  return a;
+}
+
 bool Model::build_steps(std::string &err) {
   const auto &ops = plan.ops;
   const size_t n = ops.size();
@@ -393,6 +405,17 @@ bool Model::build_steps(std::string &err) {
                                return std::find(inside.begin(), inside.end(), s.op) != inside.end();
                              }),
               steps.end());
+  // A channel mean right after the depthwise convolution that produces its
+  // input: the depthwise kernel sums its outputs per channel as it stores
+  // them, and the mean step only joins those sums (no second read).
+  for (size_t k = 1; k < steps.size(); k++) {
+    Step &d = steps[k - 1], &m = steps[k];
+    if (d.kind != S_DW || m.kind != S_MEAN || ops[d.op].y != ops[m.op].x) continue;
+    if (dw_mean_supported(dw_shape(ops[d.op]))) {
+      d.dw_sums = true;
+      m.mean_of_dw = d.op;
+    }
+  }
   return true;
 }
 
@@ -553,7 +576,10 @@ bool Model::arrange(Batch &b, std::string &err) {
   size_t ws = 0;
   for (const Step &s : steps) {
     const Op &op = p.ops[s.op];
-    if (s.kind == S_MEAN) ws = std::max(ws, 2 * mean_partial_doubles(int(op.ih * op.iw), int(op.ic), int(L)));
+    if (s.kind == S_MEAN && s.mean_of_dw >= 0)
+      ws = std::max(ws, 2 * L * size_t(dw_mean_blocks(dw_shape(p.ops[s.mean_of_dw]))) * op.ic);
+    else if (s.kind == S_MEAN)
+      ws = std::max(ws, 2 * mean_partial_doubles(int(op.ih * op.iw), int(op.ic), int(L)));
     if (s.kind == S_CTC) {
       size_t ntn = (s.gemm_n + s.tile.bn - 1) / s.tile.bn;
       ws = std::max(ws, L * op.iw * ntn * 4);
@@ -691,7 +717,8 @@ void Model::build_launches(Batch &b) {
       case S_DW: {
         DwArgs a{L, int(op.ih), int(op.iw), int(op.oc), int(op.oh), int(op.ow), int(op.kh), int(op.kw),
                  int(op.sh), int(op.sw), int(op.pt), int(op.pl), b.dev(op.x), b.stride(op.x), W + op.w0,
-                 bias, op.fused, Y, ys};
+                 bias, op.fused, Y, ys, nullptr};
+        if (s.dw_sums) a.mean_part = reinterpret_cast<double *>(b.arena + b.ws_off);
         b.launches.push_back({"dwconv", s.op, [a](hipStream_t st) { return launch_dwconv(a, st); }});
         break;
       }
@@ -752,6 +779,16 @@ void Model::build_launches(Batch &b) {
           const Op &f1 = p.ops[s.fc1], &f2 = p.ops[s.fc2];
           sa = SeArgs{W + f1.w0, f1.b1 ? W + f1.b0 : nullptr, int(f1.oc), f1.fused,
                       W + f2.w0, f2.b1 ? W + f2.b0 : nullptr, int(f2.oc), f2.fused};
+        }
+        if (s.mean_of_dw >= 0) {
+          DwArgs d = dw_shape(p.ops[s.mean_of_dw]);
+          d.lanes = L;
+          const int chunks = dw_mean_blocks(d);
+          b.launches.push_back({se ? "se_squeeze" : "channel_mean", s.op, [=](hipStream_t st) {
+                                  return launch_mean_finish(part, pixels, c, chunks, L, se ? &sa : nullptr, Y, ys,
+                                                            st);
+                                }});
+          break;
         }
         b.launches.push_back({se ? "se_squeeze" : "channel_mean", s.op,
                               [=](hipStream_t st) {
@@ -877,7 +914,8 @@ void Model::account(Batch &b) const {
         l.bytes = F * L * (in_px * op.ic + out_px * op.oc);
         break;
       case S_MEAN:
-        l.bytes = F * L * (in_px * op.ic + op.oc);
+        // Joining a depthwise step's sums reads none of the input again.
+        l.bytes = F * L * ((s.mean_of_dw >= 0 ? 0.0 : in_px * op.ic) + op.oc);
         if (s.fc1 >= 0) {
           const Op &f1 = p.ops[s.fc1], &f2 = p.ops[s.fc2];
           l.flops = 2.0 * L * (double(f1.ic) * f1.oc + double(f2.ic) * f2.oc);

@@ -88,24 +88,26 @@ def test_windowed_gemm(oracle, k, s, pad, ci, co):
     near(got, want)
 
 
-def test_gemm_gate_and_residual(oracle):
+@pytest.mark.parametrize("k,c,hw", [(3, 32, (21, 19)), (5, 96, (40, 52)), (3, 480, (12, 13))])
+def test_gemm_gate_and_residual(oracle, k, c, hw):
     # dw -> SE (mean, 1x1 ReLU, 1x1 hard sigmoid) -> gated pointwise + input.
-    c = 32
-    wd = RNG.normal(0, 0.3, (3, 3, c)).astype(np.float32)
-    w1 = RNG.normal(0, 0.3, (1, 1, c, 8)).astype(np.float32)
-    w2 = RNG.normal(0, 0.3, (1, 1, 8, c)).astype(np.float32)
+    # The depthwise kernel also sums its outputs per channel for the mean.
+    mid = c // 4
+    wd = RNG.normal(0, 0.3, (k, k, c)).astype(np.float32)
+    w1 = RNG.normal(0, 0.3, (1, 1, c, mid)).astype(np.float32)
+    w2 = RNG.normal(0, 0.3, (1, 1, mid, c)).astype(np.float32)
     wp = RNG.normal(0, 0.2, (1, 1, c, c)).astype(np.float32)
     bv = RNG.normal(0, 0.3, c).astype(np.float32)
 
     def build(b, t):
-        d = b.dwconv(t, wd, bv, k=(3, 3), fused="hardswish")
+        d = b.dwconv(t, wd, bv, k=(k, k), fused="hardswish")
         m = b.mean(d)
-        h = b.conv(m, w1, bv[:8], fused="relu")
+        h = b.conv(m, w1, bv[:mid], fused="relu")
         g = b.conv(h, w2, bv, fused="hardsigmoid")
         y = b.conv(b.channelmul(d, g), wp, bv)
         return [b.add(y, t), g]
 
-    got, want = both(build, (21, 19, c), oracle)
+    got, want = both(build, (*hw, c), oracle)
     near([[gl[0]] for gl in got], [[wl[0]] for wl in want])
     # The gate: the same mean to f64 rounding, then the same 1x1 sums.
     near([[gl[1]] for gl in got], [[wl[1]] for wl in want], tol=1e-6)
