@@ -12,6 +12,7 @@
 #define PPOCR_HIP_H
 
 #include <stddef.h>
+#include <stdint.h>
 
 #ifdef __cplusplus
 extern "C" {
@@ -152,6 +153,76 @@ int ppocr_hip_layer_norm(const float *x, const float *w, float *y, size_t rows, 
  * shaders/ctc.comp): for each of `rows` rows of `cols` values, y[2r] = the
  * first column holding the maximum (as f32), y[2r+1] = 1 / sum exp(v - max). */
 int ppocr_hip_row_argmax(const float *x, float *y, size_t rows, size_t cols, void *stream);
+
+/* --- Host stages either side of the model ---------------------------------
+ * CPU code in the same library: the recogniser's text from its [T][2]
+ * output, and the detector's text boxes from its probability map. Each
+ * reproduces the reference's results bit for bit. */
+
+typedef struct ppocr_dictionary ppocr_dictionary;
+
+/* Replaces `Dictionary::from_metadata` (src/rec.rs:53-79): classes = blank,
+ * the lines of `text` split as Python's str.splitlines splits them, a space. */
+int ppocr_dictionary_load(const char *text, size_t len, ppocr_dictionary **out, char *err, size_t err_len);
+void ppocr_dictionary_free(ppocr_dictionary *d);
+/* `Dictionary::len` (src/rec.rs:82-85). */
+size_t ppocr_dictionary_len(const ppocr_dictionary *d);
+/* `Dictionary::class` (src/rec.rs:93-96): UTF-8 bytes, `*len` of them; NULL
+ * for an index out of range. */
+const char *ppocr_dictionary_class(const ppocr_dictionary *d, size_t index, size_t *len);
+
+/* Replaces `ctc_decode` (src/rec.rs:133-152): repeats collapse, blanks drop,
+ * score = mean of the kept probabilities each rounded to 5 decimals (numpy's
+ * pairwise f64 sum), rounded again; 0 when nothing is kept. `text` receives
+ * UTF-8 and a NUL (returns 2 when `text_cap` is too small; `*text_len` then
+ * says how many bytes the text needs, without the NUL). */
+int ppocr_ctc_decode(const ppocr_dictionary *d, const uint32_t *best, const float *prob, size_t steps,
+                     char *text, size_t text_cap, size_t *text_len, double *score, char *err, size_t err_len);
+/* The same from the argmax recogniser's output as `ppocr_gpu_lane_output`
+ * gives it: `steps` pairs (class as f32, probability). */
+int ppocr_ctc_decode_pairs(const ppocr_dictionary *d, const float *pairs, size_t steps, char *text,
+                           size_t text_cap, size_t *text_len, double *score, char *err, size_t err_len);
+
+/* Replaces `find_contours` (src/contour.rs:44-140): the borders of the
+ * nonzero pixels as cv2.findContours(RETR_LIST, CHAIN_APPROX_SIMPLE) returns
+ * them. Writes the corners of all contours as (x, y) pairs into `points`
+ * and each contour's corner count into `lengths`; returns 2 (with the needed
+ * sizes in `*n_points` and `*n_contours`) when the buffers are too small. */
+int ppocr_find_contours(const uint8_t *mask, size_t width, size_t height, int32_t *points, size_t points_cap,
+                        size_t *lengths, size_t contours_cap, size_t *n_points, size_t *n_contours);
+
+/* Replaces `min_area_rect` and `RotatedRect::points` (src/geometry.rs:
+ * 207-261, 28-42): `rect` = centre x, y, width, height, angle (degrees);
+ * `corners` = cv2.boxPoints, (x, y) x 4. Either may be NULL. */
+int ppocr_min_area_rect(const int32_t *points, size_t n, float *rect, float *corners);
+
+/* Replaces `unclip` (src/geometry.rs:320-410): the quad (x, y) x 4 grown by
+ * area * ratio / perimeter with round joins, as pyclipper computes it;
+ * `*n` points into `ring` (returns 2 when `cap` is too small). */
+int ppocr_unclip(const float *quad, double ratio, int32_t *ring, size_t cap, size_t *n);
+
+/* `DbOptions` (src/det.rs:291-321); RapidOCR's defaults are 0.3, 0.5, 1.5,
+ * 1000. */
+typedef struct ppocr_db_options {
+  float thresh;
+  double box_thresh;
+  double unclip_ratio;
+  size_t max_candidates;
+} ppocr_db_options;
+
+/* Replaces `boxes_from_prob` (src/det.rs:430-452): the text boxes of a
+ * map_w x map_h probability map, in the pixels of a dest_w x dest_h page, in
+ * reading order, each four (x, y) corners (f32) into `boxes` (8 floats a
+ * box). `mask` (map_w * map_h bytes, nonzero = text) may come from
+ * ppocr_hip_db_mask; NULL thresholds `prob` here. Returns 2 when `boxes_cap`
+ * is too small (`*n_boxes` says how many there are). */
+int ppocr_db_boxes(const float *prob, const uint8_t *mask, size_t map_w, size_t map_h, size_t dest_w,
+                   size_t dest_h, const ppocr_db_options *options, float *boxes, size_t boxes_cap,
+                   size_t *n_boxes, char *err, size_t err_len);
+
+/* The DB threshold on the GPU (src/det.rs:438): mask[i] = prob[i] > thresh
+ * (f32), n bytes, device pointers. */
+int ppocr_hip_db_mask(const float *prob, uint8_t *mask, size_t n, float thresh, void *stream);
 
 #ifdef __cplusplus
 }

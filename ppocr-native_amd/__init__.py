@@ -74,6 +74,19 @@ def lib() -> C.CDLL:
         "ppocr_hip_channel_mul": ([vp, vp, vp, sz, sz, vp], C.c_int),
         "ppocr_hip_layer_norm": ([vp, vp, vp, sz, sz, vp], C.c_int),
         "ppocr_hip_row_argmax": ([vp, vp, sz, sz, vp], C.c_int),
+        "ppocr_hip_db_mask": ([vp, vp, sz, C.c_float, vp], C.c_int),
+        "ppocr_dictionary_load": ([cp, sz, C.POINTER(vp), cp, sz], C.c_int),
+        "ppocr_dictionary_free": ([vp], None),
+        "ppocr_dictionary_len": ([vp], sz),
+        "ppocr_dictionary_class": ([vp, sz, szp], C.POINTER(C.c_char)),
+        "ppocr_ctc_decode": ([vp, C.POINTER(C.c_uint32), fp, sz, C.c_char_p, sz, szp,
+                              C.POINTER(C.c_double), cp, sz], C.c_int),
+        "ppocr_ctc_decode_pairs": ([vp, fp, sz, C.c_char_p, sz, szp, C.POINTER(C.c_double), cp, sz],
+                                   C.c_int),
+        "ppocr_find_contours": ([vp, sz, sz, C.POINTER(C.c_int32), sz, szp, sz, szp, szp], C.c_int),
+        "ppocr_min_area_rect": ([C.POINTER(C.c_int32), sz, fp, fp], C.c_int),
+        "ppocr_unclip": ([fp, C.c_double, C.POINTER(C.c_int32), sz, szp], C.c_int),
+        "ppocr_db_boxes": ([fp, vp, sz, sz, sz, sz, vp, fp, sz, szp, cp, sz], C.c_int),
     }
     for name, (args, res) in sig.items():
         f = getattr(L, name)

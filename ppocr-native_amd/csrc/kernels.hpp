@@ -195,4 +195,7 @@ struct HeadArgs {
 bool head_supported(int ic, int oc1);
 hipError_t launch_db_head(const HeadArgs &a, hipStream_t s);
 
+// mask[i] = prob[i] > thresh over n floats (bytes out).
+hipError_t launch_db_mask(const float *prob, uint8_t *mask, long n, float thresh, hipStream_t s);
+
 }  // namespace ppocr

@@ -1043,4 +1043,26 @@ hipError_t launch_convt_small(const ConvtArgs &a, hipStream_t s) {
   return hipGetLastError();
 }
 
+// ------------------------------------------------------------ DB mask
+
+// mask[i] = prob[i] > thresh, four pixels a thread (the DB threshold,
+// src/det.rs:438, compared in f32).
+__global__ __launch_bounds__(256) void db_mask_kernel(const float *prob, uint8_t *mask, long n, float thresh) {
+  const long i = ((long)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+  if (i + 4 <= n && (reinterpret_cast<uintptr_t>(prob) & 15) == 0 && (reinterpret_cast<uintptr_t>(mask) & 3) == 0) {
+    const f32x4 p = *reinterpret_cast<const f32x4 *>(prob + i);
+    const uint32_t m = uint32_t(p.x > thresh) | uint32_t(p.y > thresh) << 8 | uint32_t(p.z > thresh) << 16 |
+                       uint32_t(p.w > thresh) << 24;
+    *reinterpret_cast<uint32_t *>(mask + i) = m;
+    return;
+  }
+  for (long k = i; k < n && k < i + 4; k++) mask[k] = prob[k] > thresh;
+}
+
+hipError_t launch_db_mask(const float *prob, uint8_t *mask, long n, float thresh, hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(db_mask_kernel, dim3(blocks_for((n + 3) / 4, 256)), dim3(256), 0, s, prob, mask, n, thresh);
+  return hipGetLastError();
+}
+
 }  // namespace ppocr

@@ -104,4 +104,10 @@ int ppocr_hip_row_argmax(const float *x, float *y, size_t rows, size_t cols, voi
   return code(launch_row_argmax(x, y, int(rows), int(cols), hipStream_t(stream)));
 }
 
+int ppocr_hip_db_mask(const float *prob, uint8_t *mask, size_t n, float thresh, void *stream) {
+  if (n == 0) return 0;
+  if (!prob || !mask || n > (size_t)1 << 40) return int(hipErrorInvalidValue);
+  return code(launch_db_mask(prob, mask, long(n), thresh, hipStream_t(stream)));
+}
+
 }  // extern "C"

@@ -86,3 +86,28 @@ def test_row_argmax(oracle):
     assert np.array_equal(got[:, 0], want[:, 0])
     assert got[5, 0] == 17
     np.testing.assert_allclose(got[:, 1], want[:, 1], rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("n", [320 * 320, 1001])
+def test_db_mask_gives_the_boxes(n):
+    # The DB threshold on the GPU, bytes out; on the reference's own map it
+    # gives the mask boxes_from_prob thresholds on the host, and so the same
+    # 11 boxes (tests/golden/prob.npy).
+    from pathlib import Path
+    from ppocr_native_amd import post
+    gold = Path(__file__).resolve().parent / "golden"
+    prob = np.load(gold / "prob.npy", allow_pickle=False).reshape(-1)[:n].copy()
+    prob[:8] = np.float32(0.3)  # on the threshold: not text
+    dp, dm = DeviceArray.of(prob), DeviceArray(n)
+    P.lib().ppocr_hip_db_mask(dp.addr, dm.addr, n, 0.3, None)
+    synchronize()
+    mask = dm.download(n, np.uint8)
+    assert np.array_equal(mask, (prob > np.float32(0.3)).astype(np.uint8))
+    if n == 320 * 320:
+        full = np.load(gold / "prob.npy", allow_pickle=False)
+        dp2 = DeviceArray.of(full.reshape(-1).copy())
+        P.lib().ppocr_hip_db_mask(dp2.addr, dm.addr, n, 0.3, None)
+        synchronize()
+        got = post.boxes_from_prob(full, 320, 320, 325, 323, mask=dm.download(n, np.uint8))
+        assert np.array_equal(post.boxes_from_prob(full, 320, 320, 325, 323), got)
+        assert got.shape == (11, 4, 2)
