@@ -224,6 +224,44 @@ int ppocr_db_boxes(const float *prob, const uint8_t *mask, size_t map_w, size_t 
  * (f32), n bytes, device pointers. */
 int ppocr_hip_db_mask(const float *prob, uint8_t *mask, size_t n, float thresh, void *stream);
 
+/* --- Image stages on the GPU ------------------------------------------------
+ * Device pointers, 8-bit three-channel images with rows top to bottom (HWC,
+ * as the worker decodes pages), sides up to 32768. Results are the
+ * reference's CPU results, bit for bit. */
+
+/* Replaces `resize_linear` (src/image.rs:68-142): cv2.resize INTER_LINEAR on
+ * 8 bits, sw x sh -> dw x dh. */
+int ppocr_hip_resize_linear(const uint8_t *src, size_t sw, size_t sh, uint8_t *dst, size_t dw, size_t dh,
+                            void *stream);
+
+/* Replaces `det_input_hwc` (src/det.rs:228-289): the page resized to ow x oh,
+ * v * (1/255 as f32), then (x - mean[c]) / std[c] in f64, one f32 rounding;
+ * HWC f32 into `out` (3 * ow * oh floats, e.g. the detector's input). */
+int ppocr_hip_det_input(const uint8_t *page, size_t w, size_t h, float *out, size_t ow, size_t oh,
+                        const double *mean, const double *std, void *stream);
+
+/* The recogniser tensor width for a w x h crop and, in `*resized_w`, the
+ * width the crop is resized to (src/rec.rs:20-31); 0 for an empty crop. */
+size_t ppocr_rec_width(size_t w, size_t h, size_t *resized_w);
+
+/* Replaces `rec_input` (src/rec.rs:19-43), HWC: 48 rows of
+ * ppocr_rec_width(w, h) pixels, the crop resized to height 48 and scaled to
+ * [-1, 1] in f32, zeros right of it. `out_cap` floats at `out`; `*width`
+ * receives the tensor width. */
+int ppocr_hip_rec_input(const uint8_t *crop, size_t w, size_t h, float *out, size_t out_cap, size_t *width,
+                        void *stream);
+
+/* The size `ppocr_hip_crop_text` gives a quad's crop, after any turn. */
+int ppocr_crop_size(const float *quad, size_t *width, size_t *height);
+
+/* Replaces `crop_text` (src/crop.rs:84-127): the quad (x, y) x 4, top-left,
+ * top-right, bottom-right, bottom-left, mapped onto an upright rectangle and
+ * sampled bicubically (edges repeated), turned a quarter counter-clockwise
+ * when 1.5 times taller than wide. `*out_w` x `*out_h` pixels into `out`
+ * (`out_cap` bytes). */
+int ppocr_hip_crop_text(const uint8_t *page, size_t w, size_t h, const float *quad, uint8_t *out,
+                        size_t out_cap, size_t *out_w, size_t *out_h, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

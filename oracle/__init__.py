@@ -206,3 +206,83 @@ def row_argmax(x, rows: int, cols: int, nthreads: int | None = None):
     y = np.empty(2 * rows, np.float32)
     lib().oracle_row_argmax(x, y, rows, cols, nthreads or threads())
     return y
+
+
+# ---------------------------------------------------------------- image stages
+# Restatements of the reference's image arithmetic (oracle/image.c); images
+# are uint8 HxWx3 arrays.
+
+def _u8p(a):
+    return a.ctypes.data_as(C.POINTER(C.c_uint8))
+
+
+def _img(a) -> np.ndarray:
+    a = np.ascontiguousarray(a, np.uint8)
+    assert a.ndim == 3 and a.shape[2] == 3, a.shape
+    return a
+
+
+def resize_linear(image, width: int, height: int) -> np.ndarray:
+    src = _img(image)
+    out = np.empty((height, width, 3), np.uint8)
+    L = lib()
+    L.oracle_resize_linear.argtypes = [C.POINTER(C.c_uint8), C.c_size_t, C.c_size_t,
+                                       C.POINTER(C.c_uint8), C.c_size_t, C.c_size_t]
+    L.oracle_resize_linear(_u8p(src), src.shape[1], src.shape[0], _u8p(out), width, height)
+    return out
+
+
+def det_input(image, width: int, height: int, mean, std) -> np.ndarray:
+    """HWC f32, height x width x 3."""
+    src = _img(image)
+    out = np.empty((height, width, 3), np.float32)
+    m = (C.c_double * 3)(*mean)
+    s = (C.c_double * 3)(*std)
+    L = lib()
+    L.oracle_det_input.argtypes = [C.POINTER(C.c_uint8), C.c_size_t, C.c_size_t, C.c_size_t, C.c_size_t,
+                                   C.POINTER(C.c_double), C.POINTER(C.c_double), C.POINTER(C.c_float)]
+    L.oracle_det_input(_u8p(src), src.shape[1], src.shape[0], width, height, m, s,
+                       out.ctypes.data_as(C.POINTER(C.c_float)))
+    return out
+
+
+def rec_width(w: int, h: int) -> tuple[int, int]:
+    """(tensor width, resized width) of a w x h crop."""
+    L = lib()
+    L.oracle_rec_width.argtypes = [C.c_size_t, C.c_size_t, C.POINTER(C.c_size_t)]
+    L.oracle_rec_width.restype = C.c_size_t
+    rw = C.c_size_t()
+    width = L.oracle_rec_width(w, h, C.byref(rw))
+    return width, rw.value
+
+
+def rec_input(crop) -> np.ndarray:
+    """HWC f32, 48 x width x 3."""
+    src = _img(crop)
+    width, _ = rec_width(src.shape[1], src.shape[0])
+    out = np.empty((48, width, 3), np.float32)
+    L = lib()
+    L.oracle_rec_input.argtypes = [C.POINTER(C.c_uint8), C.c_size_t, C.c_size_t, C.POINTER(C.c_float),
+                                   C.c_size_t]
+    L.oracle_rec_input.restype = C.c_size_t
+    got = L.oracle_rec_input(_u8p(src), src.shape[1], src.shape[0],
+                             out.ctypes.data_as(C.POINTER(C.c_float)), out.size)
+    assert got == width
+    return out
+
+
+def crop_text(image, quad) -> np.ndarray:
+    src = _img(image)
+    q = np.ascontiguousarray(np.asarray(quad, np.float32).reshape(8))
+    L = lib()
+    L.oracle_crop_size.argtypes = [C.POINTER(C.c_float), C.POINTER(C.c_size_t), C.POINTER(C.c_size_t)]
+    L.oracle_crop_text.argtypes = [C.POINTER(C.c_uint8), C.c_size_t, C.c_size_t, C.POINTER(C.c_float),
+                                   C.POINTER(C.c_uint8), C.c_size_t, C.POINTER(C.c_size_t),
+                                   C.POINTER(C.c_size_t)]
+    qp = q.ctypes.data_as(C.POINTER(C.c_float))
+    w, h = C.c_size_t(), C.c_size_t()
+    L.oracle_crop_size(qp, C.byref(w), C.byref(h))
+    out = np.empty(max(w.value * h.value * 3, 1), np.uint8)
+    assert L.oracle_crop_text(_u8p(src), src.shape[1], src.shape[0], qp, _u8p(out), out.size,
+                              C.byref(w), C.byref(h))
+    return out[:w.value * h.value * 3].reshape(h.value, w.value, 3)

@@ -198,4 +198,17 @@ hipError_t launch_db_head(const HeadArgs &a, hipStream_t s);
 // mask[i] = prob[i] > thresh over n floats (bytes out).
 hipError_t launch_db_mask(const float *prob, uint8_t *mask, long n, float thresh, hipStream_t s);
 
+// ------------------------------------------------------------- image stages
+
+// Device-memory image stages (HWC, 8-bit BGR in). See image.hip.
+struct CropMap {
+  double v[9];  // rectangle -> quad projective map, row major, v[8] = 1
+};
+hipError_t launch_resize(const uint8_t *src, int sw, int sh, uint8_t *dst, int dw, int dh, hipStream_t s);
+hipError_t launch_det_input(const uint8_t *src, int sw, int sh, float *out, int dw, int dh, const double *mean,
+                            const double *sd, hipStream_t s);
+hipError_t launch_rec_input(const uint8_t *src, int sw, int sh, float *out, int width, int rw, hipStream_t s);
+hipError_t launch_crop(const uint8_t *img, int iw, int ih, const CropMap &m, uint8_t *out, int width, int height,
+                       bool turn, hipStream_t s);
+
 }  // namespace ppocr

@@ -1,8 +1,12 @@
-// The engine's elementwise and reduction layers as single kernels on device
-// pointers: the ppocr_hip_* entry points of include/ppocr_hip.h. They launch
-// the kernels the model uses for the same layers.
+// The ppocr_hip_* entry points of include/ppocr_hip.h on device pointers:
+// the engine's elementwise and reduction layers as single kernels (the ones
+// the model launches for those layers), the DB threshold, and the image
+// stages either side of the networks (resize, detector and recogniser
+// inputs, text crop).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+#include <cmath>
 #include <mutex>
 #include <vector>
 
@@ -53,6 +57,54 @@ double *partial_for(size_t doubles, hipError_t *err) {
 }
 
 }  // namespace
+
+// The crop's size, before any turn: the longer of each pair of opposite
+// sides, truncated (src/crop.rs:85-86; side lengths in f32).
+static void crop_size(const float *q, size_t *w, size_t *h) {
+  auto d = [&](int a, int b) {
+    const float dx = q[2 * a] - q[2 * b], dy = q[2 * a + 1] - q[2 * b + 1];
+    return std::sqrt(dx * dx + dy * dy);
+  };
+  *w = size_t(std::fmax(d(0, 1), d(2, 3)));
+  *h = size_t(std::fmax(d(0, 3), d(1, 2)));
+}
+
+// The projective map sending the width x height rectangle's corners to the
+// quad: eight linear equations in f64, Gaussian elimination with partial
+// pivoting (ties to the lower row), src/crop.rs:7-53.
+static ppocr::CropMap rect_to_quad(double width, double height, const float *q) {
+  double m[8][9];
+  const double from[4][2] = {{0, 0}, {width, 0}, {width, height}, {0, height}};
+  for (int i = 0; i < 4; i++) {
+    const double x = from[i][0], y = from[i][1], u = double(q[2 * i]), v = double(q[2 * i + 1]);
+    const double r0[9] = {x, y, 1.0, 0.0, 0.0, 0.0, -x * u, -y * u, u};
+    const double r1[9] = {0.0, 0.0, 0.0, x, y, 1.0, -x * v, -y * v, v};
+    std::copy(r0, r0 + 9, m[i]);
+    std::copy(r1, r1 + 9, m[i + 4]);
+  }
+  for (int col = 0; col < 8; col++) {
+    int piv = col;
+    for (int r = col + 1; r < 8; r++)
+      if (std::fabs(m[r][col]) >= std::fabs(m[piv][col])) piv = r;
+    std::swap(m[col], m[piv]);
+    const double p = m[col][col];
+    if (p == 0.0) continue;
+    double prow[9];
+    std::copy(m[col], m[col] + 9, prow);
+    for (int r = 0; r < 8; r++) {
+      const double f = m[r][col] / p;
+      if (r == col || f == 0.0) continue;
+      for (int k = col; k < 9; k++) m[r][k] -= f * prow[k];
+    }
+  }
+  ppocr::CropMap out;
+  for (int i = 0; i < 8; i++) out.v[i] = m[i][i] == 0.0 ? 0.0 : m[i][8] / m[i][i];
+  out.v[8] = 1.0;
+  return out;
+}
+
+// Largest image side the image stages take (keeps every index in 32 bits).
+static const size_t kMaxSide = 1 << 15;
 
 extern "C" {
 
@@ -108,6 +160,67 @@ int ppocr_hip_db_mask(const float *prob, uint8_t *mask, size_t n, float thresh, 
   if (n == 0) return 0;
   if (!prob || !mask || n > (size_t)1 << 40) return int(hipErrorInvalidValue);
   return code(launch_db_mask(prob, mask, long(n), thresh, hipStream_t(stream)));
+}
+
+// ------------------------------------------------------------ image stages
+
+int ppocr_hip_resize_linear(const uint8_t *src, size_t sw, size_t sh, uint8_t *dst, size_t dw, size_t dh,
+                            void *stream) {
+  if (!sw || !sh || !dw || !dh || !src || !dst || sw > kMaxSide || sh > kMaxSide || dw > kMaxSide || dh > kMaxSide)
+    return int(hipErrorInvalidValue);
+  return code(launch_resize(src, int(sw), int(sh), dst, int(dw), int(dh), hipStream_t(stream)));
+}
+
+int ppocr_hip_det_input(const uint8_t *page, size_t w, size_t h, float *out, size_t ow, size_t oh,
+                        const double *mean, const double *std, void *stream) {
+  if (!w || !h || !ow || !oh || !page || !out || !mean || !std || w > kMaxSide || h > kMaxSide || ow > kMaxSide ||
+      oh > kMaxSide)
+    return int(hipErrorInvalidValue);
+  return code(launch_det_input(page, int(w), int(h), out, int(ow), int(oh), mean, std, hipStream_t(stream)));
+}
+
+size_t ppocr_rec_width(size_t w, size_t h, size_t *resized_w) {
+  if (!w || !h) return 0;
+  const double height = 48.0, r = double(w) / double(h);
+  const double ratio = std::max(320.0 / height, r);
+  const size_t width = size_t(height * ratio);
+  const double fitted = std::ceil(height * r);
+  if (resized_w) *resized_w = fitted > double(width) ? width : size_t(fitted);
+  return width;
+}
+
+int ppocr_hip_rec_input(const uint8_t *crop, size_t w, size_t h, float *out, size_t out_cap, size_t *width,
+                        void *stream) {
+  size_t rw = 0;
+  const size_t wd = ppocr_rec_width(w, h, &rw);
+  if (width) *width = wd;
+  if (!wd || !crop || !out || w > kMaxSide || h > kMaxSide || wd > kMaxSide || rw == 0) return int(hipErrorInvalidValue);
+  if (48 * wd * 3 > out_cap) return int(hipErrorInvalidValue);
+  return code(launch_rec_input(crop, int(w), int(h), out, int(wd), int(rw), hipStream_t(stream)));
+}
+
+int ppocr_crop_size(const float *quad, size_t *width, size_t *height) {
+  if (!quad) return 1;
+  size_t w, h;
+  crop_size(quad, &w, &h);
+  const bool turn = double(h) / double(w) >= 1.5;
+  if (width) *width = turn ? h : w;
+  if (height) *height = turn ? w : h;
+  return 0;
+}
+
+int ppocr_hip_crop_text(const uint8_t *page, size_t w, size_t h, const float *quad, uint8_t *out, size_t out_cap,
+                        size_t *out_w, size_t *out_h, void *stream) {
+  if (!page || !quad || !w || !h || w > kMaxSide || h > kMaxSide) return int(hipErrorInvalidValue);
+  size_t cw, ch;
+  crop_size(quad, &cw, &ch);
+  const bool turn = double(ch) / double(cw) >= 1.5;
+  if (out_w) *out_w = turn ? ch : cw;
+  if (out_h) *out_h = turn ? cw : ch;
+  if (cw * ch == 0) return 0;
+  if (!out || cw > kMaxSide || ch > kMaxSide || cw * ch * 3 > out_cap) return int(hipErrorInvalidValue);
+  const CropMap m = rect_to_quad(double(cw), double(ch), quad);
+  return code(launch_crop(page, int(w), int(h), m, out, int(cw), int(ch), turn, hipStream_t(stream)));
 }
 
 }  // extern "C"
