@@ -191,6 +191,97 @@ def bench_micro(P, repeats: int = 20) -> dict:
     return out
 
 
+def bench_stages(P, nets, repeats: int = 20) -> dict:
+    """The stages either side of the networks: GPU image kernels on a
+    2550x3300 page (letter at 300 dpi) resident in HBM, and the host DB and
+    CTC steps on this host's CPU."""
+    import ctypes as C
+    from ppocr_native_amd import images, post
+    from ppocr_native_amd.devmem import DeviceArray, Timer, synchronize
+    L = images._sig()
+    rng = np.random.default_rng(3)
+    out = {}
+
+    def timeit(fn):
+        fn()
+        synchronize()
+        t = Timer()
+        t.start()
+        for _ in range(repeats):
+            fn()
+        return t.stop() / repeats
+
+    ph, pw = 3300, 2550
+    page = rng.integers(0, 256, (ph, pw, 3), dtype=np.uint8)
+    dpage = DeviceArray.of(page.reshape(-1))
+    oh, ow = 960, 736
+    dinp = DeviceArray(4 * oh * ow * 3)
+    m, sd = (C.c_double * 3)(*images.MEAN), (C.c_double * 3)(*images.STD)
+    ms = timeit(lambda: L.ppocr_hip_det_input(dpage.addr, pw, ph, dinp.addr, ow, oh, m, sd, None))
+    # Bytes the kernel must move: the f32 tensor written and, at most, the
+    # page rows and columns its taps touch (2 source rows x 2 columns per
+    # output pixel, less where neighbours share them).
+    nb = 4 * oh * ow * 3 + min(ph, 2 * oh) * min(pw, 2 * ow) * 3
+    out["det_input 2550x3300 -> 736x960"] = {"ms": round(ms, 4), "gb_per_s": round(nb / ms / 1e6, 1),
+                                             "frac_hbm": round(nb / ms / 1e6 / PEAK_HBM_GBS, 3),
+                                             "bytes": nb}
+    # 16 tilted line crops of about 600 x 40 pixels, then their recogniser inputs.
+    quads = []
+    for i in range(16):
+        x, y, w, h, t = 100 + 7 * i, 200 + 180 * i, 600 + 10 * i, 40, 0.02 * (i - 8)
+        c, s = np.cos(t), np.sin(t)
+        quads.append(np.asarray([[x, y], [x + w * c, y + w * s], [x + w * c - h * s, y + w * s + h * c],
+                                 [x - h * s, y + h * c]], np.float32))
+    sizes = [images.crop_size(q) for q in quads]
+    dcrop = [DeviceArray(cw * ch * 3) for cw, ch in sizes]
+    widths = [images.rec_width(cw, ch)[0] for cw, ch in sizes]
+    dins = [DeviceArray(4 * 48 * wd * 3) for wd in widths]
+    ow_, oh_ = C.c_size_t(), C.c_size_t()
+    qps = [q.ctypes.data_as(C.POINTER(C.c_float)) for q in quads]
+
+    def crops():
+        for q, d, (cw, ch) in zip(qps, dcrop, sizes):
+            L.ppocr_hip_crop_text(dpage.addr, pw, ph, q, d.addr, cw * ch * 3, C.byref(ow_), C.byref(oh_), None)
+
+    ms = timeit(crops)
+    px = sum(cw * ch for cw, ch in sizes)
+    out["crop_text 16 lines"] = {"ms": round(ms, 4), "pixels": px,
+                                 "gb_per_s": round(px * 3 * 2 / ms / 1e6, 1)}
+    wd_ = C.c_size_t()
+
+    def rec_inputs():
+        for d, di, (cw, ch), wd in zip(dcrop, dins, sizes, widths):
+            L.ppocr_hip_rec_input(d.addr, cw, ch, di.addr, 48 * wd * 3, C.byref(wd_), None)
+
+    ms = timeit(rec_inputs)
+    out["rec_input 16 lines"] = {"ms": round(ms, 4), "floats": sum(48 * w * 3 for w in widths)}
+    # Host: DB boxes of the 320x320 reference map and of a 960x960 map, and
+    # CTC decode of 16 lines of 80 steps.
+    gold = ROOT / "tests" / "golden"
+    prob = np.load(gold / "prob.npy", allow_pickle=False)
+    t0 = time.perf_counter()
+    for _ in range(repeats):
+        boxes = post.boxes_from_prob(prob, 320, 320, 325, 323)
+    out["db_boxes 320x320 (host)"] = {"ms": round((time.perf_counter() - t0) * 1e3 / repeats, 4),
+                                      "boxes": int(boxes.shape[0])}
+    big = np.kron(prob, np.ones((3, 3), np.float32))
+    t0 = time.perf_counter()
+    for _ in range(5):
+        boxes = post.boxes_from_prob(big, 960, 960, 2550, 3300)
+    out["db_boxes 960x960 (host)"] = {"ms": round((time.perf_counter() - t0) * 1e3 / 5, 4),
+                                      "boxes": int(boxes.shape[0])}
+    d = post.Dictionary.from_metadata((gold / "characters.txt").read_text(encoding="utf-8"))
+    pairs = [np.stack([rng.integers(0, 18710, 80).astype(np.float32),
+                       rng.uniform(0.5, 1, 80).astype(np.float32)], 1) for _ in range(16)]
+    t0 = time.perf_counter()
+    for _ in range(repeats):
+        for q in pairs:
+            post.ctc_decode_pairs(q, d)
+    out["ctc_decode 16 lines x 80 steps (host)"] = {
+        "ms": round((time.perf_counter() - t0) * 1e3 / repeats, 4)}
+    return out
+
+
 def cpu_baseline(nets, det_plan, rec_plan, budget_s: float) -> tuple[dict, dict]:
     sys.path.insert(0, str(ROOT))
     import oracle
@@ -281,6 +372,8 @@ def main() -> int:
         log("bench: fused block, microkernels")
         result["block"] = bench_block(P, nets, args.steps, args.warmup)
         result["micro"] = bench_micro(P)
+        log("bench: stages either side of the networks")
+        result["stages"] = bench_stages(P, nets)
     else:
         rec_plan = nets.recognizer_plan(init="baseline")
     if not args.no_cpu:
