@@ -25,7 +25,7 @@ import numpy as np
 ROOT = Path(__file__).resolve().parent
 PEAK_HBM_GBS = 8000.0
 PEAK_FP32_MFMA_TFLOPS = 157.3
-GEMM_LAUNCHES = {"pointwise_gemm", "conv_gemm", "convt_gemm", "ctc_gemm"}
+GEMM_LAUNCHES = {"pointwise_gemm", "conv_gemm", "conv_patch", "convt_gemm", "ctc_gemm"}
 
 
 def package():

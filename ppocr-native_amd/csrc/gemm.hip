@@ -370,6 +370,141 @@ __global__ __launch_bounds__(256) void conv_mfma(ConvArgs a) {
   }
 }
 
+// A windowed convolution (kh, kw <= 3, stride 1 or 2, one to four sources,
+// upsampled by 2^shift, channels a multiple of 4) on tiles of the output:
+// 16 pixels wide by 4 * WR rows of one lane, BN output channels. For each
+// block of CB input channels the workgroup stages in LDS the input patch its
+// window covers (the tile plus the halo) and the block's weights for every
+// tap, then runs all taps from there: each input element is fetched, and its
+// source and position decoded, once per block instead of once per tap.
+// Channel blocks are the packed weights' chunks (BK = CB), so the reduction
+// order is channel block, tap, channel; bias, activation, residual and the
+// second activation as in conv_mfma's epilogue. Wave w owns output rows
+// w * WR .. w * WR + WR - 1 of the tile, one 16 x 16 MFMA row block each.
+template <int WR, int BN, int CB>
+__global__ __launch_bounds__(256) void conv_patch(ConvArgs a, int tiles_x, int tiles_y) {
+  constexpr int S = CB + 4;        // LDS row of one pixel / one (n, tap)
+  constexpr int KS = CB / 4;       // channels per lane group per tap
+  constexpr int KW = KS >= 4 ? 4 : KS;
+  constexpr int KR = KS / KW;
+  constexpr int NT = BN / 16;
+  constexpr int TH = 4 * WR, TW = 16;
+  constexpr int CQ = CB / 4;       // float4 groups per pixel
+  extern __shared__ __attribute__((aligned(16))) float lds[];
+  const int taps = a.kh * a.kw;
+  const int PR = (TH - 1) * a.sh + a.kh, PC = (TW - 1) * a.sw + a.kw;
+  float *P = lds;                      // PR * PC pixels x S
+  float *Bs = lds + PR * PC * S;       // BN x taps x S
+
+  const int ntn = (a.n + BN - 1) / BN;
+  int t = blockIdx.x;
+  const int tn = t % ntn;
+  t /= ntn;
+  const int tx0 = (t % tiles_x) * TW;
+  t /= tiles_x;
+  const int ty0 = (t % tiles_y) * TH;
+  const int ln = t / tiles_y;
+  const int n0 = tn * BN;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int li = lane & 15, lg = lane >> 4;
+  const int iy0 = ty0 * a.sh - a.pt, ix0 = tx0 * a.sw - a.pl;
+
+  f32x4 acc[WR][NT];
+#pragma unroll
+  for (int i = 0; i < WR; i++)
+#pragma unroll
+    for (int j = 0; j < NT; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  for (int cc = 0; cc < a.cpt; cc++) {
+    if (cc) __syncthreads();  // the previous block's reads are done
+    // The patch: pixel-major, each pixel's CB channels (zero outside the
+    // image and past the last channel).
+    const int pe = PR * PC * CQ;
+    for (int e = tid; e < pe; e += 256) {
+      const int pix = e / CQ, q = e - pix * CQ;
+      const int py = pix / PC, px = pix - py * PC;
+      const int iy = iy0 + py, ix = ix0 + px, c = cc * CB + q * 4;
+      f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (c < a.ctot && iy >= 0 && iy < a.ih && ix >= 0 && ix < a.iw) {
+        const ConvSrc src = pick_src(a, c);
+        const int cl = c - src.coff;
+        const long at = (long)(iy >> src.shift) * (a.iw >> src.shift) + (ix >> src.shift);
+        v = *reinterpret_cast<const f32x4 *>(src.p + (long)ln * src.lane_stride + at * src.c + cl);
+        if (a.gate && src.coff == 0)
+          v = v * *reinterpret_cast<const f32x4 *>(a.gate + (long)ln * a.gate_lane_stride + cl);
+      }
+      *reinterpret_cast<f32x4 *>(P + pix * S + q * 4) = v;
+    }
+    // The block's weights: for each output column and tap, CB values.
+    const int be = BN * taps * CQ;
+    for (int e = tid; e < be; e += 256) {
+      const int n = e / (taps * CQ), r = e - n * (taps * CQ);
+      const int tp = r / CQ, q = r - tp * CQ;
+      const f32x4 w = *reinterpret_cast<const f32x4 *>(a.wt + (long)(n0 + n) * a.wt_k +
+                                                      (long)(tp * a.cpt + cc) * CB + q * 4);
+      *reinterpret_cast<f32x4 *>(Bs + (n * taps + tp) * S + q * 4) = w;
+    }
+    __syncthreads();
+    for (int tp = 0; tp < taps; tp++) {
+      const int ky = tp / a.kw, kx = tp - ky * a.kw;
+#pragma unroll
+      for (int r = 0; r < KR; r++) {
+        typedef typename VecT<KW>::T KT;
+        KT av[WR], bv[NT];
+#pragma unroll
+        for (int i = 0; i < WR; i++) {
+          const int ty = wave * WR + i;
+          const int pix = (ty * a.sh + ky) * PC + li * a.sw + kx;
+          av[i] = *reinterpret_cast<const KT *>(P + pix * S + lg * KS + r * KW);
+        }
+#pragma unroll
+        for (int j = 0; j < NT; j++)
+          bv[j] = *reinterpret_cast<const KT *>(Bs + ((j * 16 + li) * taps + tp) * S + lg * KS + r * KW);
+#pragma unroll
+        for (int k = 0; k < KW; k++) {
+#pragma unroll
+          for (int i = 0; i < WR; i++) {
+#pragma unroll
+            for (int j = 0; j < NT; j++) {
+              float x, w;
+              if constexpr (KW == 1) {
+                x = av[i];
+                w = bv[j];
+              } else {
+                x = av[i][k];
+                w = bv[j][k];
+              }
+              acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(x, w, acc[i][j], 0, 0, 0);
+            }
+          }
+        }
+      }
+    }
+  }
+
+#pragma unroll
+  for (int i = 0; i < WR; i++) {
+    const int oy = ty0 + wave * WR + i;
+    if (oy >= a.oh) continue;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int ox = tx0 + lg * 4 + r;
+      if (ox >= a.ow) continue;
+      const long rem = (long)oy * a.ow + ox;
+#pragma unroll
+      for (int j = 0; j < NT; j++) {
+        const int n = n0 + j * 16 + li;
+        if (n >= a.n) continue;
+        float v = acc[i][j][r];
+        if (a.bias) v = v + a.bias[n];
+        v = act(v, a.act);
+        if (a.res) v = act(v + a.res[(long)ln * a.res_lane_stride + rem * a.n + n], a.act2);
+        a.y[(long)ln * a.y_lane_stride + rem * a.n + n] = v;
+      }
+    }
+  }
+}
+
 // One wave per row: join the row's tile partials, then y = (best, 1 / sum).
 __global__ __launch_bounds__(256) void ctc_merge(const float4 *part, int rows, int ntiles,
                                                  float *y, long y_lane_stride, int rows_per_lane) {
@@ -428,6 +563,9 @@ static hipError_t go(const ConvArgs &a, hipStream_t s) {
 
 bool gemm_tile_supported(const GemmTile &t) {
   if (t.bk == 64) return t.vec && t.wm == 16 && (t.bn == 16 || t.bn == 32 || t.bn == 64);
+  // One chunk per tap of 48 or 96 channels: windowed, 64-row tiles.
+  if (t.bk == 48 || t.bk == 96)
+    return t.vec && !t.pointwise && t.wm == 16 && (t.bn == 16 || t.bn == 32 || t.bn == 64);
   bool tile = (t.wm == 32 || t.wm == 16) && (t.bn == 16 || t.bn == 32 || t.bn == 64);
   if (!tile) return false;
   if (t.vec) return t.bk == 8 || t.bk == 16 || t.bk == 32;
@@ -450,9 +588,69 @@ hipError_t launch_conv(const ConvArgs &a, const GemmTile &t, hipStream_t s) {
     if (a.nsrc != 1 || a.src[0].shift != 0 || a.ctot != a.src[0].c) return hipErrorInvalidValue;
     PPOCR_CHUNKS(L_POINTWISE)
   } else if (a.nsrc == 1 && a.src[0].shift == 0 && a.kh <= 8 && a.kw <= 8) {
+    if (t.bk == 96) { PPOCR_TILES_SMALL(96, L_WINDOW) }
+    if (t.bk == 48) { PPOCR_TILES_SMALL(48, L_WINDOW) }
     PPOCR_CHUNKS(L_WINDOW)
   } else {
+    if (t.bk == 96) { PPOCR_TILES_SMALL(96, L_SOURCES) }
+    if (t.bk == 48) { PPOCR_TILES_SMALL(48, L_SOURCES) }
     PPOCR_CHUNKS(L_SOURCES)
+  }
+  return hipErrorInvalidValue;
+}
+
+bool patch_supported(const ConvArgs &a, int bk, int bn) {
+  if (a.mode != GEMM_STORE || a.kh < 1 || a.kw < 1 || a.kh > 3 || a.kw > 3) return false;
+  if (a.sh != a.sw || (a.sh != 1 && a.sh != 2)) return false;
+  if ((bk != 8 && bk != 16 && bk != 32) || (bn != 16 && bn != 32 && bn != 64)) return false;
+  for (int k = 0; k < a.nsrc; k++)
+    if (a.src[k].c % 4 || a.src[k].coff % 4) return false;
+  return patch_lds_bytes(a, 2, bk, bn) <= 160 * 1024;
+}
+
+size_t patch_lds_bytes(const ConvArgs &a, int wr, int bk, int bn) {
+  const size_t pr = size_t(4 * wr - 1) * a.sh + a.kh, pc = size_t(15) * a.sw + a.kw;
+  return (pr * pc + size_t(bn) * a.kh * a.kw) * (bk + 4) * sizeof(float);
+}
+
+template <int WR, int BN, int CB>
+static hipError_t go_patch(const ConvArgs &a, hipStream_t s) {
+  constexpr int TH = 4 * WR;
+  const long tiles_x = (a.ow + 15) / 16, tiles_y = (a.oh + TH - 1) / TH;
+  const long ntn = (a.n + BN - 1) / BN;
+  const long blocks = (long)a.lanes * tiles_y * tiles_x * ntn;
+  if (blocks <= 0 || blocks > 0x7fffffffL) return hipErrorInvalidValue;
+  const size_t shm = patch_lds_bytes(a, WR, CB, BN);
+  if (shm > 160 * 1024) return hipErrorInvalidValue;
+  if (shm > 64 * 1024) {
+    static bool raised = false;  // once per process: the limit is a property of the kernel
+    if (!raised) {
+      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(conv_patch<WR, BN, CB>),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+      if (e != hipSuccess) return e;
+      raised = true;
+    }
+  }
+  hipLaunchKernelGGL((conv_patch<WR, BN, CB>), dim3((unsigned)blocks), dim3(256), shm, s, a, (int)tiles_x,
+                     (int)tiles_y);
+  return hipGetLastError();
+}
+
+#define PPOCR_PATCH(WR, CB)                                        \
+  if (bn == 16) return go_patch<WR, 16, CB>(a, s);               \
+  if (bn == 32) return go_patch<WR, 32, CB>(a, s);               \
+  if (bn == 64) return go_patch<WR, 64, CB>(a, s);
+
+hipError_t launch_conv_patch(const ConvArgs &a, int wr, int bk, int bn, hipStream_t s) {
+  if (!patch_supported(a, bk, bn) || (wr != 1 && wr != 2)) return hipErrorInvalidValue;
+  if (wr == 2) {
+    if (bk == 32) { PPOCR_PATCH(2, 32) }
+    if (bk == 16) { PPOCR_PATCH(2, 16) }
+    if (bk == 8) { PPOCR_PATCH(2, 8) }
+  } else {
+    if (bk == 32) { PPOCR_PATCH(1, 32) }
+    if (bk == 16) { PPOCR_PATCH(1, 16) }
+    if (bk == 8) { PPOCR_PATCH(1, 8) }
   }
   return hipErrorInvalidValue;
 }

@@ -63,6 +63,12 @@ struct GemmTile {
 // WM 16 (BN 64); BK 64 (channel layout) with WM 16 and BN 16, 32, 64.
 bool gemm_tile_supported(const GemmTile &t);
 hipError_t launch_conv(const ConvArgs &a, const GemmTile &t, hipStream_t s);
+// The halo-tile windowed convolution (GEMM_STORE, kh, kw <= 3, stride 1 or
+// 2, channels a multiple of 4): output tiles 16 wide x 4 * wr rows, bn
+// columns, channel blocks of bk (the packed weights' chunk).
+bool patch_supported(const ConvArgs &a, int bk, int bn);
+size_t patch_lds_bytes(const ConvArgs &a, int wr, int bk, int bn);
+hipError_t launch_conv_patch(const ConvArgs &a, int wr, int bk, int bn, hipStream_t s);
 
 // CTC choice from the GEMM's per-tile partials: y[2m] = best, y[2m+1] = 1/sum.
 hipError_t launch_ctc_merge(const float *part, int rows, int ntiles, float *y, long y_lane_stride,

@@ -79,6 +79,7 @@ struct Step {
   int fc1 = -1, fc2 = -1;  // squeeze-and-excite 1x1 layers after a Mean
   int head2 = -1;          // the narrow transposed convolution folded into S_HEAD
   bool dw_sums = false;    // S_DW: also sum its output per channel for the next step's mean
+  bool patch = false;      // S_GEMM: a windowed convolution on halo tiles (conv_patch)
   int mean_of_dw = -1;     // S_MEAN: the depthwise operation whose sums it joins
   int elt = 0;             // EltMode
   std::vector<Source> sources;
@@ -462,9 +463,42 @@ bool Model::pack(std::string &err) {
         if (waste < best_waste - 1e-12) best = cand, best_waste = waste;
       }
       bk = best;
+      // A windowed convolution over 48 channels in all, or over 96 on a small
+      // map: one chunk per tap, fewer load round trips in sequence (a large
+      // map keeps chunks of 32: more waves per CU hide the loads better).
+      bool shifted = false;
+      for (auto &x : srcs) shifted = shifted || x.shift > 0;
+      const size_t out_px = op.oh * op.ow;
+      if (s.kind == S_GEMM && op.kind == K_CONV && !pw && !shifted &&
+          (ctot == 48 || (ctot == 96 && out_px < 16384)))
+        bk = ctot;
       // The CTC head has thousands of tiles and is throughput-bound: small
       // chunks keep the LDS footprint small and the occupancy high.
       if (s.kind == S_CTC) bk = 8;
+      // A windowed convolution up to 3 x 3, stride 1 or 2, over upsampled
+      // sources: halo tiles (each source pixel decoded once per channel
+      // block, not once per tap), whose channel block (the chunk) is at most
+      // 32 and small enough that the patch and the block's weights fit in LDS.
+      if (s.kind == S_GEMM && op.kind == K_CONV && !pw && op.kh <= 3 && op.kw <= 3 && op.sh == op.sw &&
+          (op.sh == 1 || op.sh == 2) && shifted) {
+        const int bn0 = N <= 16 ? 16 : (N <= 32 ? 32 : 64);
+        auto lds = [&](int b) {
+          const size_t pr = 7 * op.sh + op.kh, pc = 15 * op.sw + op.kw;
+          return (pr * pc + size_t(bn0) * taps) * size_t(b + 4) * sizeof(float);
+        };
+        int pb = 0;
+        double pw_best = 1e9;
+        for (int cand : {32, 16, 8}) {
+          if (lds(cand) > 160 * 1024) continue;
+          double waste = double((ctot + cand - 1) / cand * cand) / ctot - 1.0;
+          if (waste <= 0.125) {
+            pb = cand;
+            break;
+          }
+          if (waste < pw_best - 1e-12) pb = cand, pw_best = waste;
+        }
+        if (pb) s.patch = true, bk = pb;
+      }
       cpt = (ctot + bk - 1) / bk;
       s.chunks = taps * cpt;
     } else {
@@ -474,7 +508,7 @@ bool Model::pack(std::string &err) {
     }
     int bn = N <= 16 ? 16 : (N <= 32 ? 32 : 64);
     if (s.kind == S_CTC) bn = 64;
-    int wm = bk == 64 ? 16 : 32;
+    int wm = bk >= 48 ? 16 : 32;
     s.tile = GemmTile{wm, bn, bk, vec, pw};
     if (!gemm_tile_supported(s.tile) && s.kind != S_CTC)
       return err = fmt("operation %d: no GEMM tile for this shape", s.op), false;
@@ -678,6 +712,17 @@ void Model::build_launches(Batch &b) {
         }
         a.y = Y, a.y_lane_stride = ys;
         GemmTile t = s.tile;
+        if (s.patch) {
+          // Tiles of 8 rows when there are enough of them, else of 4.
+          const long ntn = (a.n + t.bn - 1) / t.bn;
+          const long tiles8 = long(L) * ((a.oh + 7) / 8) * ((a.ow + 15) / 16) * ntn;
+          const int wr = tiles8 >= 512 ? 2 : 1;
+          const int bk = t.bk, bn = t.bn;
+          b.launches.push_back({"conv_patch", s.op, [a, wr, bk, bn](hipStream_t st) {
+                                  return launch_conv_patch(a, wr, bk, bn, st);
+                                }});
+          break;
+        }
         long M = long(L) * a.oh * a.ow;
         long tiles = (M + 127) / 128 * ((a.n + t.bn - 1) / t.bn);
         // Fewer than four tiles per CU of 128 rows: take 64-row tiles.

@@ -79,12 +79,52 @@ def test_pointwise_gemm(oracle, ci, co):
                                            ((3, 3), (1, 1), (1, 1, 1, 1), 96, 24),
                                            ((2, 2), (1, 1), (0, 1, 0, 1), 24, 12),
                                            ((1, 3), (1, 1), (0, 0, 1, 1), 40, 60),
-                                           ((3, 3), (2, 1), (1, 1, 1, 1), 7, 33)])
+                                           ((3, 3), (2, 1), (1, 1, 1, 1), 7, 33),
+                                           ((3, 3), (1, 1), (1, 1, 1, 1), 10, 20)])
 def test_windowed_gemm(oracle, k, s, pad, ci, co):
     w = RNG.normal(0, 1 / np.sqrt(ci * k[0] * k[1]), (k[0], k[1], ci, co)).astype(np.float32)
     bias = RNG.normal(0, 0.3, co).astype(np.float32)
     got, want = both(lambda b, t: b.conv(t, w, bias, k=k, s=s, pad=pad, fused="swish"),
                      (15, 18, ci), oracle)
+    near(got, want)
+
+
+@pytest.mark.parametrize("k,s,ci,co,hw,lanes", [
+    (3, 1, 96, 24, (30, 40), 3),     # the neck's 3 x 3: 8-row tiles? no, 4-row
+    (3, 1, 96, 24, (256, 256), 1),   # 512 tiles of 8 rows
+    (3, 2, 48, 32, (33, 50), 2),     # stride 2, two sources below
+    (2, 1, 24, 12, (37, 29), 2),     # the stem's 2 x 2
+    (3, 1, 20, 96, (17, 35), 2),     # two column tiles of 64, channel block 16 + 4 padding
+    (1, 3, 40, 60, (9, 70), 2),
+    (3, 1, 32, 32, (20, 24), 2),     # residual add folded into the epilogue
+])
+def test_patch_conv(oracle, k, s, ci, co, hw, lanes):
+    # Windowed convolutions on halo tiles: two sources (the second input of
+    # a two-input conv), a residual add folded into the epilogue, and a
+    # channel gate folded into the first source.
+    kh, kw = (k, k) if k != 1 else (1, 3)
+    half = ci // 2 if ci % 8 == 0 else 0
+    w = RNG.normal(0, 1 / np.sqrt(ci * kh * kw), (kh, kw, ci, co)).astype(np.float32)
+    bias = RNG.normal(0, 0.3, co).astype(np.float32)
+    g = RNG.uniform(0.5, 1.5, (1, 1, ci - half if half else ci)).astype(np.float32)
+    pad = (kh // 2, (kh - 1) // 2, kw // 2, (kw - 1) // 2) if kh != 2 else (0, 1, 0, 1)
+    wg1 = RNG.normal(0, 0.3, (1, 1, ci - half if half else ci, 4)).astype(np.float32)
+    wg2 = RNG.normal(0, 0.3, (1, 1, 4, ci - half if half else ci)).astype(np.float32)
+
+    def build(b, t):
+        if half:
+            x1 = b.conv(t, RNG.normal(0, 0.3, (1, 1, ci, ci - half)).astype(np.float32), None)
+            x2 = b.conv(t, RNG.normal(0, 0.3, (1, 1, ci, half)).astype(np.float32), None)
+        else:
+            x1, x2 = t, None
+        m = b.mean(x1)
+        gate = b.conv(b.conv(m, wg1, None, fused="relu"), wg2, None, fused="hardsigmoid")
+        y = b.conv(b.channelmul(x1, gate), w, bias, k=(kh, kw), s=(s, s), pad=pad, fused="hardswish", x2=x2)
+        if s == 1 and co == ci and kh != 2:
+            y = b.add(y, t)
+        return y
+
+    got, want = both(build, (*hw, ci), oracle, lanes=lanes)
     near(got, want)
 
 
