@@ -26,6 +26,13 @@ ROOT = Path(__file__).resolve().parent
 PEAK_HBM_GBS = 8000.0
 PEAK_FP32_MFMA_TFLOPS = 157.3
 GEMM_LAUNCHES = {"pointwise_gemm", "conv_gemm", "conv_patch", "convt_gemm", "ctc_gemm"}
+# HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE,
+# scaled by a plain copy kernel's counters (x2.0 / x1.0), for the launches
+# the bench reports a roofline of: (kernel, plan operation) -> (read, write)
+# KiB and the profile summary the numbers come from.
+MEASURED_TRAFFIC = {
+    ("conv_patch", 94): (14830, 5400, "profiles/conv_patch_240x240_4src_96to24_hbm_counters.md"),
+}
 
 
 def package():
@@ -351,7 +358,11 @@ def main() -> int:
         "eager_ms_per_step": round(det_eager, 4),
         "with_host_copies_img_per_s": round(1e3 / pcie_ms, 2),
     }
-    result["roofline"]["traffic"] = None
+    measured = MEASURED_TRAFFIC.get((dom["name"], dom["op"]))
+    result["roofline"]["traffic"] = (measured[0] + measured[1]) * 1024 if measured else None
+    if measured:
+        result["roofline"]["traffic_source"] = measured[2]
+        result["roofline"]["algorithmic_bytes"] = round(dom["bytes"])
     result["roofline"]["kernel"] = f"{dom['name']} (op {dom['op']})"
     result["roofline"]["launch_ms"] = round(dom["ms"], 5)
     result["det_kernels"] = by_kernel(det_rows)
