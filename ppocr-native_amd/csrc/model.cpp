@@ -93,6 +93,12 @@ struct Launch {
   std::string name;
   int op;
   std::function<hipError_t(hipStream_t)> fn;
+  // Launches of the same batch this one must follow: those that write what
+  // it reads or reads what it writes (memory homes are reused, so an earlier
+  // reader of a home must finish before a later writer), and the previous
+  // launch of its own step.
+  std::vector<int> deps;
+  int step = -1;
   // Algorithmic work of the launch: floating-point operations of the layer,
   // and bytes it must move (each input and the weights read once, each
   // output written once), for roofline fractions.
@@ -107,6 +113,8 @@ struct Batch {
   std::vector<size_t> home;   // plan buffer -> home, or SIZE_MAX
   std::vector<size_t> home_floats, home_off;
   size_t ws_off = 0;          // workspace in the arena, floats
+  std::vector<size_t> step_ws;  // each step's own workspace, floats past ws_off
+  std::vector<hipEvent_t> done; // per launch: recorded when another stream waits for it
   float *arena = nullptr;
   size_t arena_floats = 0;
   float *host_in = nullptr;   // pinned, lanes * in_len
@@ -117,6 +125,7 @@ struct Batch {
   std::vector<Launch> launches;
 
   float *dev(size_t slot) const { return arena + home_off[home[slot]]; }
+  float *ws(size_t step) const { return arena + ws_off + step_ws[step]; }
   long stride(size_t slot) const { return long(home_floats[home[slot]]); }
 };
 
@@ -127,6 +136,17 @@ struct Model {
   std::string name;
   int integrated = 0;
   hipStream_t stream = nullptr;
+  // Extra streams (default priority) for launches that do not depend on
+  // each other: the fork/join points are events, so a run is still one
+  // stream's work to the caller (and one graph when captured).
+  static constexpr int kSide = 3;
+  // Whether independent launches run on the side streams (and homes are
+  // reused only where that adds no ordering). Off: a run with them ended in
+  // a host crash on the 960 x 960 detector whose cause is not found yet;
+  // every launch then goes on `stream` in plan order.
+  static constexpr bool kConcurrent = false;
+  hipStream_t side[kSide] = {};
+  hipEvent_t fork = nullptr, join[kSide] = {};
   Plan plan;
   std::vector<float> weights;     // host copy of the plan's weights
   float *dweights = nullptr;      // the plan's weights on the device
@@ -147,6 +167,8 @@ struct Model {
   ~Model();
   void drop_graph();
   bool enqueue(std::string &err);
+  bool launch_all(std::string &err);
+  void link(Batch &b) const;
   bool load(const uint8_t *bytes, size_t len, std::string &err);
   bool build_steps(std::string &err);
   bool pack(std::string &err);
@@ -163,6 +185,8 @@ Model::~Model() {
   if (stream) hipStreamSynchronize(stream);
   drop_graph();
   for (auto &b : batches) {
+    for (hipEvent_t e : b->done)
+      if (e) hipEventDestroy(e);
     if (b->arena) hipFree(b->arena);
     if (b->host_in) hipHostFree(b->host_in);
     for (float *p : b->host_out)
@@ -170,6 +194,11 @@ Model::~Model() {
   }
   if (dweights) hipFree(dweights);
   if (dpacked) hipFree(dpacked);
+  for (int k = 0; k < kSide; k++) {
+    if (side[k]) hipStreamSynchronize(side[k]), hipStreamDestroy(side[k]);
+    if (join[k]) hipEventDestroy(join[k]);
+  }
+  if (fork) hipEventDestroy(fork);
   if (stream) hipStreamDestroy(stream);
 }
 
@@ -551,6 +580,11 @@ bool Model::load(const uint8_t *bytes, size_t len, std::string &err) {
   if (name.empty()) name = prop.gcnArchName;
   integrated = prop.integrated;
   HIPTRY(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking), "creating a stream");
+  for (int k = 0; k < kSide; k++) {
+    HIPTRY(hipStreamCreateWithFlags(&side[k], hipStreamNonBlocking), "creating a stream");
+    HIPTRY(hipEventCreateWithFlags(&join[k], hipEventDisableTiming), "creating an event");
+  }
+  HIPTRY(hipEventCreateWithFlags(&fork, hipEventDisableTiming), "creating an event");
   HIPTRY(hipMalloc(&dweights, std::max<size_t>(weights.size(), 1) * sizeof(float)),
          "allocating the weights");
   if (!weights.empty())
@@ -572,32 +606,64 @@ bool Model::arrange(Batch &b, std::string &err) {
     for (size_t s : step_reads(steps[i])) last[s] = i;
   for (size_t s : p.out_slot) last[s] = SIZE_MAX;
   b.home.assign(p.pool.size(), SIZE_MAX);
+  // Steps each step depends on through the data, transitively (the
+  // launches' RAW edges). A freed home is reused only by a step that already
+  // follows every reader of the home's last buffer: reuse then adds no
+  // ordering the data does not, and independent steps stay independent.
+  const size_t n = steps.size();
+  std::vector<size_t> producer(p.pool.size(), SIZE_MAX);
+  std::vector<std::vector<size_t>> slot_readers(p.pool.size());
+  for (size_t i = 0; i < n; i++) {
+    producer[step_writes(steps[i])] = i;
+    for (size_t sl : step_reads(steps[i])) slot_readers[sl].push_back(i);
+  }
+  std::vector<std::vector<bool>> anc(n, std::vector<bool>(n, false));
+  for (size_t i = 0; i < n; i++)
+    for (size_t sl : step_reads(steps[i])) {
+      const size_t w = producer[sl];
+      if (w == SIZE_MAX || w >= i) continue;
+      anc[i][w] = true;
+      for (size_t k = 0; k < w; k++)
+        if (anc[w][k]) anc[i][k] = true;
+    }
   std::vector<size_t> sizes, freel;
-  // The smallest free home that holds n floats, else the largest grown.
-  auto place = [&](size_t n) {
-    n = round_up(std::max<size_t>(n, 1), 64);
+  std::vector<std::vector<size_t>> held_by;  // per home: the readers of its last buffer
+  // For step i: the smallest free home it may take that holds n floats,
+  // else the largest it may take, grown; else a new home.
+  auto place = [&](size_t need, size_t i) {
+    need = round_up(std::max<size_t>(need, 1), 64);
+    auto allowed = [&](size_t h) {
+      if (!kConcurrent) return true;
+      for (size_t r : held_by[h])
+        if (i == SIZE_MAX || !anc[i][r]) return false;
+      return true;
+    };
     int best = -1;
     for (size_t k = 0; k < freel.size(); k++)
-      if (sizes[freel[k]] >= n && (best < 0 || sizes[freel[k]] < sizes[freel[best]])) best = int(k);
+      if (allowed(freel[k]) && sizes[freel[k]] >= need && (best < 0 || sizes[freel[k]] < sizes[freel[best]]))
+        best = int(k);
     if (best < 0)
       for (size_t k = 0; k < freel.size(); k++)
-        if (best < 0 || sizes[freel[k]] > sizes[freel[best]]) best = int(k);
+        if (allowed(freel[k]) && (best < 0 || sizes[freel[k]] > sizes[freel[best]])) best = int(k);
     if (best >= 0) {
       size_t h = freel[best];
       freel.erase(freel.begin() + best);
-      sizes[h] = std::max(sizes[h], n);
+      sizes[h] = std::max(sizes[h], need);
       return h;
     }
-    sizes.push_back(n);
+    sizes.push_back(need);
+    held_by.emplace_back();
     return sizes.size() - 1;
   };
-  b.home[p.in_slot] = place(p.pool[p.in_slot]);
-  for (size_t i = 0; i < steps.size(); i++) {
+  b.home[p.in_slot] = place(p.pool[p.in_slot], SIZE_MAX);
+  for (size_t i = 0; i < n; i++) {
     size_t y = step_writes(steps[i]);
-    b.home[y] = place(p.pool[y]);
-    for (size_t s : step_reads(steps[i]))
-      if (last[s] == i && std::find(freel.begin(), freel.end(), b.home[s]) == freel.end())
-        freel.push_back(b.home[s]);
+    b.home[y] = place(p.pool[y], i);
+    for (size_t sl : step_reads(steps[i]))
+      if (last[sl] == i && std::find(freel.begin(), freel.end(), b.home[sl]) == freel.end()) {
+        freel.push_back(b.home[sl]);
+        held_by[b.home[sl]] = slot_readers[sl];
+      }
   }
   b.home_floats = sizes;
   b.home_off.resize(sizes.size());
@@ -606,20 +672,26 @@ bool Model::arrange(Batch &b, std::string &err) {
     b.home_off[h] = off;
     off += round_up(sizes[h] * L, 64);
   }
-  // Workspace: channel-mean partials (f64) and CTC tile partials.
+  // Workspace: channel-mean partials (f64), CTC tile partials, attention
+  // scores; each step its own region, so that steps which do not depend on
+  // each other can run at the same time.
   size_t ws = 0;
-  for (const Step &s : steps) {
+  b.step_ws.assign(steps.size(), 0);
+  for (size_t i = 0; i < steps.size(); i++) {
+    const Step &s = steps[i];
     const Op &op = p.ops[s.op];
+    size_t need = 0;
     if (s.kind == S_MEAN && s.mean_of_dw >= 0)
-      ws = std::max(ws, 2 * L * size_t(dw_mean_blocks(dw_shape(p.ops[s.mean_of_dw]))) * op.ic);
+      need = 2 * L * size_t(dw_mean_blocks(dw_shape(p.ops[s.mean_of_dw]))) * op.ic;
     else if (s.kind == S_MEAN)
-      ws = std::max(ws, 2 * mean_partial_doubles(int(op.ih * op.iw), int(op.ic), int(L)));
+      need = 2 * mean_partial_doubles(int(op.ih * op.iw), int(op.ic), int(L));
     if (s.kind == S_CTC) {
       size_t ntn = (s.gemm_n + s.tile.bn - 1) / s.tile.bn;
-      ws = std::max(ws, L * op.iw * ntn * 4);
+      need = L * op.iw * ntn * 4;
     }
-    if (s.kind == S_ATTN)
-      ws = std::max(ws, attention_scratch_floats(int(op.iw), int(op.oc), int(op.n2), int(L)));
+    if (s.kind == S_ATTN) need = attention_scratch_floats(int(op.iw), int(op.oc), int(op.n2), int(L));
+    b.step_ws[i] = ws;
+    ws += round_up(need, 64);
   }
   b.ws_off = off;
   off += round_up(std::max<size_t>(ws, 64), 64);
@@ -665,7 +737,9 @@ void Model::build_launches(Batch &b) {
   const Plan &p = b.plan;
   const int L = int(b.lanes.size());
   const float *W = dweights;
-  for (const Step &s : steps) {
+  for (size_t si = 0; si < steps.size(); si++) {
+    const Step &s = steps[si];
+    const size_t first_launch = b.launches.size();
     const Op &op = p.ops[s.op];
     const size_t y = step_writes(s);
     float *Y = b.dev(y);
@@ -747,7 +821,7 @@ void Model::build_launches(Batch &b) {
         a.bias = W + op.b0;
         a.mode = GEMM_CTC;
         a.vocab = int(op.n2);
-        float *part = b.arena + b.ws_off;
+        float *part = b.ws(si);
         a.part = part;
         a.y = Y, a.y_lane_stride = ys;
         GemmTile t = s.tile;
@@ -763,7 +837,8 @@ void Model::build_launches(Batch &b) {
         DwArgs a{L, int(op.ih), int(op.iw), int(op.oc), int(op.oh), int(op.ow), int(op.kh), int(op.kw),
                  int(op.sh), int(op.sw), int(op.pt), int(op.pl), b.dev(op.x), b.stride(op.x), W + op.w0,
                  bias, op.fused, Y, ys, nullptr};
-        if (s.dw_sums) a.mean_part = reinterpret_cast<double *>(b.arena + b.ws_off);
+        // The sums go to the workspace of the mean step that follows.
+        if (s.dw_sums) a.mean_part = reinterpret_cast<double *>(b.ws(si + 1));
         b.launches.push_back({"dwconv", s.op, [a](hipStream_t st) { return launch_dwconv(a, st); }});
         break;
       }
@@ -817,7 +892,7 @@ void Model::build_launches(Batch &b) {
         const float *x = b.dev(op.x);
         long xs = b.stride(op.x);
         int pixels = int(op.ih * op.iw), c = int(op.ic);
-        double *part = reinterpret_cast<double *>(b.arena + b.ws_off);
+        double *part = reinterpret_cast<double *>(b.ws(si));
         bool se = s.fc1 >= 0;
         SeArgs sa{};
         if (se) {
@@ -856,7 +931,7 @@ void Model::build_launches(Batch &b) {
         long xs = b.stride(op.x);
         float scale = weights[op.w0];
         int t = int(op.iw), c = int(op.oc), heads = int(op.n2);
-        float *scratch = b.arena + b.ws_off;
+        float *scratch = b.ws(si);
         b.launches.push_back({"attention", s.op, [=](hipStream_t st) {
                                 return launch_attention(x, xs, scale, t, c, heads, L, Y, ys, scratch, st);
                               }});
@@ -900,7 +975,53 @@ void Model::build_launches(Batch &b) {
         break;
       }
     }
+    for (size_t k = first_launch; k < b.launches.size(); k++) b.launches[k].step = int(si);
   }
+  link(b);
+}
+
+// The dependencies between a batch's launches, from the memory each step
+// reads and writes: its inputs' and output's homes (a home holds different
+// buffers over a run, so a later writer waits for the earlier readers) and
+// its own workspace region. A launch also follows the previous launch of its
+// step. Independent launches may then run on different streams.
+void Model::link(Batch &b) const {
+  const size_t H = b.home_floats.size();
+  const size_t R = H + steps.size();
+  std::vector<int> writer(R, -1);
+  std::vector<std::vector<int>> readers(R);
+  for (hipEvent_t e : b.done)
+    if (e) hipEventDestroy(e);
+  b.done.assign(b.launches.size(), nullptr);
+  for (size_t j = 0; j < b.launches.size(); j++) {
+    Launch &l = b.launches[j];
+    const Step &s = steps[size_t(l.step)];
+    std::vector<size_t> rd, wr;
+    for (size_t slot : step_reads(s)) rd.push_back(b.home[slot]);
+    wr.push_back(b.home[step_writes(s)]);
+    const size_t ws = H + size_t(l.step);
+    if (s.kind == S_MEAN || s.kind == S_CTC || s.kind == S_ATTN) rd.push_back(ws), wr.push_back(ws);
+    if (s.kind == S_DW && s.dw_sums) wr.push_back(ws + 1);  // the next step's partial sums
+    std::vector<int> deps;
+    if (j > 0 && b.launches[j - 1].step == l.step) deps.push_back(int(j - 1));
+    for (size_t r : rd)
+      if (writer[r] >= 0) deps.push_back(writer[r]);
+    for (size_t w : wr) {
+      if (writer[w] >= 0) deps.push_back(writer[w]);
+      deps.insert(deps.end(), readers[w].begin(), readers[w].end());
+    }
+    std::sort(deps.begin(), deps.end());
+    deps.erase(std::unique(deps.begin(), deps.end()), deps.end());
+    deps.erase(std::remove(deps.begin(), deps.end(), int(j)), deps.end());
+    l.deps = deps;
+    for (size_t r : rd) readers[r].push_back(int(j));
+    for (size_t w : wr) writer[w] = int(j), readers[w].clear();
+  }
+  // An event for each launch some other launch waits for.
+  if (!kConcurrent) return;
+  for (const Launch &l : b.launches)
+    for (int d : l.deps)
+      if (!b.done[size_t(d)]) hipEventCreateWithFlags(&b.done[size_t(d)], hipEventDisableTiming);
 }
 
 // Each launch's algorithmic work, in the order build_launches made them.
@@ -1058,8 +1179,8 @@ void Model::drop_graph() {
 bool Model::enqueue(std::string &err) {
   if (use_graphs && !graph_exec && eager_runs >= 1) {
     bool ok = hipStreamBeginCapture(stream, hipStreamCaptureModeRelaxed) == hipSuccess;
-    for (size_t g = 0; ok && g < active_batches; g++)
-      for (const Launch &l : batches[g]->launches) ok = ok && l.fn(stream) == hipSuccess;
+    std::string ignored;
+    ok = ok && launch_all(ignored);
     hipGraph_t captured = nullptr;
     hipError_t end = hipStreamEndCapture(stream, &captured);
     ok = ok && end == hipSuccess && captured;
@@ -1076,14 +1197,70 @@ bool Model::enqueue(std::string &err) {
     HIPTRY(hipGraphLaunch(graph_exec, stream), "launching the run's graph");
     return true;
   }
+  if (!launch_all(err)) return false;
+  eager_runs++;
+  return true;
+}
+
+// Every launch of the active batches: each on the stream of the dependency
+// it continues when it can, else on the stream idle longest; it waits for
+// its dependencies on other streams by their events. The side streams start
+// after the model stream's earlier work (the input copy) and the model
+// stream waits for all of them at the end, so a run is ordered like one
+// stream's work.
+bool Model::launch_all(std::string &err) {
+  if (!kConcurrent) {
+    for (size_t g = 0; g < active_batches; g++)
+      for (const Launch &l : batches[g]->launches) {
+        hipError_t e = l.fn(stream);
+        if (e != hipSuccess)
+          return err = fmt("launching %s (operation %d): %s", l.name.c_str(), l.op, hipGetErrorString(e)), false;
+      }
+    return true;
+  }
+  hipStream_t S[1 + kSide] = {stream};
+  for (int k = 0; k < kSide; k++) S[1 + k] = side[k];
+  bool started[1 + kSide] = {true};
+  HIPTRY(hipEventRecord(fork, stream), "recording the run's start");
+  long last[1 + kSide];  // global index of the last launch on each stream
+  for (int k = 0; k <= kSide; k++) last[k] = -1 - k;
+  long global = 0;
   for (size_t g = 0; g < active_batches; g++) {
-    for (const Launch &l : batches[g]->launches) {
-      hipError_t e = l.fn(stream);
+    Batch &b = *batches[g];
+    const long base = global;
+    std::vector<int> where(b.launches.size(), 0);
+    for (size_t j = 0; j < b.launches.size(); j++, global++) {
+      const Launch &l = b.launches[j];
+      int st = -1;
+      if (!l.deps.empty()) {
+        const int d = l.deps.back();
+        if (last[where[size_t(d)]] == base + d) st = where[size_t(d)];
+      }
+      if (st < 0) {
+        st = 0;
+        for (int k = 1; k <= kSide; k++)
+          if (last[k] < last[st]) st = k;
+      }
+      if (!started[st]) {
+        HIPTRY(hipStreamWaitEvent(S[st], fork, 0), "ordering a stream after the run's start");
+        started[st] = true;
+      }
+      for (int d : l.deps)
+        if (where[size_t(d)] != st)
+          HIPTRY(hipStreamWaitEvent(S[st], b.done[size_t(d)], 0), "waiting for a dependency");
+      hipError_t e = l.fn(S[st]);
       if (e != hipSuccess)
         return err = fmt("launching %s (operation %d): %s", l.name.c_str(), l.op, hipGetErrorString(e)), false;
+      if (b.done[j]) HIPTRY(hipEventRecord(b.done[j], S[st]), "recording a launch");
+      where[j] = st;
+      last[st] = global;
     }
   }
-  eager_runs++;
+  for (int k = 0; k < kSide; k++)
+    if (started[1 + k]) {
+      HIPTRY(hipEventRecord(join[k], S[1 + k]), "recording a stream's end");
+      HIPTRY(hipStreamWaitEvent(stream, join[k], 0), "joining the streams");
+    }
   return true;
 }
 
