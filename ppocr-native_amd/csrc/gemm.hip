@@ -415,34 +415,44 @@ __global__ __launch_bounds__(256) void conv_patch(ConvArgs a, int tiles_x, int t
 #pragma unroll
     for (int j = 0; j < NT; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+  // Each thread stages one channel group q of every (256 / CQ)-th patch
+  // pixel, walking the pixels without divisions, and, for the weights, one
+  // or two (column, channel group) pairs across every tap.
+  constexpr int PSTEP = 256 / CQ;
+  const int q = tid % CQ, p0 = tid / CQ;
+  const int sy = PSTEP / PC, sx = PSTEP - sy * PC;
+  const int npx = PR * PC;
+  constexpr int PAIRS = BN * CQ;
   for (int cc = 0; cc < a.cpt; cc++) {
     if (cc) __syncthreads();  // the previous block's reads are done
-    // The patch: pixel-major, each pixel's CB channels (zero outside the
-    // image and past the last channel).
-    const int pe = PR * PC * CQ;
-    for (int e = tid; e < pe; e += 256) {
-      const int pix = e / CQ, q = e - pix * CQ;
-      const int py = pix / PC, px = pix - py * PC;
-      const int iy = iy0 + py, ix = ix0 + px, c = cc * CB + q * 4;
-      f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
-      if (c < a.ctot && iy >= 0 && iy < a.ih && ix >= 0 && ix < a.iw) {
-        const ConvSrc src = pick_src(a, c);
-        const int cl = c - src.coff;
-        const long at = (long)(iy >> src.shift) * (a.iw >> src.shift) + (ix >> src.shift);
-        v = *reinterpret_cast<const f32x4 *>(src.p + (long)ln * src.lane_stride + at * src.c + cl);
-        if (a.gate && src.coff == 0)
-          v = v * *reinterpret_cast<const f32x4 *>(a.gate + (long)ln * a.gate_lane_stride + cl);
+    {
+      const int c = cc * CB + q * 4;
+      const bool live_c = c < a.ctot;
+      const ConvSrc src = pick_src(a, live_c ? c : 0);
+      const int cl = c - src.coff, sh = src.shift, sw_ = a.iw >> sh;
+      const float *base = src.p + (long)ln * src.lane_stride + cl;
+      const float *gbase = a.gate && src.coff == 0 ? a.gate + (long)ln * a.gate_lane_stride + cl : nullptr;
+      const f32x4 g = gbase ? *reinterpret_cast<const f32x4 *>(gbase) : f32x4{1.f, 1.f, 1.f, 1.f};
+      int py = p0 / PC, px = p0 - (p0 / PC) * PC;
+      for (int pix = p0; pix < npx; pix += PSTEP) {
+        const int iy = iy0 + py, ix = ix0 + px;
+        f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (live_c && iy >= 0 && iy < a.ih && ix >= 0 && ix < a.iw) {
+          v = *reinterpret_cast<const f32x4 *>(base + ((long)(iy >> sh) * sw_ + (ix >> sh)) * src.c);
+          if (gbase) v = v * g;
+        }
+        *reinterpret_cast<f32x4 *>(P + pix * S + q * 4) = v;
+        px += sx, py += sy;
+        if (px >= PC) px -= PC, py++;
       }
-      *reinterpret_cast<f32x4 *>(P + pix * S + q * 4) = v;
     }
-    // The block's weights: for each output column and tap, CB values.
-    const int be = BN * taps * CQ;
-    for (int e = tid; e < be; e += 256) {
-      const int n = e / (taps * CQ), r = e - n * (taps * CQ);
-      const int tp = r / CQ, q = r - tp * CQ;
-      const f32x4 w = *reinterpret_cast<const f32x4 *>(a.wt + (long)(n0 + n) * a.wt_k +
-                                                      (long)(tp * a.cpt + cc) * CB + q * 4);
-      *reinterpret_cast<f32x4 *>(Bs + (n * taps + tp) * S + q * 4) = w;
+    for (int pr = tid; pr < PAIRS; pr += 256) {
+      const int n = pr / CQ, qq = pr - n * CQ;
+      const float *wsrc = a.wt + (long)(n0 + n) * a.wt_k + (long)cc * CB + qq * 4;
+      float *wdst = Bs + n * taps * S + qq * 4;
+      const long wstep = (long)a.cpt * CB;
+      for (int tp = 0; tp < taps; tp++)
+        *reinterpret_cast<f32x4 *>(wdst + tp * S) = *reinterpret_cast<const f32x4 *>(wsrc + tp * wstep);
     }
     __syncthreads();
     for (int tp = 0; tp < taps; tp++) {
