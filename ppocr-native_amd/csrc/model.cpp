@@ -504,12 +504,16 @@ bool Model::pack(std::string &err) {
       // The CTC head has thousands of tiles and is throughput-bound: small
       // chunks keep the LDS footprint small and the occupancy high.
       if (s.kind == S_CTC) bk = 8;
-      // A windowed convolution up to 3 x 3, stride 1 or 2, over upsampled
-      // sources: halo tiles (each source pixel decoded once per channel
-      // block, not once per tap), whose channel block (the chunk) is at most
-      // 32 and small enough that the patch and the block's weights fit in LDS.
+      // A windowed convolution up to 3 x 3, stride 1 or 2: halo tiles (each
+      // source pixel decoded once per channel block, not once per tap), whose
+      // channel block (the chunk) is at most 32 and small enough that the
+      // patch and the block's weights fit in LDS.
+      // Measured on the detector: halo tiles win over upsampled sources, on
+      // maps under 128 x 128 and over few channels; the implicit GEMM keeps
+      // large maps of many channels.
+      const bool halo = shifted || out_px < 16384 || ctot < 16;
       if (s.kind == S_GEMM && op.kind == K_CONV && !pw && op.kh <= 3 && op.kw <= 3 && op.sh == op.sw &&
-          (op.sh == 1 || op.sh == 2) && shifted) {
+          (op.sh == 1 || op.sh == 2) && halo) {
         const int bn0 = N <= 16 ? 16 : (N <= 32 ? 32 : 64);
         auto lds = [&](int b) {
           const size_t pr = 7 * op.sh + op.kh, pc = 15 * op.sw + op.kw;
