@@ -381,6 +381,12 @@ __global__ __launch_bounds__(256) void conv_mfma(ConvArgs a) {
 // order is channel block, tap, channel; bias, activation, residual and the
 // second activation as in conv_mfma's epilogue. Wave w owns output rows
 // w * WR .. w * WR + WR - 1 of the tile, one 16 x 16 MFMA row block each.
+// Registers a thread of conv_patch holds for the next channel block: patch
+// float4s (its channel group of every 256 / (CB / 4)-th pixel) and weight
+// float4s (taps x its column pairs).
+constexpr int kPatchPer = 6;
+constexpr int kWeightPer = 9;
+
 template <int WR, int BN, int CB>
 __global__ __launch_bounds__(256) void conv_patch(ConvArgs a, int tiles_x, int tiles_y) {
   constexpr int S = CB + 4;        // LDS row of one pixel / one (n, tap)
@@ -416,45 +422,71 @@ __global__ __launch_bounds__(256) void conv_patch(ConvArgs a, int tiles_x, int t
     for (int j = 0; j < NT; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   // Each thread stages one channel group q of every (256 / CQ)-th patch
-  // pixel, walking the pixels without divisions, and, for the weights, one
-  // or two (column, channel group) pairs across every tap.
+  // pixel (at most kPatchPer of them), walking the pixels without divisions,
+  // and one or two (column, channel group) pairs of the weights across every
+  // tap (at most kWeightPer float4). The next channel block's values are
+  // fetched into registers while this block's MFMAs run, then stored to LDS
+  // once every wave is done reading it.
   constexpr int PSTEP = 256 / CQ;
   const int q = tid % CQ, p0 = tid / CQ;
   const int sy = PSTEP / PC, sx = PSTEP - sy * PC;
   const int npx = PR * PC;
   constexpr int PAIRS = BN * CQ;
-  for (int cc = 0; cc < a.cpt; cc++) {
-    if (cc) __syncthreads();  // the previous block's reads are done
-    {
-      const int c = cc * CB + q * 4;
-      const bool live_c = c < a.ctot;
-      const ConvSrc src = pick_src(a, live_c ? c : 0);
-      const int cl = c - src.coff, sh = src.shift, sw_ = a.iw >> sh;
-      const float *base = src.p + (long)ln * src.lane_stride + cl;
-      const float *gbase = a.gate && src.coff == 0 ? a.gate + (long)ln * a.gate_lane_stride + cl : nullptr;
-      const f32x4 g = gbase ? *reinterpret_cast<const f32x4 *>(gbase) : f32x4{1.f, 1.f, 1.f, 1.f};
-      int py = p0 / PC, px = p0 - (p0 / PC) * PC;
-      for (int pix = p0; pix < npx; pix += PSTEP) {
-        const int iy = iy0 + py, ix = ix0 + px;
-        f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
-        if (live_c && iy >= 0 && iy < a.ih && ix >= 0 && ix < a.iw) {
-          v = *reinterpret_cast<const f32x4 *>(base + ((long)(iy >> sh) * sw_ + (ix >> sh)) * src.c);
-          if (gbase) v = v * g;
-        }
-        *reinterpret_cast<f32x4 *>(P + pix * S + q * 4) = v;
-        px += sx, py += sy;
-        if (px >= PC) px -= PC, py++;
+  constexpr int PPAIRS = (PAIRS + 255) / 256;
+  f32x4 rp[kPatchPer], rw[kWeightPer];
+  auto fetch = [&](int cc) {
+    const int c = cc * CB + q * 4;
+    const bool live_c = c < a.ctot;
+    const ConvSrc src = pick_src(a, live_c ? c : 0);
+    const int cl = c - src.coff, sh = src.shift, sw_ = a.iw >> sh;
+    const float *base = src.p + (long)ln * src.lane_stride + cl;
+    const bool gated = a.gate && src.coff == 0;
+    const f32x4 g = gated ? *reinterpret_cast<const f32x4 *>(a.gate + (long)ln * a.gate_lane_stride + cl)
+                          : f32x4{1.f, 1.f, 1.f, 1.f};
+    int py = p0 / PC, px = p0 - (p0 / PC) * PC;
+#pragma unroll
+    for (int k = 0; k < kPatchPer; k++) {
+      const int iy = iy0 + py, ix = ix0 + px;
+      f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (p0 + k * PSTEP < npx && live_c && iy >= 0 && iy < a.ih && ix >= 0 && ix < a.iw) {
+        v = *reinterpret_cast<const f32x4 *>(base + ((long)(iy >> sh) * sw_ + (ix >> sh)) * src.c);
+        if (gated) v = v * g;
       }
+      rp[k] = v;
+      px += sx, py += sy;
+      if (px >= PC) px -= PC, py++;
     }
-    for (int pr = tid; pr < PAIRS; pr += 256) {
+    const long wstep = (long)a.cpt * CB;
+#pragma unroll
+    for (int u = 0; u < PPAIRS; u++) {
+      const int pr = tid + 256 * u;
       const int n = pr / CQ, qq = pr - n * CQ;
-      const float *wsrc = a.wt + (long)(n0 + n) * a.wt_k + (long)cc * CB + qq * 4;
-      float *wdst = Bs + n * taps * S + qq * 4;
-      const long wstep = (long)a.cpt * CB;
-      for (int tp = 0; tp < taps; tp++)
-        *reinterpret_cast<f32x4 *>(wdst + tp * S) = *reinterpret_cast<const f32x4 *>(wsrc + tp * wstep);
+      const float *wsrc = a.wt + (long)(n0 + (pr < PAIRS ? n : 0)) * a.wt_k + (long)cc * CB + qq * 4;
+#pragma unroll
+      for (int tp = 0; tp < kWeightPer / PPAIRS; tp++)
+        if (pr < PAIRS && tp < taps) rw[u * (kWeightPer / PPAIRS) + tp] = *reinterpret_cast<const f32x4 *>(wsrc + tp * wstep);
     }
+  };
+  auto store = [&]() {
+#pragma unroll
+    for (int k = 0; k < kPatchPer; k++)
+      if (p0 + k * PSTEP < npx) *reinterpret_cast<f32x4 *>(P + (p0 + k * PSTEP) * S + q * 4) = rp[k];
+#pragma unroll
+    for (int u = 0; u < PPAIRS; u++) {
+      const int pr = tid + 256 * u;
+      const int n = pr / CQ, qq = pr - n * CQ;
+#pragma unroll
+      for (int tp = 0; tp < kWeightPer / PPAIRS; tp++)
+        if (pr < PAIRS && tp < taps)
+          *reinterpret_cast<f32x4 *>(Bs + (n * taps + tp) * S + qq * 4) = rw[u * (kWeightPer / PPAIRS) + tp];
+    }
+  };
+  fetch(0);
+  for (int cc = 0; cc < a.cpt; cc++) {
+    if (cc) __syncthreads();  // every wave is done with the previous block
+    store();
     __syncthreads();
+    if (cc + 1 < a.cpt) fetch(cc + 1);
     for (int tp = 0; tp < taps; tp++) {
       const int ky = tp / a.kw, kx = tp - ky * a.kw;
 #pragma unroll
@@ -609,13 +641,22 @@ hipError_t launch_conv(const ConvArgs &a, const GemmTile &t, hipStream_t s) {
   return hipErrorInvalidValue;
 }
 
-bool patch_supported(const ConvArgs &a, int bk, int bn) {
-  if (a.mode != GEMM_STORE || a.kh < 1 || a.kw < 1 || a.kh > 3 || a.kw > 3) return false;
-  if (a.sh != a.sw || (a.sh != 1 && a.sh != 2)) return false;
+bool patch_fits(int kh, int kw, int stride, int wr, int bk, int bn) {
+  if (kh < 1 || kw < 1 || kh > 3 || kw > 3 || (stride != 1 && stride != 2) || (wr != 1 && wr != 2)) return false;
   if ((bk != 8 && bk != 16 && bk != 32) || (bn != 16 && bn != 32 && bn != 64)) return false;
+  // What one thread holds for the next channel block must fit its registers.
+  const int cq = bk / 4, pstep = 256 / cq, pairs = (bn * cq + 255) / 256;
+  const int pr = (4 * wr - 1) * stride + kh, pc = 15 * stride + kw;
+  if ((pr * pc + pstep - 1) / pstep > kPatchPer) return false;
+  if (kWeightPer % pairs || kh * kw > kWeightPer / pairs) return false;
+  return size_t(pr * pc + bn * kh * kw) * (bk + 4) * sizeof(float) <= 160 * 1024;
+}
+
+bool patch_supported(const ConvArgs &a, int wr, int bk, int bn) {
+  if (a.mode != GEMM_STORE || a.sh != a.sw) return false;
   for (int k = 0; k < a.nsrc; k++)
     if (a.src[k].c % 4 || a.src[k].coff % 4) return false;
-  return patch_lds_bytes(a, 2, bk, bn) <= 160 * 1024;
+  return patch_fits(a.kh, a.kw, a.sh, wr, bk, bn);
 }
 
 size_t patch_lds_bytes(const ConvArgs &a, int wr, int bk, int bn) {
@@ -652,7 +693,7 @@ static hipError_t go_patch(const ConvArgs &a, hipStream_t s) {
   if (bn == 64) return go_patch<WR, 64, CB>(a, s);
 
 hipError_t launch_conv_patch(const ConvArgs &a, int wr, int bk, int bn, hipStream_t s) {
-  if (!patch_supported(a, bk, bn) || (wr != 1 && wr != 2)) return hipErrorInvalidValue;
+  if (!patch_supported(a, wr, bk, bn)) return hipErrorInvalidValue;
   if (wr == 2) {
     if (bk == 32) { PPOCR_PATCH(2, 32) }
     if (bk == 16) { PPOCR_PATCH(2, 16) }

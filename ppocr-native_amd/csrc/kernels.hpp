@@ -66,7 +66,8 @@ hipError_t launch_conv(const ConvArgs &a, const GemmTile &t, hipStream_t s);
 // The halo-tile windowed convolution (GEMM_STORE, kh, kw <= 3, stride 1 or
 // 2, channels a multiple of 4): output tiles 16 wide x 4 * wr rows, bn
 // columns, channel blocks of bk (the packed weights' chunk).
-bool patch_supported(const ConvArgs &a, int bk, int bn);
+bool patch_fits(int kh, int kw, int stride, int wr, int bk, int bn);
+bool patch_supported(const ConvArgs &a, int wr, int bk, int bn);
 size_t patch_lds_bytes(const ConvArgs &a, int wr, int bk, int bn);
 hipError_t launch_conv_patch(const ConvArgs &a, int wr, int bk, int bn, hipStream_t s);
 

@@ -515,14 +515,10 @@ bool Model::pack(std::string &err) {
       if (s.kind == S_GEMM && op.kind == K_CONV && !pw && op.kh <= 3 && op.kw <= 3 && op.sh == op.sw &&
           (op.sh == 1 || op.sh == 2) && halo) {
         const int bn0 = N <= 16 ? 16 : (N <= 32 ? 32 : 64);
-        auto lds = [&](int b) {
-          const size_t pr = 7 * op.sh + op.kh, pc = 15 * op.sw + op.kw;
-          return (pr * pc + size_t(bn0) * taps) * size_t(b + 4) * sizeof(float);
-        };
         int pb = 0;
         double pw_best = 1e9;
         for (int cand : {32, 16, 8}) {
-          if (lds(cand) > 160 * 1024) continue;
+          if (!patch_fits(int(op.kh), int(op.kw), int(op.sh), 1, cand, bn0)) continue;
           double waste = double((ctot + cand - 1) / cand * cand) / ctot - 1.0;
           if (waste <= 0.125) {
             pb = cand;
@@ -794,7 +790,7 @@ void Model::build_launches(Batch &b) {
           // Tiles of 8 rows when there are enough of them, else of 4.
           const long ntn = (a.n + t.bn - 1) / t.bn;
           const long tiles8 = long(L) * ((a.oh + 7) / 8) * ((a.ow + 15) / 16) * ntn;
-          const int wr = tiles8 >= 512 ? 2 : 1;
+          const int wr = tiles8 >= 512 && patch_fits(a.kh, a.kw, a.sh, 2, t.bk, t.bn) ? 2 : 1;
           const int bk = t.bk, bn = t.bn;
           b.launches.push_back({"conv_patch", s.op, [a, wr, bk, bn](hipStream_t st) {
                                   return launch_conv_patch(a, wr, bk, bn, st);
