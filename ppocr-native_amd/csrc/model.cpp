@@ -508,10 +508,9 @@ bool Model::pack(std::string &err) {
       // source pixel decoded once per channel block, not once per tap), whose
       // channel block (the chunk) is at most 32 and small enough that the
       // patch and the block's weights fit in LDS.
-      // Measured on the detector: halo tiles win over upsampled sources, on
-      // maps under 128 x 128 and over few channels; the implicit GEMM keeps
-      // large maps of many channels.
-      const bool halo = shifted || out_px < 16384 || ctot < 16;
+      // Measured on the detector: halo tiles win over upsampled sources and
+      // on maps under 128 x 128; the implicit GEMM keeps large maps.
+      const bool halo = shifted || out_px < 16384;
       if (s.kind == S_GEMM && op.kind == K_CONV && !pw && op.kh <= 3 && op.kw <= 3 && op.sh == op.sw &&
           (op.sh == 1 || op.sh == 2) && halo) {
         const int bn0 = N <= 16 ? 16 : (N <= 32 ? 32 : 64);
@@ -787,10 +786,11 @@ void Model::build_launches(Batch &b) {
         a.y = Y, a.y_lane_stride = ys;
         GemmTile t = s.tile;
         if (s.patch) {
-          // Tiles of 8 rows when there are enough of them, else of 4.
+          // Tiles of 8 rows (each wave two MFMA row blocks: half the LDS reads
+          // per MFMA) when there is about one per CU or more, else of 4.
           const long ntn = (a.n + t.bn - 1) / t.bn;
           const long tiles8 = long(L) * ((a.oh + 7) / 8) * ((a.ow + 15) / 16) * ntn;
-          const int wr = tiles8 >= 512 && patch_fits(a.kh, a.kw, a.sh, 2, t.bk, t.bn) ? 2 : 1;
+          const int wr = tiles8 >= 256 && patch_fits(a.kh, a.kw, a.sh, 2, t.bk, t.bn) ? 2 : 1;
           const int bk = t.bk, bn = t.bn;
           b.launches.push_back({"conv_patch", s.op, [a, wr, bk, bn](hipStream_t st) {
                                   return launch_conv_patch(a, wr, bk, bn, st);
