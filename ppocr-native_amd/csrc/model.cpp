@@ -510,7 +510,7 @@ bool Model::pack(std::string &err) {
       // patch and the block's weights fit in LDS.
       // Measured on the detector: halo tiles win over upsampled sources and
       // on maps under 128 x 128; the implicit GEMM keeps large maps.
-      const bool halo = shifted || out_px < 16384;
+      const bool halo = shifted || out_px < 16384 || (op.kh == 3 && op.sh == 1);
       if (s.kind == S_GEMM && op.kind == K_CONV && !pw && op.kh <= 3 && op.kw <= 3 && op.sh == op.sw &&
           (op.sh == 1 || op.sh == 2) && halo) {
         const int bn0 = N <= 16 ? 16 : (N <= 32 ? 32 : 64);
