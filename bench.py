@@ -31,7 +31,8 @@ GEMM_LAUNCHES = {"pointwise_gemm", "conv_gemm", "conv_patch", "convt_gemm", "ctc
 # the bench reports a roofline of: (kernel, plan operation) -> (read, write)
 # KiB and the profile summary the numbers come from.
 MEASURED_TRAFFIC = {
-    ("conv_patch", 94): (14830, 5400, "profiles/conv_patch_240x240_4src_96to24_hbm_counters.md"),
+    ("conv_patch", 83): (30830, 5400, "profiles/conv_patch_240x240_3x3_96to24_hbm_counters.md"),
+    ("conv_patch", 94): (12738, 5400, "profiles/conv_patch_240x240_3x3_96to24_hbm_counters.md"),
 }
 
 
