@@ -574,6 +574,372 @@ __global__ __launch_bounds__(256) void ctc_merge(const float4 *part, int rows, i
   }
 }
 
+// ------------------------------------------------------------ pointwise ring
+
+// A 1x1 convolution (one source, channels a multiple of 4, optional gate on
+// the input channels) as a GEMM whose operand tiles travel from global memory
+// straight into a ring of LDS stages (global_load_lds_dwordx4: no registers,
+// no store instructions), so that several chunks of BK channels are in
+// flight while the MFMAs run on the oldest one. On small maps the
+// register-staged kernel above waits out one load round trip per chunk; here
+// the round trips overlap.
+//
+// Tile: BM = 32 * MT rows (pixels) x BN = 32 * NT columns, four waves as a
+// 2 x 2 grid, each 16 * MT x 16 * NT. A stage holds the tile's A rows then
+// its B rows (the packed weights' rows), BK floats each, row-major, with the
+// 16-byte group g of row r stored at slot g ^ ring_swz(r) so that the
+// sixteen rows an MFMA fragment read touches land in distinct banks. A direct
+// load writes 64 lanes x 16 bytes contiguously from a wave-uniform LDS
+// address, so each lane loads whichever global group belongs at its slot.
+// Rows past the matrix and channels past ctot read kRingZeros. A GEMM of
+// fewer chunks than stages uses (and is given LDS for) only as many stages
+// as it has chunks.
+//
+// Reduction order: chunks of BK channels in order; within a chunk the MFMA
+// chain takes groups of four channels lane group by lane group. Bias,
+// activation, residual and second activation as in conv_mfma's epilogue.
+__device__ __attribute__((aligned(16))) float kRingZeros[4];
+
+static const size_t kMaxLdsBytes = 160 * 1024;
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+template <int BK>
+__device__ __forceinline__ int ring_swz(int row) {
+  if constexpr (BK == 32) return (row & 7) ^ ((row >> 3) & 1);
+  else return row & 15;
+}
+
+// Wait until at most n of this wave's vector memory operations are pending.
+template <int n>
+__device__ __forceinline__ void ring_wait() {
+  static_assert(n >= 0 && n < 64, "vmcnt holds 6 bits");
+  __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// ring_wait<k * L>() for a runtime k in [0, KMAX].
+template <int L, int KMAX>
+__device__ __forceinline__ void ring_wait_chunks(int k) {
+  if constexpr (KMAX > 0) {
+    if (k >= KMAX) {
+      ring_wait<KMAX * L>();
+      return;
+    }
+    ring_wait_chunks<L, KMAX - 1>(k);
+  } else {
+    ring_wait<0>();
+  }
+}
+
+// A workgroup barrier without the memory fence __syncthreads() adds (whose
+// vmcnt(0) would wait out every chunk in flight): the direct loads a stage
+// needs are waited for explicitly, and a wave's LDS reads of a stage have
+// returned before its MFMAs, hence before it reaches the next barrier. The
+// empty asm keeps the compiler from moving memory accesses across it.
+__device__ __forceinline__ void ring_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// Whether the ring's epilogue can store whole rows four floats at a time:
+// every row, lane and residual offset a multiple of four floats.
+__host__ __device__ inline bool ring_rows_store(const ConvArgs &a) {
+  return a.n % 4 == 0 && a.y_lane_stride % 4 == 0 && (!a.res || a.res_lane_stride % 4 == 0);
+}
+
+template <int MT, int NT, int ST, int BK>
+struct RingShape {
+  static constexpr int BM = 32 * MT, BN = 32 * NT;
+  static constexpr int G = BK / 4;            // 16-byte groups per row
+  static constexpr int RPI = 64 / G;          // rows one direct load fills
+  static constexpr int STAGE = (BM + BN) * BK;  // floats per stage
+  static constexpr int A_I = BM / (4 * RPI), B_I = BN / (4 * RPI);  // direct loads per wave per chunk
+  static constexpr int L = A_I + B_I;
+  static_assert(BM % (4 * RPI) == 0 && BN % (4 * RPI) == 0, "whole loads per wave");
+  static_assert(L * (ST - 1) < 64, "pending loads must fit vmcnt");
+};
+
+template <int MT, int NT, int ST, int BK, bool GATE>
+__global__ __launch_bounds__(256) void conv_ring(ConvArgs a, int gate_lanes, int stages) {
+  typedef RingShape<MT, NT, ST, BK> R;
+  constexpr int BM = R::BM, BN = R::BN, STAGE = R::STAGE, L = R::L, G = R::G, RPI = R::RPI;
+  extern __shared__ __attribute__((aligned(16))) float ring[];
+  float *gs = ring + stages * STAGE;  // gate rows of the lanes the tile touches
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave & 1, wn = wave >> 1;
+  const int per_lane = a.oh * a.ow;
+  const int M = a.lanes * per_lane;
+  const int ntn = (a.n + BN - 1) / BN;
+  const int tile = a.xcd_rows ? xcd_tile(blockIdx.x, gridDim.x) : blockIdx.x;
+  const int tn = tile % ntn, tm = tile / ntn;
+  const int m0 = tm * BM, n0 = tn * BN;
+  if (m0 >= M) return;
+  const int chunks = (a.ctot + BK - 1) / BK;
+  const int KP = chunks * BK;
+
+  // The gate rows, zero past ctot, before any direct load is issued.
+  const int lane0 = m0 / per_lane;
+  if constexpr (GATE) {
+    const int kv = KP / 4;
+    for (int e = tid; e < gate_lanes * kv; e += 256) {
+      const int l = e / kv, k = (e - l * kv) * 4;
+      f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (k < a.ctot && lane0 + l < a.lanes)
+        v = *reinterpret_cast<const f32x4 *>(a.gate + (long)(lane0 + l) * a.gate_lane_stride + k);
+      *reinterpret_cast<f32x4 *>(gs + l * KP + k) = v;
+    }
+    __syncthreads();
+  }
+
+  // The global row and group each lane fetches for each of its direct loads.
+  const int lrow = lane / G, lslot = lane % G;
+  const float *a_src[R::A_I];
+  int a_k[R::A_I];
+#pragma unroll
+  for (int i = 0; i < R::A_I; i++) {
+    const int r = (i * 4 + wave) * RPI + lrow;
+    const int m = m0 + r;
+    const int g = lslot ^ ring_swz<BK>(r);
+    a_k[i] = g * 4;
+    if (m < M) {
+      const int ln = m / per_lane, px = m - ln * per_lane;
+      a_src[i] = a.src[0].p + (long)ln * a.src[0].lane_stride + (long)px * a.ctot + g * 4;
+    } else {
+      a_src[i] = nullptr;
+    }
+  }
+  const float *b_src[R::B_I];
+  int b_k[R::B_I];
+#pragma unroll
+  for (int i = 0; i < R::B_I; i++) {
+    const int r = (i * 4 + wave) * RPI + lrow;
+    const int n = n0 + r;
+    const int g = lslot ^ ring_swz<BK>(r);
+    b_k[i] = g * 4;
+    b_src[i] = n < a.n ? a.wt + (long)n * a.wt_k + g * 4 : nullptr;
+  }
+
+  auto issue = [&](int q, int st) {
+    const int k0 = q * BK;
+    float *base = ring + st * STAGE;
+#pragma unroll
+    for (int i = 0; i < R::A_I; i++) {
+      const float *p = a_src[i] && k0 + a_k[i] < a.ctot ? a_src[i] + k0 : kRingZeros;
+      __builtin_amdgcn_global_load_lds((const void *)p, (lds_void *)(base + (i * 4 + wave) * RPI * BK), 16, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < R::B_I; i++) {
+      const float *p = b_src[i] && k0 + b_k[i] < a.ctot ? b_src[i] + k0 : kRingZeros;
+      __builtin_amdgcn_global_load_lds((const void *)p, (lds_void *)(base + (BM + (i * 4 + wave) * RPI) * BK), 16,
+                                       0, 0);
+    }
+  };
+
+  f32x4 acc[MT][NT];
+#pragma unroll
+  for (int i = 0; i < MT; i++)
+#pragma unroll
+    for (int j = 0; j < NT; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int li = lane & 15, lg = lane >> 4;
+  int ar[MT], asw[MT], arel[MT];
+#pragma unroll
+  for (int i = 0; i < MT; i++) {
+    ar[i] = wm * 16 * MT + i * 16 + li;
+    asw[i] = ring_swz<BK>(ar[i]);
+    const int m = min(m0 + ar[i], M - 1);
+    arel[i] = min(m / per_lane - lane0, gate_lanes - 1);
+  }
+  int br[NT], bsw[NT];
+#pragma unroll
+  for (int j = 0; j < NT; j++) {
+    br[j] = wn * 16 * NT + j * 16 + li;
+    bsw[j] = ring_swz<BK>(br[j]);
+    br[j] += BM;
+  }
+
+#pragma unroll
+  for (int s = 0; s < ST - 1; s++)
+    if (s < chunks) issue(s, s);
+
+  for (int q = 0; q < chunks; q++) {
+    // Chunk q is complete once no more than the later chunks' loads are
+    // pending; the barrier then also frees the stage chunk q - 1 used.
+    ring_wait_chunks<L, ST - 2>(min(ST - 2, chunks - 1 - q));
+    ring_barrier();
+    if (q + ST - 1 < chunks) issue(q + ST - 1, (q + ST - 1) % ST);
+    const float *base = ring + (q % ST) * STAGE;
+#pragma unroll
+    for (int r = 0; r < BK / 16; r++) {
+      const int g = r * 4 + lg;
+      f32x4 av[MT], bv[NT];
+#pragma unroll
+      for (int i = 0; i < MT; i++) {
+        av[i] = *reinterpret_cast<const f32x4 *>(base + ar[i] * BK + (g ^ asw[i]) * 4);
+        if constexpr (GATE) av[i] = av[i] * *reinterpret_cast<const f32x4 *>(gs + arel[i] * KP + q * BK + g * 4);
+      }
+#pragma unroll
+      for (int j = 0; j < NT; j++) bv[j] = *reinterpret_cast<const f32x4 *>(base + br[j] * BK + (g ^ bsw[j]) * 4);
+#pragma unroll
+      for (int k = 0; k < 4; k++)
+#pragma unroll
+        for (int i = 0; i < MT; i++)
+#pragma unroll
+          for (int j = 0; j < NT; j++)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[i][k], bv[j][k], acc[i][j], 0, 0, 0);
+    }
+  }
+
+  // Bias per column once; rows and columns past the matrix store nothing.
+  float bias_v[NT];
+  int col[NT];
+#pragma unroll
+  for (int j = 0; j < NT; j++) {
+    col[j] = n0 + wn * 16 * NT + j * 16 + li;
+    bias_v[j] = a.bias && col[j] < a.n ? a.bias[col[j]] : 0.0f;
+  }
+  if (a.mode == GEMM_STORE && ring_rows_store(a)) {
+    // Through LDS: the tile, after bias and activation, row-major (rows
+    // padded by 4 so that the four row groups of a store land in distinct
+    // banks); then each thread stores four consecutive outputs of a row,
+    // with the residual and second activation, so a wave writes whole rows.
+    constexpr int TS = BN + 4;
+    __syncthreads();  // every wave is done with the ring
+#pragma unroll
+    for (int i = 0; i < MT; i++)
+#pragma unroll
+      for (int r = 0; r < 4; r++)
+#pragma unroll
+        for (int j = 0; j < NT; j++) {
+          float v = acc[i][j][r];
+          if (a.bias) v = v + bias_v[j];
+          ring[(wm * 16 * MT + i * 16 + lg * 4 + r) * TS + wn * 16 * NT + j * 16 + li] = act(v, a.act);
+        }
+    __syncthreads();
+    constexpr int CV = BN / 4;
+    for (int e = tid; e < BM * CV; e += 256) {
+      const int row = e / CV, c4 = e - row * CV;
+      const int m = m0 + row, n = n0 + c4 * 4;
+      if (m >= M || n >= a.n) continue;
+      const int ln = m / per_lane, rem = m - ln * per_lane;
+      f32x4 v = *reinterpret_cast<const f32x4 *>(ring + row * TS + c4 * 4);
+      if (a.res) {
+        const f32x4 rv = *reinterpret_cast<const f32x4 *>(a.res + (long)ln * a.res_lane_stride + (long)rem * a.n + n);
+        v.x = act(v.x + rv.x, a.act2);
+        v.y = act(v.y + rv.y, a.act2);
+        v.z = act(v.z + rv.z, a.act2);
+        v.w = act(v.w + rv.w, a.act2);
+      }
+      *reinterpret_cast<f32x4 *>(a.y + (long)ln * a.y_lane_stride + (long)rem * a.n + n) = v;
+    }
+    return;
+  }
+#pragma unroll
+  for (int i = 0; i < MT; i++) {
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int m = m0 + wm * 16 * MT + i * 16 + lg * 4 + r;
+      const int ln = m / per_lane, rem = m - ln * per_lane;
+#pragma unroll
+      for (int j = 0; j < NT; j++) {
+        const int n = col[j];
+        if (m < M && n < a.n) {
+          float v = acc[i][j][r];
+          if (a.bias) v = v + bias_v[j];
+          v = act(v, a.act);
+          if (a.res) v = act(v + a.res[(long)ln * a.res_lane_stride + (long)rem * a.n + n], a.act2);
+          long at;
+          if (a.mode == GEMM_SPREAD) {
+            const int iy = rem / a.iw, ix = rem - iy * a.iw;
+            const int tap = n / a.spread_oc, o = n - tap * a.spread_oc;
+            const int ky = tap / a.spread_kw, kx = tap - ky * a.spread_kw;
+            const int kh = a.n / (a.spread_kw * a.spread_oc);
+            const long ow = (long)a.iw * a.spread_kw;
+            at = ((long)(iy * kh + ky) * ow + (long)ix * a.spread_kw + kx) * a.spread_oc + o;
+          } else {
+            at = (long)rem * a.n + n;
+          }
+          a.y[(long)ln * a.y_lane_stride + at] = v;
+        }
+      }
+    }
+  }
+}
+
+// Lanes whose gate rows a tile of bm rows can touch.
+static int ring_gate_lanes(const ConvArgs &a, int bm) {
+  const long per_lane = (long)a.oh * a.ow;
+  return (int)std::min<long>(a.lanes, bm / per_lane + 2);
+}
+
+// Stages a GEMM uses: its chunk count when below the ring's.
+static int ring_stages(const ConvArgs &a, int st, int bk) {
+  const int chunks = (a.ctot + bk - 1) / bk;
+  return std::min(st, chunks);
+}
+
+static size_t ring_lds(const ConvArgs &a, int mt, int nt, int st, int bk) {
+  const int bm = 32 * mt, bn = 32 * nt, kp = (a.ctot + bk - 1) / bk * bk;
+  size_t b = (size_t)ring_stages(a, st, bk) * (bm + bn) * bk * sizeof(float);
+  if (a.mode == GEMM_STORE && ring_rows_store(a)) b = std::max(b, (size_t)bm * (bn + 4) * sizeof(float));
+  if (a.gate) b += (size_t)ring_gate_lanes(a, bm) * kp * sizeof(float);
+  return b;
+}
+
+template <int MT, int NT, int ST, int BK, bool GATE>
+static hipError_t go_ring1(const ConvArgs &a, hipStream_t s) {
+  typedef RingShape<MT, NT, ST, BK> R;
+  const long M = (long)a.lanes * a.oh * a.ow;
+  const long tiles = (M + R::BM - 1) / R::BM * ((a.n + R::BN - 1) / R::BN);
+  if (tiles <= 0 || tiles > 0x7fffffffL) return hipErrorInvalidValue;
+  const size_t lds = ring_lds(a, MT, NT, ST, BK);
+  if (lds > kMaxLdsBytes) return hipErrorInvalidValue;
+  static bool raised = false;  // once per instantiation: the limit is a property of the kernel
+  if (!raised) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(conv_ring<MT, NT, ST, BK, GATE>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxLdsBytes);
+    if (e != hipSuccess) return e;
+    raised = true;
+  }
+  hipLaunchKernelGGL((conv_ring<MT, NT, ST, BK, GATE>), dim3((unsigned)tiles), dim3(256), lds, s, a,
+                     ring_gate_lanes(a, R::BM), ring_stages(a, ST, BK));
+  return hipGetLastError();
+}
+
+template <int MT, int NT, int ST, int BK>
+static hipError_t go_ring(const ConvArgs &a, hipStream_t s) {
+  return a.gate ? go_ring1<MT, NT, ST, BK, true>(a, s) : go_ring1<MT, NT, ST, BK, false>(a, s);
+}
+
+bool ring_supported(const ConvArgs &a) {
+  if (a.mode != GEMM_STORE && a.mode != GEMM_SPREAD) return false;
+  if (a.nsrc != 1 || a.src[0].shift != 0 || a.ctot != a.src[0].c || a.ctot % 4 != 0) return false;
+  if (a.kh != 1 || a.kw != 1 || a.sh != 1 || a.sw != 1 || a.pt != 0 || a.pl != 0) return false;
+  if (a.oh != a.ih || a.ow != a.iw) return false;
+  return true;
+}
+
+bool ring_fits(const ConvArgs &a, const RingTile &t) {
+  return ring_lds(a, t.mt, t.nt, t.st, t.bk) <= kMaxLdsBytes;
+}
+
+#define PPOCR_RING(MT, NT, ST, BK) \
+  if (t.mt == MT && t.nt == NT && t.st == ST && t.bk == BK) return go_ring<MT, NT, ST, BK>(a, s);
+
+// The tiles compiled (ring_tile in the model picks among them).
+#define PPOCR_RING_TILES                                                                         \
+  PPOCR_RING(1, 1, 3, 32) PPOCR_RING(1, 1, 4, 32) PPOCR_RING(1, 2, 3, 32) PPOCR_RING(1, 2, 4, 32) \
+  PPOCR_RING(1, 3, 3, 32) PPOCR_RING(1, 3, 4, 32)
+
+hipError_t launch_conv_ring(const ConvArgs &a, const RingTile &t, hipStream_t s) {
+  if (!ring_supported(a) || !ring_fits(a, t)) return hipErrorInvalidValue;
+  PPOCR_RING_TILES
+  return hipErrorInvalidValue;
+}
+
 template <int WM, int BN, int BK, int LAY, bool CTC>
 static hipError_t go(const ConvArgs &a, hipStream_t s) {
   long M = (long)a.lanes * a.oh * a.ow;

@@ -63,6 +63,16 @@ struct GemmTile {
 // WM 16 (BN 64); BK 64 (channel layout) with WM 16 and BN 16, 32, 64.
 bool gemm_tile_supported(const GemmTile &t);
 hipError_t launch_conv(const ConvArgs &a, const GemmTile &t, hipStream_t s);
+// The 1x1 convolution (GEMM_STORE or GEMM_SPREAD, one source of ctot
+// channels, a multiple of 4) with its operand chunks in an LDS ring fed by
+// direct loads: tiles of 32 * mt rows x 32 * nt columns, st stages of bk
+// channels (compiled: mt 1, nt 1 to 3, st 3 or 4, bk 32).
+struct RingTile {
+  int mt, nt, st, bk;
+};
+bool ring_supported(const ConvArgs &a);
+bool ring_fits(const ConvArgs &a, const RingTile &t);
+hipError_t launch_conv_ring(const ConvArgs &a, const RingTile &t, hipStream_t s);
 // The halo-tile windowed convolution (GEMM_STORE, kh, kw <= 3, stride 1 or
 // 2, channels a multiple of 4): output tiles 16 wide x 4 * wr rows, bn
 // columns, channel blocks of bk (the packed weights' chunk).

@@ -450,6 +450,22 @@ bool Model::build_steps(std::string &err) {
 }
 
 // Choose each GEMM step's reduction chunk and tile, and repack its weights:
+// The LDS-ring GEMM's tile for an M x N product, from a sweep of tiles,
+// stage counts and chunk widths over the detector's and recogniser's 1x1
+// layers: 32-row tiles throughout (more workgroups per CU beat larger
+// tiles); 96 columns when N is 96 and that leaves over one tile per CU,
+// 64 when that leaves about three, else 32; three stages when tiles are
+// plentiful (more of them fit a CU), else four.
+static RingTile ring_tile(long M, int N) {
+  auto tiles = [&](int n) { return (M + 31) / 32 * ((N + 32L * n - 1) / (32L * n)); };
+  int nt = 1;
+  if (N == 96 && tiles(3) >= 384)
+    nt = 3;
+  else if (N > 32 && (N <= 64 || tiles(2) >= 768))
+    nt = 2;
+  return RingTile{1, nt, tiles(nt) >= 512 ? 3 : 4, 32};
+}
+
 // row n of the packed matrix holds column n's reduction in the kernel's chunk
 // order, zero where the padding of a chunk lies.
 //  - channel layout (every source's channels a multiple of 4): per tap, the
@@ -798,10 +814,16 @@ void Model::build_launches(Batch &b) {
           break;
         }
         long M = long(L) * a.oh * a.ow;
+        a.xcd_rows = 1;
+        if (t.pointwise && ring_supported(a) && ring_fits(a, ring_tile(M, a.n))) {
+          const RingTile rt = ring_tile(M, a.n);
+          const char *nm = op.kind == K_CONVTRANSPOSE ? "convt_gemm" : "pointwise_gemm";
+          b.launches.push_back({nm, s.op, [a, rt](hipStream_t st) { return launch_conv_ring(a, rt, st); }});
+          break;
+        }
         long tiles = (M + 127) / 128 * ((a.n + t.bn - 1) / t.bn);
         // Fewer than four tiles per CU of 128 rows: take 64-row tiles.
         if (tiles < 1024) t.wm = 16;
-        a.xcd_rows = 1;
         const char *nm = op.kind == K_CONVTRANSPOSE ? "convt_gemm" : (t.pointwise ? "pointwise_gemm" : "conv_gemm");
         b.launches.push_back({nm, s.op, [a, t](hipStream_t st) { return launch_conv(a, t, st); }});
         break;

@@ -67,7 +67,8 @@ def test_depthwise_exact(oracle, k, s, c):
     exact(got, want)
 
 
-@pytest.mark.parametrize("ci,co", [(16, 16), (24, 48), (96, 96), (12, 20), (480, 120), (8, 64)])
+@pytest.mark.parametrize("ci,co", [(16, 16), (24, 48), (96, 96), (12, 20), (480, 120), (8, 64),
+                                   (20, 10), (36, 6), (64, 200)])
 def test_pointwise_gemm(oracle, ci, co):
     w = RNG.normal(0, 1 / np.sqrt(ci), (1, 1, ci, co)).astype(np.float32)
     bias = RNG.normal(0, 0.3, co).astype(np.float32)
@@ -128,10 +129,13 @@ def test_patch_conv(oracle, k, s, ci, co, hw, lanes):
     near(got, want)
 
 
-@pytest.mark.parametrize("k,c,hw", [(3, 32, (21, 19)), (5, 96, (40, 52)), (3, 480, (12, 13))])
+@pytest.mark.parametrize("k,c,hw", [(3, 32, (21, 19)), (5, 96, (40, 52)), (3, 200, (9, 9)),
+                                     (5, 384, (14, 11)), (3, 480, (12, 13))])
 def test_gemm_gate_and_residual(oracle, k, c, hw):
     # dw -> SE (mean, 1x1 ReLU, 1x1 hard sigmoid) -> gated pointwise + input.
     # The depthwise kernel also sums its outputs per channel for the mean.
+    # The SE weights reach LDS together (c <= 200), one layer after the
+    # other (384 x 96 each) or not at all (480 x 120, read from memory).
     mid = c // 4
     wd = RNG.normal(0, 0.3, (k, k, c)).astype(np.float32)
     w1 = RNG.normal(0, 0.3, (1, 1, c, mid)).astype(np.float32)
@@ -151,6 +155,23 @@ def test_gemm_gate_and_residual(oracle, k, c, hw):
     near([[gl[0]] for gl in got], [[wl[0]] for wl in want])
     # The gate: the same mean to f64 rounding, then the same 1x1 sums.
     near([[gl[1]] for gl in got], [[wl[1]] for wl in want], tol=1e-6)
+
+
+def test_gated_pointwise_many_lanes(oracle):
+    # 15-pixel lanes: a 32-row tile of the 1x1 GEMM spans up to four lanes,
+    # each with its own gate row; the residual rides along.
+    c = 64
+    w1 = RNG.normal(0, 0.3, (1, 1, c, 16)).astype(np.float32)
+    w2 = RNG.normal(0, 0.3, (1, 1, 16, c)).astype(np.float32)
+    wp = RNG.normal(0, 0.2, (1, 1, c, c)).astype(np.float32)
+    bv = RNG.normal(0, 0.3, c).astype(np.float32)
+
+    def build(b, t):
+        g = b.conv(b.conv(b.mean(t), w1, None, fused="relu"), w2, None, fused="hardsigmoid")
+        return b.add(b.conv(b.channelmul(t, g), wp, bv), t)
+
+    got, want = both(build, (3, 5, c), oracle, lanes=7)
+    near(got, want)
 
 
 def test_upsampled_concat_sources(oracle):
