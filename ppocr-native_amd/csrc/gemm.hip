@@ -602,6 +602,10 @@ __device__ __attribute__((aligned(16))) float kRingZeros[4];
 
 static const size_t kMaxLdsBytes = 160 * 1024;
 
+// The chunk width of a windowed convolution on the ring: the packer lays each
+// tap's channels out in chunks of this many floats.
+constexpr int kRingBK = 32;
+
 typedef __attribute__((address_space(3))) void lds_void;
 
 template <int BK>
@@ -660,7 +664,7 @@ struct RingShape {
   static_assert(L * (ST - 1) < 64, "pending loads must fit vmcnt");
 };
 
-template <int MT, int NT, int ST, int BK, bool GATE>
+template <int MT, int NT, int ST, int BK, bool GATE, bool WIN>
 __global__ __launch_bounds__(256) void conv_ring(ConvArgs a, int gate_lanes, int stages) {
   typedef RingShape<MT, NT, ST, BK> R;
   constexpr int BM = R::BM, BN = R::BN, STAGE = R::STAGE, L = R::L, G = R::G, RPI = R::RPI;
@@ -677,7 +681,7 @@ __global__ __launch_bounds__(256) void conv_ring(ConvArgs a, int gate_lanes, int
   const int tn = tile % ntn, tm = tile / ntn;
   const int m0 = tm * BM, n0 = tn * BN;
   if (m0 >= M) return;
-  const int chunks = (a.ctot + BK - 1) / BK;
+  const int chunks = WIN ? a.chunks : (a.ctot + BK - 1) / BK;
   const int KP = chunks * BK;
 
   // The gate rows, zero past ctot, before any direct load is issued.
@@ -696,19 +700,25 @@ __global__ __launch_bounds__(256) void conv_ring(ConvArgs a, int gate_lanes, int
 
   // The global row and group each lane fetches for each of its direct loads.
   const int lrow = lane / G, lslot = lane % G;
+  // Pointwise: the row's pointer at its group. Windowed: the row's lane and
+  // window corner (a row past the matrix sits far outside the image).
   const float *a_src[R::A_I];
-  int a_k[R::A_I];
+  int a_k[R::A_I], a_ln[WIN ? R::A_I : 1], a_y[WIN ? R::A_I : 1], a_x[WIN ? R::A_I : 1];
 #pragma unroll
   for (int i = 0; i < R::A_I; i++) {
     const int r = (i * 4 + wave) * RPI + lrow;
     const int m = m0 + r;
     const int g = lslot ^ ring_swz<BK>(r);
     a_k[i] = g * 4;
-    if (m < M) {
-      const int ln = m / per_lane, px = m - ln * per_lane;
-      a_src[i] = a.src[0].p + (long)ln * a.src[0].lane_stride + (long)px * a.ctot + g * 4;
-    } else {
+    const int ln = m / per_lane, px = m - ln * per_lane;
+    if constexpr (WIN) {
+      const int oy = px / a.ow, ox = px - oy * a.ow;
+      a_ln[i] = ln;
+      a_y[i] = m < M ? oy * a.sh - a.pt : -(1 << 20);
+      a_x[i] = ox * a.sw - a.pl;
       a_src[i] = nullptr;
+    } else {
+      a_src[i] = m < M ? a.src[0].p + (long)ln * a.src[0].lane_stride + (long)px * a.ctot + g * 4 : nullptr;
     }
   }
   const float *b_src[R::B_I];
@@ -725,14 +735,33 @@ __global__ __launch_bounds__(256) void conv_ring(ConvArgs a, int gate_lanes, int
   auto issue = [&](int q, int st) {
     const int k0 = q * BK;
     float *base = ring + st * STAGE;
-#pragma unroll
-    for (int i = 0; i < R::A_I; i++) {
-      const float *p = a_src[i] && k0 + a_k[i] < a.ctot ? a_src[i] + k0 : kRingZeros;
-      __builtin_amdgcn_global_load_lds((const void *)p, (lds_void *)(base + (i * 4 + wave) * RPI * BK), 16, 0, 0);
+    // Windowed: chunk q is channel block cc of tap (ky, kx).
+    int ky = 0, kx = 0, cb = 0;
+    if constexpr (WIN) {
+      const int tap = q / a.cpt;
+      cb = (q - tap * a.cpt) * BK;
+      ky = tap / a.kw;
+      kx = tap - ky * a.kw;
     }
 #pragma unroll
+    for (int i = 0; i < R::A_I; i++) {
+      const float *p = kRingZeros;
+      if constexpr (WIN) {
+        const int c = cb + a_k[i], iy = a_y[i] + ky, ix = a_x[i] + kx;
+        if (c < a.ctot && iy >= 0 && iy < a.ih && ix >= 0 && ix < a.iw) {
+          const ConvSrc s = pick_src(a, c);
+          const long pix = (long)(iy >> s.shift) * (a.iw >> s.shift) + (ix >> s.shift);
+          p = s.p + (long)a_ln[i] * s.lane_stride + pix * s.c + (c - s.coff);
+        }
+      } else {
+        if (a_src[i] && k0 + a_k[i] < a.ctot) p = a_src[i] + k0;
+      }
+      __builtin_amdgcn_global_load_lds((const void *)p, (lds_void *)(base + (i * 4 + wave) * RPI * BK), 16, 0, 0);
+    }
+    // The packed rows are zero past each tap's channels.
+#pragma unroll
     for (int i = 0; i < R::B_I; i++) {
-      const float *p = b_src[i] && k0 + b_k[i] < a.ctot ? b_src[i] + k0 : kRingZeros;
+      const float *p = b_src[i] && (WIN || k0 + b_k[i] < a.ctot) ? b_src[i] + k0 : kRingZeros;
       __builtin_amdgcn_global_load_lds((const void *)p, (lds_void *)(base + (BM + (i * 4 + wave) * RPI) * BK), 16,
                                        0, 0);
     }
@@ -875,21 +904,25 @@ static int ring_gate_lanes(const ConvArgs &a, int bm) {
   return (int)std::min<long>(a.lanes, bm / per_lane + 2);
 }
 
-// Stages a GEMM uses: its chunk count when below the ring's.
-static int ring_stages(const ConvArgs &a, int st, int bk) {
-  const int chunks = (a.ctot + bk - 1) / bk;
-  return std::min(st, chunks);
+// Whether the ring runs a windowed convolution (implicit GEMM over taps).
+static bool ring_window(const ConvArgs &a) { return a.kh != 1 || a.kw != 1 || a.nsrc != 1 || a.sh != 1 || a.sw != 1; }
+
+static int ring_chunks(const ConvArgs &a, int bk) {
+  return ring_window(a) ? a.chunks : (a.ctot + bk - 1) / bk;
 }
 
+// Stages a GEMM uses: its chunk count when below the ring's.
+static int ring_stages(const ConvArgs &a, int st, int bk) { return std::min(st, ring_chunks(a, bk)); }
+
 static size_t ring_lds(const ConvArgs &a, int mt, int nt, int st, int bk) {
-  const int bm = 32 * mt, bn = 32 * nt, kp = (a.ctot + bk - 1) / bk * bk;
+  const int bm = 32 * mt, bn = 32 * nt, kp = ring_chunks(a, bk) * bk;
   size_t b = (size_t)ring_stages(a, st, bk) * (bm + bn) * bk * sizeof(float);
   if (a.mode == GEMM_STORE && ring_rows_store(a)) b = std::max(b, (size_t)bm * (bn + 4) * sizeof(float));
   if (a.gate) b += (size_t)ring_gate_lanes(a, bm) * kp * sizeof(float);
   return b;
 }
 
-template <int MT, int NT, int ST, int BK, bool GATE>
+template <int MT, int NT, int ST, int BK, bool GATE, bool WIN>
 static hipError_t go_ring1(const ConvArgs &a, hipStream_t s) {
   typedef RingShape<MT, NT, ST, BK> R;
   const long M = (long)a.lanes * a.oh * a.ow;
@@ -899,27 +932,35 @@ static hipError_t go_ring1(const ConvArgs &a, hipStream_t s) {
   if (lds > kMaxLdsBytes) return hipErrorInvalidValue;
   static bool raised = false;  // once per instantiation: the limit is a property of the kernel
   if (!raised) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(conv_ring<MT, NT, ST, BK, GATE>),
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(conv_ring<MT, NT, ST, BK, GATE, WIN>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxLdsBytes);
     if (e != hipSuccess) return e;
     raised = true;
   }
-  hipLaunchKernelGGL((conv_ring<MT, NT, ST, BK, GATE>), dim3((unsigned)tiles), dim3(256), lds, s, a,
+  hipLaunchKernelGGL((conv_ring<MT, NT, ST, BK, GATE, WIN>), dim3((unsigned)tiles), dim3(256), lds, s, a,
                      ring_gate_lanes(a, R::BM), ring_stages(a, ST, BK));
   return hipGetLastError();
 }
 
 template <int MT, int NT, int ST, int BK>
 static hipError_t go_ring(const ConvArgs &a, hipStream_t s) {
-  return a.gate ? go_ring1<MT, NT, ST, BK, true>(a, s) : go_ring1<MT, NT, ST, BK, false>(a, s);
+  if (ring_window(a)) return go_ring1<MT, NT, ST, BK, false, true>(a, s);
+  return a.gate ? go_ring1<MT, NT, ST, BK, true, false>(a, s) : go_ring1<MT, NT, ST, BK, false, false>(a, s);
 }
 
 bool ring_supported(const ConvArgs &a) {
   if (a.mode != GEMM_STORE && a.mode != GEMM_SPREAD) return false;
-  if (a.nsrc != 1 || a.src[0].shift != 0 || a.ctot != a.src[0].c || a.ctot % 4 != 0) return false;
-  if (a.kh != 1 || a.kw != 1 || a.sh != 1 || a.sw != 1 || a.pt != 0 || a.pl != 0) return false;
-  if (a.oh != a.ih || a.ow != a.iw) return false;
-  return true;
+  if (a.ctot % 4 != 0) return false;
+  if (!ring_window(a))
+    return a.nsrc == 1 && a.src[0].shift == 0 && a.ctot == a.src[0].c && a.oh == a.ih && a.ow == a.iw &&
+           a.pt == 0 && a.pl == 0;
+  // Windowed: GEMM_STORE, no gate, every source's channels a multiple of 4,
+  // weights packed per tap in chunks of kRingBK.
+  if (a.mode != GEMM_STORE || a.gate || a.nsrc < 1 || a.nsrc > 4) return false;
+  for (int k = 0; k < a.nsrc; k++)
+    if (a.src[k].c % 4 != 0 || a.src[k].coff % 4 != 0) return false;
+  const int cpt = (a.ctot + kRingBK - 1) / kRingBK;
+  return a.cpt == cpt && a.chunks == a.kh * a.kw * cpt && a.wt_k == (long)a.chunks * kRingBK;
 }
 
 bool ring_fits(const ConvArgs &a, const RingTile &t) {

@@ -80,6 +80,7 @@ struct Step {
   int head2 = -1;          // the narrow transposed convolution folded into S_HEAD
   bool dw_sums = false;    // S_DW: also sum its output per channel for the next step's mean
   bool patch = false;      // S_GEMM: a windowed convolution on halo tiles (conv_patch)
+  bool ring = false;       // S_GEMM: a windowed convolution on the LDS ring (conv_ring)
   int mean_of_dw = -1;     // S_MEAN: the depthwise operation whose sums it joins
   int elt = 0;             // EltMode
   std::vector<Source> sources;
@@ -543,6 +544,15 @@ bool Model::pack(std::string &err) {
         }
         if (pb) s.patch = true, bk = pb;
       }
+      // A windowed convolution that neither halo tiles nor the register-staged
+      // implicit GEMM take well (a window wider than 3 or unequal strides)
+      // and has no gate: the LDS ring, whose direct loads fetch each tap's
+      // channels in chunks of 32. (On the stem's large maps the ring's
+      // 32-row tiles re-read each tap's rows and the weights from L2 per
+      // tile and lose to the 128-row implicit GEMM.)
+      if (s.kind == S_GEMM && op.kind == K_CONV && !pw && !s.patch && s.gate < 0 &&
+          (op.kh > 3 || op.kw > 3 || op.sh != op.sw || op.kh * op.kw == 1))
+        s.ring = true, bk = 32;
       cpt = (ctot + bk - 1) / bk;
       s.chunks = taps * cpt;
     } else {
@@ -815,9 +825,9 @@ void Model::build_launches(Batch &b) {
         }
         long M = long(L) * a.oh * a.ow;
         a.xcd_rows = 1;
-        if (t.pointwise && ring_supported(a) && ring_fits(a, ring_tile(M, a.n))) {
+        if ((t.pointwise || s.ring) && ring_supported(a) && ring_fits(a, ring_tile(M, a.n))) {
           const RingTile rt = ring_tile(M, a.n);
-          const char *nm = op.kind == K_CONVTRANSPOSE ? "convt_gemm" : "pointwise_gemm";
+          const char *nm = op.kind == K_CONVTRANSPOSE ? "convt_gemm" : (t.pointwise ? "pointwise_gemm" : "conv_gemm");
           b.launches.push_back({nm, s.op, [a, rt](hipStream_t st) { return launch_conv_ring(a, rt, st); }});
           break;
         }

@@ -90,6 +90,48 @@ def test_windowed_gemm(oracle, k, s, pad, ci, co):
     near(got, want)
 
 
+@pytest.mark.parametrize("k,s,pad,ci,co,hw,lanes,two", [
+    ((2, 2), (1, 1), (0, 1, 0, 1), 24, 12, (130, 131), 1, False),   # the stem's 2 x 2 on a large map
+    ((3, 3), (2, 2), (1, 1, 1, 1), 24, 32, (262, 258), 1, True),    # stride 2 over two sources
+    ((5, 5), (1, 1), (2, 2, 2, 2), 8, 20, (17, 23), 2, False),      # wider than the halo tiles take
+    ((3, 3), (2, 1), (1, 1, 1, 1), 12, 40, (21, 18), 3, False),     # unequal strides
+    ((1, 1), (2, 2), (0, 0, 0, 0), 16, 24, (19, 26), 2, False),     # a strided 1 x 1
+    ((5, 5), (1, 1), (2, 2, 2, 2), 8, 12, (15, 14), 2, True),       # two sources, wide window
+])
+def test_ring_windowed(oracle, k, s, pad, ci, co, hw, lanes, two):
+    # Windowed convolutions: the wide window, unequal strides and the strided
+    # 1 x 1 run on the LDS ring, each lane's direct loads gathering its row's
+    # window (zeros outside the image and past the channels); the stem's
+    # shapes on large maps run on the register-staged implicit GEMM.
+    cin = 2 * ci if two else ci
+    w = RNG.normal(0, 1 / np.sqrt(cin * k[0] * k[1]), (k[0], k[1], cin, co)).astype(np.float32)
+    bias = RNG.normal(0, 0.3, co).astype(np.float32)
+    wx = RNG.normal(0, 0.3, (1, 1, ci, ci)).astype(np.float32)
+
+    def build(b, t):
+        x2 = b.conv(t, wx, None, fused="relu") if two else None
+        return b.conv(t, w, bias, k=k, s=s, pad=pad, fused="hardswish", x2=x2)
+
+    got, want = both(build, (*hw, ci), oracle, lanes=lanes)
+    near(got, want)
+
+
+def test_ring_upsampled_sources(oracle):
+    # A 5 x 5 convolution (on the LDS ring) over a map upsampled by 2 stacked
+    # with a full-size one: the direct loads read the small map at (y/2, x/2).
+    c = 8
+    wq = RNG.normal(0, 0.3, (1, 1, 4, c)).astype(np.float32)
+    w5 = RNG.normal(0, 0.1, (5, 5, 2 * c, 12)).astype(np.float32)
+
+    def build(b, t):
+        full = b.conv(t, wq, None)
+        half = b.avgpool(full, (2, 2), (2, 2))
+        return b.conv(b.upsample(half, 2), w5, None, k=(5, 5), pad=(2, 2, 2, 2), fused="relu", x2=full)
+
+    got, want = both(build, (14, 18, 4), oracle)
+    near(got, want)
+
+
 @pytest.mark.parametrize("k,s,ci,co,hw,lanes", [
     (3, 1, 96, 24, (30, 40), 3),     # the neck's 3 x 3: 8-row tiles? no, 4-row
     (3, 1, 96, 24, (256, 256), 1),   # 512 tiles of 8 rows
