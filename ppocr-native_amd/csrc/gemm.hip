@@ -370,6 +370,7 @@ __global__ __launch_bounds__(256) void conv_mfma(ConvArgs a) {
   }
 }
 
+
 // A windowed convolution (kh, kw <= 3, stride 1 or 2, one to four sources,
 // upsampled by 2^shift, channels a multiple of 4) on tiles of the output:
 // 16 pixels wide by 4 * WR rows of one lane, BN output channels. For each
@@ -388,7 +389,10 @@ constexpr int kPatchPer = 6;
 constexpr int kWeightPer = 9;
 
 template <int WR, int BN, int CB>
-__global__ __launch_bounds__(256) void conv_patch(ConvArgs a, int tiles_x, int tiles_y) {
+__global__ __launch_bounds__(256) void conv_patch(Group<ConvArgs> grp) {
+  const int prob = group_problem(grp);
+  const ConvArgs &a = grp.a[prob];
+  const int tiles_x = grp.x[prob], tiles_y = grp.y[prob];
   constexpr int S = CB + 4;        // LDS row of one pixel / one (n, tap)
   constexpr int KS = CB / 4;       // channels per lane group per tap
   constexpr int KW = KS >= 4 ? 4 : KS;
@@ -403,7 +407,7 @@ __global__ __launch_bounds__(256) void conv_patch(ConvArgs a, int tiles_x, int t
   float *Bs = lds + PR * PC * S;       // BN x taps x S
 
   const int ntn = (a.n + BN - 1) / BN;
-  int t = blockIdx.x;
+  int t = (int)blockIdx.x - grp.first[prob];
   const int tn = t % ntn;
   t /= ntn;
   const int tx0 = (t % tiles_x) * TW;
@@ -664,9 +668,14 @@ struct RingShape {
   static_assert(L * (ST - 1) < 64, "pending loads must fit vmcnt");
 };
 
+
 template <int MT, int NT, int ST, int BK, bool GATE, bool WIN>
-__global__ __launch_bounds__(256) void conv_ring(ConvArgs a, int gate_lanes, int stages) {
+__global__ __launch_bounds__(256) void conv_ring(Group<ConvArgs> grp) {
   typedef RingShape<MT, NT, ST, BK> R;
+  const int prob = group_problem(grp);
+  const ConvArgs &a = grp.a[prob];
+  const int gate_lanes = grp.x[prob], stages = grp.y[prob];
+  const int blk = (int)blockIdx.x - grp.first[prob], nblk = grp.first[prob + 1] - grp.first[prob];
   constexpr int BM = R::BM, BN = R::BN, STAGE = R::STAGE, L = R::L, G = R::G, RPI = R::RPI;
   extern __shared__ __attribute__((aligned(16))) float ring[];
   float *gs = ring + stages * STAGE;  // gate rows of the lanes the tile touches
@@ -677,7 +686,7 @@ __global__ __launch_bounds__(256) void conv_ring(ConvArgs a, int gate_lanes, int
   const int per_lane = a.oh * a.ow;
   const int M = a.lanes * per_lane;
   const int ntn = (a.n + BN - 1) / BN;
-  const int tile = a.xcd_rows ? xcd_tile(blockIdx.x, gridDim.x) : blockIdx.x;
+  const int tile = a.xcd_rows ? xcd_tile(blk, nblk) : blk;
   const int tn = tile % ntn, tm = tile / ntn;
   const int m0 = tm * BM, n0 = tn * BN;
   if (m0 >= M) return;
@@ -923,12 +932,26 @@ static size_t ring_lds(const ConvArgs &a, int mt, int nt, int st, int bk) {
 }
 
 template <int MT, int NT, int ST, int BK, bool GATE, bool WIN>
-static hipError_t go_ring1(const ConvArgs &a, hipStream_t s) {
+static hipError_t go_ring1(const ConvArgs *as, int n, hipStream_t s) {
   typedef RingShape<MT, NT, ST, BK> R;
-  const long M = (long)a.lanes * a.oh * a.ow;
-  const long tiles = (M + R::BM - 1) / R::BM * ((a.n + R::BN - 1) / R::BN);
-  if (tiles <= 0 || tiles > 0x7fffffffL) return hipErrorInvalidValue;
-  const size_t lds = ring_lds(a, MT, NT, ST, BK);
+  Group<ConvArgs> grp{};
+  grp.n = n;
+  long total = 0;
+  size_t lds = 0;
+  for (int p = 0; p < n; p++) {
+    const ConvArgs &a = as[p];
+    const long M = (long)a.lanes * a.oh * a.ow;
+    const long tiles = (M + R::BM - 1) / R::BM * ((a.n + R::BN - 1) / R::BN);
+    if (tiles <= 0) return hipErrorInvalidValue;
+    grp.first[p] = (int)total;
+    total += tiles;
+    if (total > 0x7fffffffL) return hipErrorInvalidValue;
+    grp.x[p] = ring_gate_lanes(a, R::BM);
+    grp.y[p] = ring_stages(a, ST, BK);
+    grp.a[p] = a;
+    lds = std::max(lds, ring_lds(a, MT, NT, ST, BK));
+  }
+  grp.first[n] = (int)total;
   if (lds > kMaxLdsBytes) return hipErrorInvalidValue;
   static bool raised = false;  // once per instantiation: the limit is a property of the kernel
   if (!raised) {
@@ -937,15 +960,15 @@ static hipError_t go_ring1(const ConvArgs &a, hipStream_t s) {
     if (e != hipSuccess) return e;
     raised = true;
   }
-  hipLaunchKernelGGL((conv_ring<MT, NT, ST, BK, GATE, WIN>), dim3((unsigned)tiles), dim3(256), lds, s, a,
-                     ring_gate_lanes(a, R::BM), ring_stages(a, ST, BK));
+  hipLaunchKernelGGL((conv_ring<MT, NT, ST, BK, GATE, WIN>), dim3((unsigned)total), dim3(256), lds, s, grp);
   return hipGetLastError();
 }
 
 template <int MT, int NT, int ST, int BK>
-static hipError_t go_ring(const ConvArgs &a, hipStream_t s) {
-  if (ring_window(a)) return go_ring1<MT, NT, ST, BK, false, true>(a, s);
-  return a.gate ? go_ring1<MT, NT, ST, BK, true, false>(a, s) : go_ring1<MT, NT, ST, BK, false, false>(a, s);
+static hipError_t go_ring(const ConvArgs *as, int n, hipStream_t s) {
+  if (ring_window(as[0])) return go_ring1<MT, NT, ST, BK, false, true>(as, n, s);
+  return as[0].gate ? go_ring1<MT, NT, ST, BK, true, false>(as, n, s)
+                    : go_ring1<MT, NT, ST, BK, false, false>(as, n, s);
 }
 
 bool ring_supported(const ConvArgs &a) {
@@ -968,17 +991,25 @@ bool ring_fits(const ConvArgs &a, const RingTile &t) {
 }
 
 #define PPOCR_RING(MT, NT, ST, BK) \
-  if (t.mt == MT && t.nt == NT && t.st == ST && t.bk == BK) return go_ring<MT, NT, ST, BK>(a, s);
+  if (t.mt == MT && t.nt == NT && t.st == ST && t.bk == BK) return go_ring<MT, NT, ST, BK>(as, n, s);
 
 // The tiles compiled (ring_tile in the model picks among them).
 #define PPOCR_RING_TILES                                                                         \
   PPOCR_RING(1, 1, 3, 32) PPOCR_RING(1, 1, 4, 32) PPOCR_RING(1, 2, 3, 32) PPOCR_RING(1, 2, 4, 32) \
   PPOCR_RING(1, 3, 3, 32) PPOCR_RING(1, 3, 4, 32)
 
-hipError_t launch_conv_ring(const ConvArgs &a, const RingTile &t, hipStream_t s) {
-  if (!ring_supported(a) || !ring_fits(a, t)) return hipErrorInvalidValue;
+hipError_t launch_conv_ring_group(const ConvArgs *as, int n, const RingTile &t, hipStream_t s) {
+  if (n < 1 || n > kGroupMax) return hipErrorInvalidValue;
+  for (int p = 0; p < n; p++)
+    if (!ring_supported(as[p]) || !ring_fits(as[p], t) || ring_window(as[p]) != ring_window(as[0]) ||
+        (as[p].gate != nullptr) != (as[0].gate != nullptr))
+      return hipErrorInvalidValue;
   PPOCR_RING_TILES
   return hipErrorInvalidValue;
+}
+
+hipError_t launch_conv_ring(const ConvArgs &a, const RingTile &t, hipStream_t s) {
+  return launch_conv_ring_group(&a, 1, t, s);
 }
 
 template <int WM, int BN, int BK, int LAY, bool CTC>
@@ -1072,13 +1103,26 @@ size_t patch_lds_bytes(const ConvArgs &a, int wr, int bk, int bn) {
 }
 
 template <int WR, int BN, int CB>
-static hipError_t go_patch(const ConvArgs &a, hipStream_t s) {
+static hipError_t go_patch(const ConvArgs *as, int n, hipStream_t s) {
   constexpr int TH = 4 * WR;
-  const long tiles_x = (a.ow + 15) / 16, tiles_y = (a.oh + TH - 1) / TH;
-  const long ntn = (a.n + BN - 1) / BN;
-  const long blocks = (long)a.lanes * tiles_y * tiles_x * ntn;
-  if (blocks <= 0 || blocks > 0x7fffffffL) return hipErrorInvalidValue;
-  const size_t shm = patch_lds_bytes(a, WR, CB, BN);
+  Group<ConvArgs> grp{};
+  grp.n = n;
+  long blocks = 0;
+  size_t shm = 0;
+  for (int p = 0; p < n; p++) {
+    const ConvArgs &a = as[p];
+    const long tiles_x = (a.ow + 15) / 16, tiles_y = (a.oh + TH - 1) / TH;
+    const long ntn = (a.n + BN - 1) / BN;
+    const long nb = (long)a.lanes * tiles_y * tiles_x * ntn;
+    if (nb <= 0) return hipErrorInvalidValue;
+    grp.first[p] = (int)blocks;
+    blocks += nb;
+    if (blocks > 0x7fffffffL) return hipErrorInvalidValue;
+    grp.x[p] = (int)tiles_x, grp.y[p] = (int)tiles_y;
+    grp.a[p] = a;
+    shm = std::max(shm, patch_lds_bytes(a, WR, CB, BN));
+  }
+  grp.first[n] = (int)blocks;
   if (shm > 160 * 1024) return hipErrorInvalidValue;
   if (shm > 64 * 1024) {
     static bool raised = false;  // once per process: the limit is a property of the kernel
@@ -1089,18 +1133,23 @@ static hipError_t go_patch(const ConvArgs &a, hipStream_t s) {
       raised = true;
     }
   }
-  hipLaunchKernelGGL((conv_patch<WR, BN, CB>), dim3((unsigned)blocks), dim3(256), shm, s, a, (int)tiles_x,
-                     (int)tiles_y);
+  hipLaunchKernelGGL((conv_patch<WR, BN, CB>), dim3((unsigned)blocks), dim3(256), shm, s, grp);
   return hipGetLastError();
 }
 
 #define PPOCR_PATCH(WR, CB)                                        \
-  if (bn == 16) return go_patch<WR, 16, CB>(a, s);               \
-  if (bn == 32) return go_patch<WR, 32, CB>(a, s);               \
-  if (bn == 64) return go_patch<WR, 64, CB>(a, s);
+  if (bn == 16) return go_patch<WR, 16, CB>(as, n, s);           \
+  if (bn == 32) return go_patch<WR, 32, CB>(as, n, s);           \
+  if (bn == 64) return go_patch<WR, 64, CB>(as, n, s);
 
 hipError_t launch_conv_patch(const ConvArgs &a, int wr, int bk, int bn, hipStream_t s) {
-  if (!patch_supported(a, wr, bk, bn)) return hipErrorInvalidValue;
+  return launch_conv_patch_group(&a, 1, wr, bk, bn, s);
+}
+
+hipError_t launch_conv_patch_group(const ConvArgs *as, int n, int wr, int bk, int bn, hipStream_t s) {
+  if (n < 1 || n > kGroupMax) return hipErrorInvalidValue;
+  for (int p = 0; p < n; p++)
+    if (!patch_supported(as[p], wr, bk, bn)) return hipErrorInvalidValue;
   if (wr == 2) {
     if (bk == 32) { PPOCR_PATCH(2, 32) }
     if (bk == 16) { PPOCR_PATCH(2, 16) }

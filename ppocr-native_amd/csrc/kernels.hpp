@@ -26,6 +26,29 @@ struct ConvSrc {
 
 enum GemmMode : int { GEMM_STORE = 0, GEMM_SPREAD = 1, GEMM_CTC = 2 };
 
+// Up to kGroupMax independent problems of one kernel in one launch (so that
+// small layers which do not depend on each other fill the GPU together):
+// workgroup b runs block b - first[p] of problem p, first[p] <= b <
+// first[p + 1]; x and y carry two per-problem integers of the kernel.
+constexpr int kGroupMax = 4;
+template <typename A>
+struct Group {
+  int n;
+  int first[kGroupMax + 1];
+  int x[kGroupMax], y[kGroupMax];
+  A a[kGroupMax];
+};
+
+// The problem of a grouped launch that workgroup blockIdx.x belongs to.
+template <typename A>
+__device__ __forceinline__ int group_problem(const Group<A> &g) {
+  int p = 0;
+#pragma unroll
+  for (int k = 1; k < kGroupMax; k++)
+    if (k < g.n && (int)blockIdx.x >= g.first[k]) p = k;
+  return p;
+}
+
 struct ConvArgs {
   int lanes;
   int ih, iw, oh, ow;   // per-lane window image and output sizes
@@ -73,6 +96,9 @@ struct RingTile {
 bool ring_supported(const ConvArgs &a);
 bool ring_fits(const ConvArgs &a, const RingTile &t);
 hipError_t launch_conv_ring(const ConvArgs &a, const RingTile &t, hipStream_t s);
+// n <= kGroupMax problems, each ring_supported with the same gate and window
+// kind and ring_fits for t, as one launch.
+hipError_t launch_conv_ring_group(const ConvArgs *a, int n, const RingTile &t, hipStream_t s);
 // The halo-tile windowed convolution (GEMM_STORE, kh, kw <= 3, stride 1 or
 // 2, channels a multiple of 4): output tiles 16 wide x 4 * wr rows, bn
 // columns, channel blocks of bk (the packed weights' chunk).
@@ -80,6 +106,8 @@ bool patch_fits(int kh, int kw, int stride, int wr, int bk, int bn);
 bool patch_supported(const ConvArgs &a, int wr, int bk, int bn);
 size_t patch_lds_bytes(const ConvArgs &a, int wr, int bk, int bn);
 hipError_t launch_conv_patch(const ConvArgs &a, int wr, int bk, int bn, hipStream_t s);
+// n <= kGroupMax problems, each patch_supported for (wr, bk, bn), as one launch.
+hipError_t launch_conv_patch_group(const ConvArgs *a, int n, int wr, int bk, int bn, hipStream_t s);
 
 // CTC choice from the GEMM's per-tile partials: y[2m] = best, y[2m+1] = 1/sum.
 hipError_t launch_ctc_merge(const float *part, int rows, int ntiles, float *y, long y_lane_stride,
@@ -131,6 +159,10 @@ struct EltArgs {
   float *y; long y_lane_stride;
 };
 hipError_t launch_eltwise(const EltArgs &a, hipStream_t s);
+// Whether launch_eltwise takes four floats at a time (the same for every
+// member of a grouped launch).
+bool eltwise_vec(const EltArgs &a);
+hipError_t launch_eltwise_group(const EltArgs *a, int n, hipStream_t s);
 
 struct PoolArgs {
   int avg, lanes, ih, iw, c, oh, ow, kh, kw, sh, sw;
@@ -156,6 +188,21 @@ hipError_t launch_mean(const float *x, long x_lane_stride, int pixels, int c, in
 // The second pass alone, over `chunks` partial rows of c per lane.
 hipError_t launch_mean_finish(const double *partial, int pixels, int c, int chunks, int lanes,
                               const SeArgs *se, float *y, long y_lane_stride, hipStream_t s);
+// One channel mean (with its squeeze-and-excite when has_se) of a grouped
+// launch: the partial sums come from x by the first pass or, with x null,
+// are already in partial (chunks rows per lane, written by a depthwise
+// convolution).
+struct MeanJob {
+  const float *x;
+  long x_lane_stride;
+  int pixels, c, lanes, chunks;
+  double *partial;
+  SeArgs se;
+  int has_se;
+  float *y;
+  long y_lane_stride;
+};
+hipError_t launch_mean_group(const MeanJob *j, int n, hipStream_t s);
 
 hipError_t launch_layernorm(const float *x, long x_lane_stride, const float *w, int rows, int c,
                             int lanes, float *y, long y_lane_stride, hipStream_t s);

@@ -300,11 +300,13 @@ __device__ __forceinline__ void vstore(float *p, const float (&v)[V]) {
 }
 
 template <int V>
-__global__ __launch_bounds__(256) void eltwise_kernel(EltArgs a) {
+__global__ __launch_bounds__(256) void eltwise_kernel(Group<EltArgs> grp) {
+  const int prob = group_problem(grp);
+  const EltArgs &a = grp.a[prob];
+  const long blk = (long)blockIdx.x - grp.first[prob], nblk = grp.first[prob + 1] - grp.first[prob];
   const long per = (long)a.oh * a.ow * a.c;
   const long nv = (long)a.lanes * per / V;
-  for (long g = (long)blockIdx.x * blockDim.x + threadIdx.x; g < nv;
-       g += (long)gridDim.x * blockDim.x) {
+  for (long g = blk * blockDim.x + threadIdx.x; g < nv; g += nblk * blockDim.x) {
     long e = g * V;
     int ln = (int)(e / per);
     long off = e - (long)ln * per;
@@ -367,8 +369,7 @@ __global__ __launch_bounds__(256) void eltwise_kernel(EltArgs a) {
   }
 }
 
-hipError_t launch_eltwise(const EltArgs &a, hipStream_t s) {
-  long n = (long)a.lanes * a.oh * a.ow * a.c;
+bool eltwise_vec(const EltArgs &a) {
   bool vec = a.c % 4 == 0 && (a.mode != ELT_CONCAT || (a.ca % 4 == 0 && a.cb % 4 == 0));
   // Flat modes need whole vectors inside each lane's tensor.
   if (a.mode == ELT_ADD || a.mode == ELT_MUL || a.mode == ELT_ACT)
@@ -376,13 +377,31 @@ hipError_t launch_eltwise(const EltArgs &a, hipStream_t s) {
   auto a16 = [](const void *p) { return p == nullptr || (uintptr_t(p) & 15) == 0; };
   if (!a16(a.a) || !a16(a.b) || !a16(a.g) || !a16(a.y)) vec = false;
   if (vec && (a.a_lane_stride % 4 || a.b_lane_stride % 4 || a.y_lane_stride % 4)) vec = false;
-  long nv = vec ? n / 4 : n;
-  unsigned blocks = blocks_for(nv, 256);
-  if (blocks > 65536u * 4) blocks = 65536u * 4;
-  if (vec) hipLaunchKernelGGL(eltwise_kernel<4>, dim3(blocks), dim3(256), 0, s, a);
-  else hipLaunchKernelGGL(eltwise_kernel<1>, dim3(blocks), dim3(256), 0, s, a);
+  return vec;
+}
+
+hipError_t launch_eltwise_group(const EltArgs *as, int n, hipStream_t s) {
+  if (n < 1 || n > kGroupMax) return hipErrorInvalidValue;
+  const bool vec = eltwise_vec(as[0]);
+  Group<EltArgs> grp{};
+  grp.n = n;
+  long blocks = 0;
+  for (int p = 0; p < n; p++) {
+    if (eltwise_vec(as[p]) != vec) return hipErrorInvalidValue;
+    const long e = (long)as[p].lanes * as[p].oh * as[p].ow * as[p].c;
+    long b = blocks_for(vec ? e / 4 : e, 256);
+    if (b > 65536L * 4) b = 65536L * 4;
+    grp.first[p] = (int)blocks;
+    blocks += b;
+    grp.a[p] = as[p];
+  }
+  grp.first[n] = (int)blocks;
+  if (vec) hipLaunchKernelGGL(eltwise_kernel<4>, dim3((unsigned)blocks), dim3(256), 0, s, grp);
+  else hipLaunchKernelGGL(eltwise_kernel<1>, dim3((unsigned)blocks), dim3(256), 0, s, grp);
   return hipGetLastError();
 }
+
+hipError_t launch_eltwise(const EltArgs &a, hipStream_t s) { return launch_eltwise_group(&a, 1, s); }
 
 // ------------------------------------------------------------ pooling
 
@@ -448,11 +467,15 @@ hipError_t launch_pool(const PoolArgs &a, hipStream_t s) {
 // Pass 1: a block sums a run of `chunk` pixels of one lane for every channel
 // in f64; threads split into `rows` pixel strides of `c` channels, joined in
 // a fixed order in LDS.
-__global__ __launch_bounds__(256) void mean_partial(const float *x, long x_lane_stride, int pixels,
-                                                   int c, int chunk, int chunks, double *partial) {
+__global__ __launch_bounds__(256) void mean_partial(Group<MeanJob> grp) {
   __shared__ double sums[256];
-  int ln = blockIdx.y, run = blockIdx.x;
-  const float *xl = x + (long)ln * x_lane_stride;
+  const int prob = group_problem(grp);
+  const MeanJob &j = grp.a[prob];
+  const int pixels = j.pixels, c = j.c, chunk = grp.x[prob], chunks = j.chunks;
+  double *partial = j.partial;
+  const int blk = (int)blockIdx.x - grp.first[prob];
+  int ln = blk / chunks, run = blk - ln * chunks;
+  const float *xl = j.x + (long)ln * j.x_lane_stride;
   int p0 = run * chunk, p1 = min(p0 + chunk, pixels);
   double *out = partial + ((long)ln * chunks + run) * c;
   for (int c0 = 0; c0 < c; c0 += 256) {
@@ -514,16 +537,21 @@ __device__ __forceinline__ float se_column(const float *w, int stride, const flo
 // larger layer reads its weights from global memory.
 constexpr int kSeStage = 16384;
 
-__global__ __launch_bounds__(1024) void mean_finish(const double *partial, int pixels, int c,
-                                                   int chunks, SeArgs se, int has_se, float *y,
-                                                   long y_lane_stride) {
+__global__ __launch_bounds__(1024) void mean_finish(Group<MeanJob> grp) {
   extern __shared__ float smem[];
   __shared__ double red[1024];
+  const int prob = group_problem(grp);
+  const MeanJob &j = grp.a[prob];
+  const double *partial = j.partial;
+  const int pixels = j.pixels, c = j.c, chunks = j.chunks, has_se = j.has_se;
+  const SeArgs &se = j.se;
+  float *y = j.y;
+  const long y_lane_stride = j.y_lane_stride;
   float *mean = smem;             // c
   float *hid = smem + c;          // mid
   float *w1s = hid + se.mid;      // c * mid when staged
   float *w2s = w1s + kSeStage;    // mid * cout when staged
-  const int ln = blockIdx.x, t = threadIdx.x;
+  const int ln = (int)blockIdx.x - grp.first[prob], t = threadIdx.x;
   // Both layers' weights are requested first, so that their loads overlap
   // the partial sums' instead of following them.
   constexpr int PER = kSeStage / 1024;
@@ -603,23 +631,38 @@ size_t mean_partial_doubles(int pixels, int c, int lanes) {
   return (size_t)lanes * chunks * c;
 }
 
-hipError_t launch_mean(const float *x, long x_lane_stride, int pixels, int c, int lanes,
-                       double *partial, const SeArgs *se, float *y, long y_lane_stride,
-                       hipStream_t s) {
-  int chunk = mean_chunk(pixels);
-  int chunks = (pixels + chunk - 1) / chunk;
-  hipLaunchKernelGGL(mean_partial, dim3(chunks, lanes), dim3(256), 0, s, x, x_lane_stride, pixels,
-                     c, chunk, chunks, partial);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  return launch_mean_finish(partial, pixels, c, chunks, lanes, se, y, y_lane_stride, s);
-}
-
-hipError_t launch_mean_finish(const double *partial, int pixels, int c, int chunks, int lanes,
-                              const SeArgs *se, float *y, long y_lane_stride, hipStream_t s) {
-  SeArgs none{};
-  size_t shm = (size_t)(c + (se ? se->mid + 2 * kSeStage : 0)) * sizeof(float);
+// Jobs whose partial sums are not there yet get the first pass (one launch
+// for all of them), then every job the second (one launch).
+hipError_t launch_mean_group(const MeanJob *jobs, int n, hipStream_t s) {
+  if (n < 1 || n > kGroupMax) return hipErrorInvalidValue;
+  Group<MeanJob> first{}, second{};
+  long b1 = 0, b2 = 0;
+  size_t shm = 0;
+  for (int p = 0; p < n; p++) {
+    MeanJob j = jobs[p];
+    if (j.lanes < 1 || j.c < 1) return hipErrorInvalidValue;
+    if (j.x) {
+      const int chunk = mean_chunk(j.pixels);
+      j.chunks = (j.pixels + chunk - 1) / chunk;
+      first.first[first.n] = (int)b1;
+      first.x[first.n] = chunk;
+      first.a[first.n++] = j;
+      b1 += (long)j.chunks * j.lanes;
+    }
+    second.first[p] = (int)b2;
+    second.a[p] = j;
+    b2 += j.lanes;
+    shm = std::max(shm, (size_t)(j.c + (j.has_se ? j.se.mid + 2 * kSeStage : 0)) * sizeof(float));
+  }
+  second.n = n;
+  first.first[first.n] = (int)b1;
+  second.first[n] = (int)b2;
   if (shm > (size_t)kMaxLds - 1024 * sizeof(double)) return hipErrorInvalidValue;
+  if (first.n) {
+    hipLaunchKernelGGL(mean_partial, dim3((unsigned)b1), dim3(256), 0, s, first);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
   static bool raised = false;  // once per process: the limit is a property of the kernel
   if (!raised) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(mean_finish),
@@ -628,9 +671,29 @@ hipError_t launch_mean_finish(const double *partial, int pixels, int c, int chun
     if (e != hipSuccess) return e;
     raised = true;
   }
-  hipLaunchKernelGGL(mean_finish, dim3(lanes), dim3(1024), shm, s, partial, pixels, c, chunks,
-                     se ? *se : none, se ? 1 : 0, y, y_lane_stride);
+  hipLaunchKernelGGL(mean_finish, dim3((unsigned)b2), dim3(1024), shm, s, second);
   return hipGetLastError();
+}
+
+hipError_t launch_mean(const float *x, long x_lane_stride, int pixels, int c, int lanes,
+                       double *partial, const SeArgs *se, float *y, long y_lane_stride,
+                       hipStream_t s) {
+  MeanJob j{};
+  j.x = x, j.x_lane_stride = x_lane_stride, j.pixels = pixels, j.c = c, j.lanes = lanes;
+  j.partial = partial;
+  if (se) j.se = *se, j.has_se = 1;
+  j.y = y, j.y_lane_stride = y_lane_stride;
+  return launch_mean_group(&j, 1, s);
+}
+
+hipError_t launch_mean_finish(const double *partial, int pixels, int c, int chunks, int lanes,
+                              const SeArgs *se, float *y, long y_lane_stride, hipStream_t s) {
+  MeanJob j{};
+  j.pixels = pixels, j.c = c, j.lanes = lanes, j.chunks = chunks;
+  j.partial = const_cast<double *>(partial);  // read only: x is null
+  if (se) j.se = *se, j.has_se = 1;
+  j.y = y, j.y_lane_stride = y_lane_stride;
+  return launch_mean_group(&j, 1, s);
 }
 
 // ------------------------------------------------------------ layer norm

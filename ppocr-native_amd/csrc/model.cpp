@@ -90,6 +90,8 @@ struct Step {
   size_t wt_off = 0, wt_k = 0;
 };
 
+enum GroupKind { GK_NONE = 0, GK_RING, GK_PATCH, GK_MEAN, GK_ELT };
+
 struct Launch {
   std::string name;
   int op;
@@ -104,6 +106,18 @@ struct Launch {
   // and bytes it must move (each input and the weights read once, each
   // output written once), for roofline fractions.
   double flops = 0, bytes = 0;
+  // Grouping: a launch of kind gk may run together with launches of the
+  // same kind and key that neither depend on it nor it on them, as one
+  // grouped launch (a grid over all their blocks). Its arguments:
+  int gk = GK_NONE;
+  long gkey = 0;
+  ConvArgs conv{};   // GK_RING, GK_PATCH
+  RingTile rt{};     // GK_RING
+  int bk = 0, bn = 0;  // GK_PATCH
+  MeanJob mean{};    // GK_MEAN
+  EltArgs elt{};     // GK_ELT
+  // A grouped launch: the launches of build order it runs.
+  std::vector<int> members;
 };
 
 // A batch of lanes of one size.
@@ -146,6 +160,10 @@ struct Model {
   // a host crash on the 960 x 960 detector whose cause is not found yet;
   // every launch then goes on `stream` in plan order.
   static constexpr bool kConcurrent = false;
+  // Whether independent launches of one kind run as grouped launches (on
+  // `stream`, in a topological order of the groups); homes are then reused
+  // only where that adds no ordering, as for kConcurrent.
+  static constexpr bool kGrouped = true;
   hipStream_t side[kSide] = {};
   hipEvent_t fork = nullptr, join[kSide] = {};
   Plan plan;
@@ -177,6 +195,7 @@ struct Model {
   bool arrange(Batch &b, std::string &err);
   void build_launches(Batch &b);
   void account(Batch &b) const;
+  void group(Batch &b) const;
   bool run(bool copy_in, bool copy_out, std::string &err);
   std::vector<size_t> step_reads(const Step &s) const;
   size_t step_writes(const Step &s) const;
@@ -658,7 +677,7 @@ bool Model::arrange(Batch &b, std::string &err) {
   auto place = [&](size_t need, size_t i) {
     need = round_up(std::max<size_t>(need, 1), 64);
     auto allowed = [&](size_t h) {
-      if (!kConcurrent) return true;
+      if (!kConcurrent && !kGrouped) return true;
       for (size_t r : held_by[h])
         if (i == SIZE_MAX || !anc[i][r]) return false;
       return true;
@@ -754,6 +773,7 @@ bool Model::arrange(Batch &b, std::string &err) {
   }
   build_launches(b);
   account(b);
+  group(b);
   return true;
 }
 
@@ -821,6 +841,8 @@ void Model::build_launches(Batch &b) {
           b.launches.push_back({"conv_patch", s.op, [a, wr, bk, bn](hipStream_t st) {
                                   return launch_conv_patch(a, wr, bk, bn, st);
                                 }});
+          Launch &l = b.launches.back();
+          l.gk = GK_PATCH, l.gkey = bk * 1000 + bn, l.conv = a, l.bk = bk, l.bn = bn;
           break;
         }
         long M = long(L) * a.oh * a.ow;
@@ -829,6 +851,8 @@ void Model::build_launches(Batch &b) {
           const RingTile rt = ring_tile(M, a.n);
           const char *nm = op.kind == K_CONVTRANSPOSE ? "convt_gemm" : (t.pointwise ? "pointwise_gemm" : "conv_gemm");
           b.launches.push_back({nm, s.op, [a, rt](hipStream_t st) { return launch_conv_ring(a, rt, st); }});
+          Launch &l = b.launches.back();
+          l.gk = GK_RING, l.gkey = (a.gate ? 1 : 0) + (s.ring ? 2 : 0), l.conv = a, l.rt = rt;
           break;
         }
         long tiles = (M + 127) / 128 * ((a.n + t.bn - 1) / t.bn);
@@ -911,6 +935,7 @@ void Model::build_launches(Batch &b) {
         static const char *names[] = {"add", "channel_mul", "upsample", "upsample_add", "concat",
                                       "residual_gate", "upsample_add_gate", "mul", "activation"};
         b.launches.push_back({names[s.elt], s.op, [a](hipStream_t st) { return launch_eltwise(a, st); }});
+        b.launches.back().gk = GK_ELT, b.launches.back().gkey = eltwise_vec(a) ? 1 : 0, b.launches.back().elt = a;
         break;
       }
       case S_POOL: {
@@ -940,12 +965,18 @@ void Model::build_launches(Batch &b) {
                                   return launch_mean_finish(part, pixels, c, chunks, L, se ? &sa : nullptr, Y, ys,
                                                             st);
                                 }});
+          Launch &l = b.launches.back();
+          l.gk = GK_MEAN;
+          l.mean = MeanJob{nullptr, 0, pixels, c, int(L), chunks, part, sa, se ? 1 : 0, Y, ys};
           break;
         }
         b.launches.push_back({se ? "se_squeeze" : "channel_mean", s.op,
                               [=](hipStream_t st) {
                                 return launch_mean(x, xs, pixels, c, L, part, se ? &sa : nullptr, Y, ys, st);
                               }});
+        Launch &l = b.launches.back();
+        l.gk = GK_MEAN;
+        l.mean = MeanJob{x, xs, pixels, c, int(L), 0, part, sa, se ? 1 : 0, Y, ys};
         break;
       }
       case S_LN: {
@@ -1054,6 +1085,166 @@ void Model::link(Batch &b) const {
   for (const Launch &l : b.launches)
     for (int d : l.deps)
       if (!b.done[size_t(d)]) hipEventCreateWithFlags(&b.done[size_t(d)], hipEventDisableTiming);
+}
+
+// Independent launches of one kind as grouped launches. Kind by kind (the
+// costliest first) and in build order, a groupable launch joins the first
+// earlier group of its kind and key that has room, none of whose launches it
+// depends on or depend on it, and whose growth keeps the order between
+// groups acyclic. The groups then run in a
+// topological order, among the ready ones the one built first. A grouped
+// launch's work is its members' sum; it is named after its first member.
+void Model::group(Batch &b) const {
+  if (!kGrouped) return;
+  const int n = int(b.launches.size());
+  std::vector<std::vector<char>> reach(static_cast<size_t>(n), std::vector<char>(static_cast<size_t>(n), 0));
+  for (int j = 0; j < n; j++)
+    for (int d : b.launches[size_t(j)].deps) {
+      reach[size_t(j)][size_t(d)] = 1;
+      for (int k = 0; k < n; k++)
+        if (reach[size_t(d)][size_t(k)]) reach[size_t(j)][size_t(k)] = 1;
+    }
+  const size_t N = size_t(n);
+  std::vector<int> gid(N);
+  std::vector<std::vector<int>> groups(N);
+  for (int j = 0; j < n; j++) gid[size_t(j)] = j, groups[size_t(j)] = {j};
+  // The groups in a topological order (empty if there is a cycle).
+  auto order = [&]() {
+    std::vector<int> indeg(N, 0), out_order;
+    std::vector<std::vector<int>> out(N);
+    for (int j = 0; j < n; j++)
+      for (int d : b.launches[size_t(j)].deps) {
+        const int a = gid[size_t(d)], c = gid[size_t(j)];
+        if (a != c) out[size_t(a)].push_back(c), indeg[size_t(c)]++;
+      }
+    std::vector<int> ready;
+    int live = 0;
+    for (int g = 0; g < n; g++)
+      if (!groups[size_t(g)].empty()) {
+        live++;
+        if (indeg[size_t(g)] == 0) ready.push_back(g);
+      }
+    while (!ready.empty()) {
+      auto it = std::min_element(ready.begin(), ready.end());
+      const int g = *it;
+      ready.erase(it);
+      out_order.push_back(g);
+      for (int c : out[size_t(g)])
+        if (--indeg[size_t(c)] == 0) ready.push_back(c);
+    }
+    if (int(out_order.size()) != live) out_order.clear();
+    return out_order;
+  };
+  // The costliest kinds first, so that cheap merges do not order them.
+  for (int kind : {GK_PATCH, GK_RING, GK_MEAN, GK_ELT})
+  for (int j = 0; j < n; j++) {
+    const Launch &l = b.launches[size_t(j)];
+    if (l.gk != kind) continue;
+    for (int g = 0; g < j; g++) {
+      auto &G = groups[size_t(g)];
+      if (G.empty() || int(G.size()) >= kGroupMax) continue;
+      const Launch &f = b.launches[size_t(G[0])];
+      if (f.gk != l.gk || f.gkey != l.gkey) continue;
+      bool independent = true;
+      for (int m : G) independent = independent && !reach[size_t(j)][size_t(m)] && !reach[size_t(m)][size_t(j)];
+      if (!independent) continue;
+      G.push_back(j);
+      groups[size_t(j)].clear();
+      gid[size_t(j)] = g;
+      if (!order().empty()) break;
+      G.pop_back();
+      groups[size_t(j)] = {j};
+      gid[size_t(j)] = j;
+    }
+  }
+  const std::vector<int> seq = order();
+  if (int(seq.size()) == n) return;  // nothing grouped
+  std::vector<Launch> out;
+  std::vector<int> at(N, -1);  // group -> index in out
+  for (int g : seq) {
+    std::vector<int> mem = groups[size_t(g)];
+    at[size_t(g)] = int(out.size());
+    if (mem.size() == 1) {
+      out.push_back(b.launches[size_t(mem[0])]);
+      out.back().members = mem;
+      continue;
+    }
+    Launch gl = b.launches[size_t(mem[0])];
+    gl.members = mem;
+    gl.flops = gl.bytes = 0;
+    for (int m : mem) gl.flops += b.launches[size_t(m)].flops, gl.bytes += b.launches[size_t(m)].bytes;
+    switch (gl.gk) {
+      case GK_RING: {
+        // Longest reductions first; one tile for all, chosen for their rows
+        // together when they share a width, else the first one's.
+        std::sort(mem.begin(), mem.end(), [&](int x, int y) {
+          return b.launches[size_t(x)].conv.ctot * b.launches[size_t(x)].conv.kh * b.launches[size_t(x)].conv.kw >
+                 b.launches[size_t(y)].conv.ctot * b.launches[size_t(y)].conv.kh * b.launches[size_t(y)].conv.kw;
+        });
+        std::vector<ConvArgs> as;
+        long M = 0;
+        bool same_n = true;
+        for (int m : mem) {
+          const ConvArgs &a = b.launches[size_t(m)].conv;
+          as.push_back(a);
+          M += long(a.lanes) * a.oh * a.ow;
+          same_n = same_n && a.n == as[0].n;
+        }
+        RingTile t = same_n ? ring_tile(M, as[0].n) : gl.rt;
+        for (const ConvArgs &a : as)
+          if (!ring_fits(a, t)) t = gl.rt;
+        gl.fn = [as, t](hipStream_t st) { return launch_conv_ring_group(as.data(), int(as.size()), t, st); };
+        break;
+      }
+      case GK_PATCH: {
+        std::vector<ConvArgs> as;
+        long tiles8 = 0;
+        bool fits2 = true;
+        for (int m : mem) {
+          const Launch &x = b.launches[size_t(m)];
+          as.push_back(x.conv);
+          tiles8 += long(x.conv.lanes) * ((x.conv.oh + 7) / 8) * ((x.conv.ow + 15) / 16) * ((x.conv.n + x.bn - 1) / x.bn);
+          fits2 = fits2 && patch_fits(x.conv.kh, x.conv.kw, x.conv.sh, 2, x.bk, x.bn);
+        }
+        const int wr = tiles8 >= 256 && fits2 ? 2 : 1, bk = gl.bk, bn = gl.bn;
+        gl.fn = [as, wr, bk, bn](hipStream_t st) {
+          return launch_conv_patch_group(as.data(), int(as.size()), wr, bk, bn, st);
+        };
+        break;
+      }
+      case GK_MEAN: {
+        std::vector<MeanJob> js;
+        for (int m : mem) js.push_back(b.launches[size_t(m)].mean);
+        gl.fn = [js](hipStream_t st) { return launch_mean_group(js.data(), int(js.size()), st); };
+        break;
+      }
+      case GK_ELT: {
+        std::vector<EltArgs> es;
+        for (int m : mem) es.push_back(b.launches[size_t(m)].elt);
+        gl.fn = [es](hipStream_t st) { return launch_eltwise_group(es.data(), int(es.size()), st); };
+        break;
+      }
+      default:
+        break;
+    }
+    out.push_back(std::move(gl));
+  }
+  // Dependencies between the new launches, from their members'.
+  for (Launch &l : out) {
+    std::vector<int> deps;
+    for (int m : l.members)
+      for (int d : b.launches[size_t(m)].deps) {
+        const int t = at[size_t(gid[size_t(d)])];
+        if (t != int(&l - out.data())) deps.push_back(t);
+      }
+    std::sort(deps.begin(), deps.end());
+    deps.erase(std::unique(deps.begin(), deps.end()), deps.end());
+    l.deps = deps;
+  }
+  for (hipEvent_t e : b.done)
+    if (e) hipEventDestroy(e);
+  b.done.assign(out.size(), nullptr);
+  b.launches = std::move(out);
 }
 
 // Each launch's algorithmic work, in the order build_launches made them.
