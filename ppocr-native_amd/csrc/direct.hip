@@ -10,6 +10,8 @@
 
 namespace ppocr {
 
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
 // Thread = one output pixel of one lane; block row blockIdx.y = a group of
 // eight output channels, whose weights the block stages in LDS first (every
 // thread of the block reads the same ones). Order per output
@@ -181,9 +183,105 @@ __global__ __launch_bounds__(256) void conv_stem_kernel(DirectArgs a) {
   }
 }
 
+// A windowed convolution over a few channels per tap (IC a multiple of 4) to
+// OC outputs (a multiple of 4): thread = one output pixel and all its
+// outputs; the weights [k][oc] in LDS, read four columns at a time; the
+// whole window loaded before the first sum. Order per output as the engine's
+// vector dense kernel (src/engine/kernels/dense.rs:23-147): the bias first
+// for pixels left of first_end, the taps [ky][kx] and their channels in
+// order, a tap outside the image reading zeros, a fused multiply-add for
+// columns below OC / 8 * 8 and a separate multiply and add above, a bias
+// not taken first added last. The block's 256 pixels x OC outputs leave
+// through LDS as whole float4 rows.
+template <int KH, int KW, int IC, int OC>
+__global__ __launch_bounds__(256) void conv_direct_pix(DirectArgs a) {
+  static_assert(IC % 4 == 0 && OC % 4 == 0, "four channels at a time");
+  constexpr int T = KH * KW, K = T * IC, FUSED = OC / 8 * 8;
+  __shared__ __attribute__((aligned(16))) float ws[K * OC];
+  __shared__ __attribute__((aligned(16))) float out[256 * OC];
+  for (int e = threadIdx.x; e < K * OC; e += 256) ws[e] = a.w[e];
+  __syncthreads();
+  const int per = a.oh * a.ow, total = a.lanes * per;
+  const int g0 = blockIdx.x * 256, g = g0 + threadIdx.x;
+  if (g < total) {
+    const int ln = g / per, rem = g - ln * per;
+    const int oy = rem / a.ow, ox = rem - oy * a.ow;
+    const float *x = a.x + (long)ln * a.x_lane_stride;
+    // Tap t's IC channels, zeros outside the image.
+    auto load = [&](int t, f32x4 *v) {
+      const int ky = t / KW, kx = t - ky * KW;
+      const int iy = oy * a.sh + ky - a.pt, ix = ox * a.sw + kx - a.pl;
+      const bool ok = iy >= 0 && iy < a.ih && ix >= 0 && ix < a.iw;
+      const f32x4 *px = reinterpret_cast<const f32x4 *>(x + ((long)iy * a.iw + ix) * IC);
+#pragma unroll
+      for (int q = 0; q < IC / 4; q++) v[q] = ok ? px[q] : f32x4{0.f, 0.f, 0.f, 0.f};
+    };
+    const bool early = ox < a.first_end;
+    float acc[OC];
+#pragma unroll
+    for (int j = 0; j < OC; j++) acc[j] = a.bias && early ? a.bias[j] : 0.0f;
+    // A runtime loop over the taps, the next tap's channels requested before
+    // the current tap's sums (a fully unrolled window lets the compiler
+    // hoist every weight read and product at once and spill them).
+    f32x4 cur[IC / 4], nxt[IC / 4];
+    load(0, cur);
+#pragma unroll 1
+    for (int t = 0; t < T; t++) {
+      load(t + 1 < T ? t + 1 : t, nxt);
+#pragma unroll
+      for (int i = 0; i < IC; i++) {
+        const float v = cur[i / 4][i % 4];
+        const float *wr = ws + (t * IC + i) * OC;
+#pragma unroll
+        for (int j = 0; j < OC; j += 4) {
+          const f32x4 w = *reinterpret_cast<const f32x4 *>(wr + j);
+#pragma unroll
+          for (int q = 0; q < 4; q++)
+            acc[j + q] = j + q < FUSED ? fmaf(w[q], v, acc[j + q]) : acc[j + q] + w[q] * v;
+        }
+      }
+#pragma unroll
+      for (int q = 0; q < IC / 4; q++) cur[q] = nxt[q];
+    }
+    f32x4 *o = reinterpret_cast<f32x4 *>(out + threadIdx.x * OC);
+#pragma unroll
+    for (int j = 0; j < OC; j += 4) {
+      float r[4];
+#pragma unroll
+      for (int q = 0; q < 4; q++) r[q] = act(a.bias && !early ? acc[j + q] + a.bias[j + q] : acc[j + q], a.act);
+      o[j / 4] = f32x4{r[0], r[1], r[2], r[3]};
+    }
+  }
+  __syncthreads();
+  const int n = min(256, total - g0);
+  const int l0 = g0 / per, l1 = (g0 + n - 1) / per;
+  if (l0 == l1) {
+    f32x4 *dst = reinterpret_cast<f32x4 *>(a.y + (long)l0 * a.y_lane_stride + (long)(g0 - l0 * per) * OC);
+    const f32x4 *src = reinterpret_cast<const f32x4 *>(out);
+    for (int e = threadIdx.x; e < n * OC / 4; e += 256) dst[e] = src[e];
+  } else {
+    for (int e = threadIdx.x; e < n * OC; e += 256) {
+      const int p = g0 + e / OC, ln = p / per, rem = p - ln * per;
+      a.y[(long)ln * a.y_lane_stride + (long)rem * OC + e % OC] = out[e];
+    }
+  }
+}
+
+// Measured on the detector's stem: 12 -> 24 beats the implicit GEMM (19.8
+// against 28.6 us at 480 x 480); 24 -> 12, whose last four columns take a
+// separate multiply and add, does not (23.6 against 21.9 us).
+bool direct_pix_supported(int kh, int kw, int ic, int oc) { return kh == 2 && kw == 2 && ic == 12 && oc == 24; }
+
 hipError_t launch_conv_direct(const DirectArgs &a, hipStream_t s) {
   const long n = (long)a.lanes * a.oh * a.ow;
   if (n <= 0 || a.oc <= 0) return hipSuccess;
+  const unsigned nb = (unsigned)((n + 255) / 256);
+  if (direct_pix_supported(a.kh, a.kw, a.ic, a.oc) && n <= 0x7fffff00L && a.fused == a.oc / 8 * 8 &&
+      (reinterpret_cast<uintptr_t>(a.x) & 15) == 0 && a.x_lane_stride % 4 == 0 &&
+      (reinterpret_cast<uintptr_t>(a.y) & 15) == 0 && a.y_lane_stride % 4 == 0) {
+    hipLaunchKernelGGL((conv_direct_pix<2, 2, 12, 24>), dim3(nb), dim3(256), 0, s, a);
+    return hipGetLastError();
+  }
   if (!direct_supported(a.kh, a.kw, a.ic) || n > 0x7fffff00L || (a.oc + 7) / 8 > 65535)
     return hipErrorInvalidValue;
   const bool stem = a.kh == 3 && a.kw == 3 && a.ic == 3 && a.first_end >= a.ow && a.fused >= a.oc &&

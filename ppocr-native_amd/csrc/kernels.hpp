@@ -243,6 +243,9 @@ struct DirectArgs {
   float *y; long y_lane_stride;
 };
 bool direct_supported(int kh, int kw, int ic);
+// The window shapes the direct kernel also takes with four or more channels
+// (each output pixel's outputs from one thread).
+bool direct_pix_supported(int kh, int kw, int ic, int oc);
 hipError_t launch_conv_direct(const DirectArgs &a, hipStream_t s);
 
 // Two 2x2 stride-2 transposed convolutions in a row: ic -> oc1 (act1), then

@@ -405,7 +405,9 @@ bool Model::build_steps(std::string &err) {
         // A windowed convolution over a few channels that are not a multiple
         // of four (the RGB stem): computed directly.
         if (s.gate < 0 && s.add < 0 && op.n2 == 0 && s.sources.size() == 1 && s.sources[0].shift == 0 &&
-            !op.is_pointwise() && op.ic % 4 != 0 && direct_supported(int(op.kh), int(op.kw), int(op.ic)))
+            !op.is_pointwise() &&
+            ((op.ic % 4 != 0 && direct_supported(int(op.kh), int(op.kw), int(op.ic))) ||
+             direct_pix_supported(int(op.kh), int(op.kw), int(op.ic), int(op.oc))))
           s.kind = S_DIRECT;
         break;
       }

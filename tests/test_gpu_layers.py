@@ -280,11 +280,13 @@ def test_pools_exact(oracle, c):
     (3, 24, 2, 2, 0, (12, 14)),
     (6, 16, 3, 1, 1, (7, 14)),    # bias first except the row's last ow % 4 pixels
     (5, 12, 3, 1, 1, (8, 13)),    # bias last; columns 8..11 multiply and add apart
+    (12, 24, 2, 1, (0, 1, 0, 1), (17, 40)),  # the stem's 12 -> 24 2 x 2: one thread per pixel
 ])
 def test_direct_conv_exact(oracle, ci, co, k, s, pad, hw):
     w = RNG.normal(0, 0.3, (k, k, ci, co)).astype(np.float32)
     bias = RNG.normal(0, 0.3, co).astype(np.float32)
-    got, want = both(lambda b, t: b.conv(t, w, bias, k=(k, k), s=(s, s), pad=(pad,) * 4,
+    pad = pad if isinstance(pad, tuple) else (pad,) * 4
+    got, want = both(lambda b, t: b.conv(t, w, bias, k=(k, k), s=(s, s), pad=pad,
                                          fused="hardswish"), (*hw, ci), oracle)
     exact(got, want)
 
