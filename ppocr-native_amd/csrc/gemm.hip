@@ -404,7 +404,7 @@ __global__ __launch_bounds__(256) void conv_patch(Group<ConvArgs> grp) {
   const int taps = a.kh * a.kw;
   const int PR = (TH - 1) * a.sh + a.kh, PC = (TW - 1) * a.sw + a.kw;
   float *P = lds;                      // PR * PC pixels x S
-  float *Bs = lds + PR * PC * S;       // BN x taps x S
+  float *Bs = lds + PR * PC * S;       // nr x taps x S, then one zero row of S
 
   const int ntn = (a.n + BN - 1) / BN;
   int t = (int)blockIdx.x - grp.first[prob];
@@ -418,6 +418,18 @@ __global__ __launch_bounds__(256) void conv_patch(Group<ConvArgs> grp) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int li = lane & 15, lg = lane >> 4;
   const int iy0 = ty0 * a.sh - a.pt, ix0 = tx0 * a.sw - a.pl;
+  // Columns of this tile that exist: only their weights are staged; the MFMA
+  // lanes of the others read the zero row.
+  const int nr = min(BN, a.n - n0);
+  float *Z = Bs + nr * taps * S;
+  if (tid < S) Z[tid] = 0.0f;
+  int bbase[NT], bstep[NT];
+#pragma unroll
+  for (int j = 0; j < NT; j++) {
+    const int n = j * 16 + li;
+    bbase[j] = n < nr ? n * taps * S : nr * taps * S;
+    bstep[j] = n < nr ? S : 0;
+  }
 
   f32x4 acc[WR][NT];
 #pragma unroll
@@ -465,10 +477,11 @@ __global__ __launch_bounds__(256) void conv_patch(Group<ConvArgs> grp) {
     for (int u = 0; u < PPAIRS; u++) {
       const int pr = tid + 256 * u;
       const int n = pr / CQ, qq = pr - n * CQ;
-      const float *wsrc = a.wt + (long)(n0 + (pr < PAIRS ? n : 0)) * a.wt_k + (long)cc * CB + qq * 4;
+      const bool real = pr < PAIRS && n < nr;
+      const float *wsrc = a.wt + (long)(n0 + (real ? n : 0)) * a.wt_k + (long)cc * CB + qq * 4;
 #pragma unroll
       for (int tp = 0; tp < kWeightPer / PPAIRS; tp++)
-        if (pr < PAIRS && tp < taps) rw[u * (kWeightPer / PPAIRS) + tp] = *reinterpret_cast<const f32x4 *>(wsrc + tp * wstep);
+        if (real && tp < taps) rw[u * (kWeightPer / PPAIRS) + tp] = *reinterpret_cast<const f32x4 *>(wsrc + tp * wstep);
     }
   };
   auto store = [&]() {
@@ -481,7 +494,7 @@ __global__ __launch_bounds__(256) void conv_patch(Group<ConvArgs> grp) {
       const int n = pr / CQ, qq = pr - n * CQ;
 #pragma unroll
       for (int tp = 0; tp < kWeightPer / PPAIRS; tp++)
-        if (pr < PAIRS && tp < taps)
+        if (pr < PAIRS && n < nr && tp < taps)
           *reinterpret_cast<f32x4 *>(Bs + (n * taps + tp) * S + qq * 4) = rw[u * (kWeightPer / PPAIRS) + tp];
     }
   };
@@ -505,7 +518,7 @@ __global__ __launch_bounds__(256) void conv_patch(Group<ConvArgs> grp) {
         }
 #pragma unroll
         for (int j = 0; j < NT; j++)
-          bv[j] = *reinterpret_cast<const KT *>(Bs + ((j * 16 + li) * taps + tp) * S + lg * KS + r * KW);
+          bv[j] = *reinterpret_cast<const KT *>(Bs + bbase[j] + tp * bstep[j] + lg * KS + r * KW);
 #pragma unroll
         for (int k = 0; k < KW; k++) {
 #pragma unroll
@@ -1087,7 +1100,7 @@ bool patch_fits(int kh, int kw, int stride, int wr, int bk, int bn) {
   const int pr = (4 * wr - 1) * stride + kh, pc = 15 * stride + kw;
   if ((pr * pc + pstep - 1) / pstep > kPatchPer) return false;
   if (kWeightPer % pairs || kh * kw > kWeightPer / pairs) return false;
-  return size_t(pr * pc + bn * kh * kw) * (bk + 4) * sizeof(float) <= 160 * 1024;
+  return size_t(pr * pc + bn * kh * kw + 1) * (bk + 4) * sizeof(float) <= 160 * 1024;
 }
 
 bool patch_supported(const ConvArgs &a, int wr, int bk, int bn) {
@@ -1099,7 +1112,8 @@ bool patch_supported(const ConvArgs &a, int wr, int bk, int bn) {
 
 size_t patch_lds_bytes(const ConvArgs &a, int wr, int bk, int bn) {
   const size_t pr = size_t(4 * wr - 1) * a.sh + a.kh, pc = size_t(15) * a.sw + a.kw;
-  return (pr * pc + size_t(bn) * a.kh * a.kw) * (bk + 4) * sizeof(float);
+  const size_t nr = size_t(std::min(bn, a.n));  // staged columns; the zero row besides
+  return (pr * pc + nr * a.kh * a.kw + 1) * (bk + 4) * sizeof(float);
 }
 
 template <int WR, int BN, int CB>
