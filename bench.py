@@ -28,11 +28,11 @@ PEAK_FP32_MFMA_TFLOPS = 157.3
 GEMM_LAUNCHES = {"pointwise_gemm", "conv_gemm", "conv_patch", "convt_gemm", "ctc_gemm"}
 # HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE,
 # scaled by a plain copy kernel's counters (x2.0 / x1.0), for the launches
-# the bench reports a roofline of: (kernel, plan operation) -> (read, write)
+# the bench reports a roofline of: (kernel, plan operations) -> (read, write)
 # KiB and the profile summary the numbers come from.
 MEASURED_TRAFFIC = {
-    ("conv_patch", 83): (30830, 5400, "profiles/conv_patch_240x240_3x3_96to24_hbm_counters.md"),
-    ("conv_patch", 94): (12738, 5400, "profiles/conv_patch_240x240_3x3_96to24_hbm_counters.md"),
+    ("conv_patch", (65, 71, 77, 83)): (46514, 7172, "profiles/conv_patch_neck_group_and_head_3x3_hbm_counters.md"),
+    ("conv_patch", (94,)): (12544, 5400, "profiles/conv_patch_neck_group_and_head_3x3_hbm_counters.md"),
 }
 
 
@@ -62,14 +62,23 @@ def roofline(name: str, flops: float, nbytes: float, ms: float) -> dict:
 
 def profile(model, repeats: int) -> list[dict]:
     names = model.launches()
+    ops = model.launch_ops()
     work = model.launch_work()
     times = model.profile_launches(repeats)
     rows = []
-    for (name, op), (fl, by), ms in zip(names, work, times):
-        r = {"name": name, "op": op, "ms": ms, "flops": fl, "bytes": by}
+    for (name, op), members, (fl, by), ms in zip(names, ops, work, times):
+        r = {"name": name, "op": op, "ops": members, "ms": ms, "flops": fl, "bytes": by}
         r.update(roofline(name, fl, by, ms))
         rows.append(r)
     return rows
+
+
+def launch_label(r: dict) -> str:
+    """A launch's kernel and plan operations (a grouped launch runs several)."""
+    ops = r.get("ops") or [r["op"]]
+    if len(ops) == 1:
+        return f"{r['name']} (op {ops[0]})"
+    return f"{r['name']} x{len(ops)} (ops {', '.join(str(o) for o in ops)})"
 
 
 def by_kernel(rows: list[dict]) -> dict:
@@ -359,15 +368,15 @@ def main() -> int:
         "eager_ms_per_step": round(det_eager, 4),
         "with_host_copies_img_per_s": round(1e3 / pcie_ms, 2),
     }
-    measured = MEASURED_TRAFFIC.get((dom["name"], dom["op"]))
+    measured = MEASURED_TRAFFIC.get((dom["name"], tuple(dom["ops"])))
     result["roofline"]["traffic"] = (measured[0] + measured[1]) * 1024 if measured else None
     if measured:
         result["roofline"]["traffic_source"] = measured[2]
         result["roofline"]["algorithmic_bytes"] = round(dom["bytes"])
-    result["roofline"]["kernel"] = f"{dom['name']} (op {dom['op']})"
+    result["roofline"]["kernel"] = launch_label(dom)
     result["roofline"]["launch_ms"] = round(dom["ms"], 5)
     result["det_kernels"] = by_kernel(det_rows)
-    result["det_launches"] = [[r["name"], r["op"], round(r["ms"] * 1e3, 1), r["frac"]] for r in det_rows]
+    result["det_launches"] = [[r["name"], r["ops"], round(r["ms"] * 1e3, 1), r["frac"]] for r in det_rows]
     if args.only in ("rec", "all"):
         log("bench: recogniser 16x3x48x320")
         rec_plan, rec_ms, rec_wall, rec_rows, rec_eager = bench_recognizer(P, nets, args.steps,
@@ -377,9 +386,9 @@ def main() -> int:
                          "unit": "lines/s", "ms_per_batch": round(rec_ms, 4),
                          "eager_ms_per_batch": round(rec_eager, 4),
                          "roofline": {k: rdom[k] for k in ("bound", "achieved", "peak", "unit", "frac")}
-                         | {"kernel": f"{rdom['name']} (op {rdom['op']})"},
+                         | {"kernel": launch_label(rdom)},
                          "kernels": by_kernel(rec_rows),
-                         "launches": [[r["name"], r["op"], round(r["ms"] * 1e3, 1), r["frac"]]
+                         "launches": [[r["name"], r["ops"], round(r["ms"] * 1e3, 1), r["frac"]]
                                       for r in rec_rows]}
         log("bench: fused block, microkernels")
         result["block"] = bench_block(P, nets, args.steps, args.warmup)

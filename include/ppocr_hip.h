@@ -109,6 +109,11 @@ int ppocr_gpu_set_graphs(ppocr_gpu_model *model, int enable);
 size_t ppocr_gpu_launch_count(const ppocr_gpu_model *model);
 const char *ppocr_gpu_launch_name(const ppocr_gpu_model *model, size_t i, size_t *op);
 
+/* The plan operations launch `i` runs: one, or for a grouped launch (layers
+ * of one kind that do not depend on each other, run as one grid) each
+ * member's. Writes up to `cap` of them to `ops` and returns how many there are. */
+size_t ppocr_gpu_launch_ops(const ppocr_gpu_model *model, size_t i, size_t *ops, size_t cap);
+
 /* Launch `i`'s algorithmic work for the lanes of its batch: `*flops` the
  * layer's floating-point operations, `*bytes` what it must move (inputs and
  * weights read once, outputs written once). Returns 0, or 1 for a bad index. */

@@ -67,6 +67,7 @@ def lib() -> C.CDLL:
         "ppocr_gpu_launch_name": ([vp, sz, szp], cp),
         "ppocr_gpu_profile_launches": ([vp, C.c_int, fp, cp, sz], C.c_int),
         "ppocr_gpu_launch_work": ([vp, sz, C.POINTER(C.c_double), C.POINTER(C.c_double)], C.c_int),
+        "ppocr_gpu_launch_ops": ([vp, sz, szp, sz], sz),
         "ppocr_hip_add": ([vp, vp, vp, sz, C.c_int, vp], C.c_int),
         "ppocr_hip_mul": ([vp, vp, vp, sz, vp], C.c_int),
         "ppocr_hip_activation": ([vp, vp, sz, C.c_int, vp], C.c_int),
@@ -197,6 +198,16 @@ class GpuModel:
             op = C.c_size_t()
             name = lib().ppocr_gpu_launch_name(self._h, i, C.byref(op))
             out.append((name.decode(), op.value))
+        return out
+
+    def launch_ops(self) -> list[list[int]]:
+        """The plan operations each launch runs (several for a grouped launch)."""
+        out = []
+        for i in range(lib().ppocr_gpu_launch_count(self._h)):
+            n = lib().ppocr_gpu_launch_ops(self._h, i, None, 0)
+            buf = (C.c_size_t * max(n, 1))()
+            lib().ppocr_gpu_launch_ops(self._h, i, buf, n)
+            out.append([int(buf[k]) for k in range(n)])
         return out
 
     def launch_work(self) -> list[tuple[float, float]]:

@@ -116,8 +116,10 @@ struct Launch {
   int bk = 0, bn = 0;  // GK_PATCH
   MeanJob mean{};    // GK_MEAN
   EltArgs elt{};     // GK_ELT
-  // A grouped launch: the launches of build order it runs.
+  // A grouped launch: the launches of build order it runs, and the plan
+  // operation each of them starts from.
   std::vector<int> members;
+  std::vector<int> member_ops;
 };
 
 // A batch of lanes of one size.
@@ -1186,10 +1188,12 @@ void Model::group(Batch &b) const {
     if (mem.size() == 1) {
       out.push_back(b.launches[size_t(mem[0])]);
       out.back().members = mem;
+      out.back().member_ops = {out.back().op};
       continue;
     }
     Launch gl = b.launches[size_t(mem[0])];
     gl.members = mem;
+    for (int m : mem) gl.member_ops.push_back(b.launches[size_t(m)].op);
     gl.flops = gl.bytes = 0;
     for (int m : mem) gl.flops += b.launches[size_t(m)].flops, gl.bytes += b.launches[size_t(m)].bytes;
     switch (gl.gk) {
@@ -1728,6 +1732,16 @@ const char *ppocr_gpu_launch_name(const ppocr_gpu_model *model, size_t i, size_t
   if (!l) return nullptr;
   if (op) *op = size_t(l->op);
   return l->name.c_str();
+}
+
+size_t ppocr_gpu_launch_ops(const ppocr_gpu_model *model, size_t i, size_t *ops, size_t cap) {
+  if (!model) return 0;
+  const ppocr::Launch *l = launch_at(model, i);
+  if (!l) return 0;
+  const std::vector<int> one{l->op};
+  const std::vector<int> &v = l->member_ops.empty() ? one : l->member_ops;
+  for (size_t k = 0; k < v.size() && k < cap && ops; k++) ops[k] = size_t(v[k]);
+  return v.size();
 }
 
 int ppocr_gpu_launch_work(const ppocr_gpu_model *model, size_t i, double *flops, double *bytes) {
