@@ -180,7 +180,18 @@ hipError_t launch_pool(const PoolArgs &a, hipStream_t s);
 struct SeArgs {
   const float *w1, *b1; int mid, act1;
   const float *w2, *b2; int cout, act2;
+  // The same weights transposed, each output's inputs contiguous: w1t[j][i]
+  // (mid rows of se_row_stride(c) floats), w2t[j][i] (cout rows of
+  // se_row_stride(mid)), zero past the inputs.
+  const float *w1t, *w2t;
 };
+// Row stride of the transposed SE weights for n inputs: n rounded up to 4,
+// plus 4 when that is a multiple of 8 floats, so that sixteen rows read as
+// float4 at one column fall in distinct LDS banks.
+__host__ __device__ inline int se_row_stride(int n) {
+  const int p = (n + 3) & ~3;
+  return (p / 4) % 2 ? p : p + 4;
+}
 size_t mean_partial_doubles(int pixels, int c, int lanes);
 hipError_t launch_mean(const float *x, long x_lane_stride, int pixels, int c, int lanes,
                        double *partial, const SeArgs *se, float *y, long y_lane_stride,

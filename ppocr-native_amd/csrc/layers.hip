@@ -507,80 +507,90 @@ __global__ __launch_bounds__(256) void mean_partial(Group<MeanJob> grp) {
   }
 }
 
-// One output column of a 1x1 layer over one pixel: from zero, inputs in
-// order, fused multiply-adds or separate products and sums. Weights are
-// fetched eight at a time ahead of their sums.
-__device__ __forceinline__ float se_column(const float *w, int stride, const float *in, int n,
-                                           bool fused) {
+// One output of a 1x1 layer over one pixel, from its contiguous weight row
+// (inputs rounded up to 4, in LDS or global memory) and the inputs (LDS):
+// from zero, inputs in order, fused multiply-adds or separate products and
+// sums; eight float4 of weights and inputs read ahead of their sums.
+template <bool FUSED>
+__device__ __forceinline__ float se_row(const float *w, const float *in, int n) {
   float acc = 0.0f;
-  int i = 0;
-  for (; i + 8 <= n; i += 8) {
-    float wv[8];
+  const int n4 = (n + 3) / 4;
+  for (int i4 = 0; i4 < n4; i4 += 8) {
+    f32x4 wv[8], xv[8];
 #pragma unroll
-    for (int k = 0; k < 8; k++) wv[k] = w[(long)(i + k) * stride];
+    for (int k = 0; k < 8; k++)
+      if (i4 + k < n4)
+        wv[k] = *reinterpret_cast<const f32x4 *>(w + 4 * (i4 + k)),
+        xv[k] = *reinterpret_cast<const f32x4 *>(in + 4 * (i4 + k));
 #pragma unroll
-    for (int k = 0; k < 8; k++) acc = fused ? fmaf(wv[k], in[i + k], acc) : acc + in[i + k] * wv[k];
-  }
-  for (; i < n; i++) {
-    float wv = w[(long)i * stride];
-    acc = fused ? fmaf(wv, in[i], acc) : acc + in[i] * wv;
+    for (int k = 0; k < 8; k++) {
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const int i = 4 * (i4 + k) + q;
+        if (i < n) acc = FUSED ? fmaf(wv[k][q], xv[k][q], acc) : acc + xv[k][q] * wv[k][q];
+      }
+    }
   }
   return acc;
 }
 
 // Pass 2: one block per lane joins the partials and divides; with an SE,
 // then the two 1x1 layers of one pixel, each output from zero with a fused
-// multiply-add per input in order, then its bias, then its activation.
-// Each channel's partials are split between J threads (a fixed split, eight
+// multiply-add per input in order (separate product and sum for the columns
+// past cols / 8 * 8, the engine's pointwise rule for one pixel), then its
+// bias, then its activation.
+//
+// The block is latency-bound, so every load it can issue early goes first:
+// each thread requests its share of the transposed weights (kSePer float4)
+// before the partial sums and moves them to LDS once the mean is known.
+// grp.x says how the weights travel: 1 both layers at once, 2 the first,
+// then the second while the first is summed, 0 neither (each output reads
+// its row from global memory, when a layer is larger than LDS). Each
+// channel's partials are split between J threads (a fixed split, eight
 // independent loads in flight per thread), joined in LDS in thread order.
-// Floats of each 1x1 layer's weights that mean_finish stages in LDS; a
-// larger layer reads its weights from global memory.
-constexpr int kSeStage = 16384;
+constexpr int kSePer = 9;
+constexpr int kSeThreads = 1024;
+constexpr int kSeStaged = kSePer * 4 * kSeThreads;  // floats one staging moves at most
 
 __global__ __launch_bounds__(1024) void mean_finish(Group<MeanJob> grp) {
-  extern __shared__ float smem[];
-  __shared__ double red[1024];
+  extern __shared__ __attribute__((aligned(16))) float smem[];
+  __shared__ double red[kSeThreads];
   const int prob = group_problem(grp);
-  const MeanJob &j = grp.a[prob];
-  const double *partial = j.partial;
-  const int pixels = j.pixels, c = j.c, chunks = j.chunks, has_se = j.has_se;
-  const SeArgs &se = j.se;
-  float *y = j.y;
-  const long y_lane_stride = j.y_lane_stride;
-  float *mean = smem;             // c
-  float *hid = smem + c;          // mid
-  float *w1s = hid + se.mid;      // c * mid when staged
-  float *w2s = w1s + kSeStage;    // mid * cout when staged
+  const MeanJob &jb = grp.a[prob];
+  const double *partial = jb.partial;
+  const int pixels = jb.pixels, c = jb.c, chunks = jb.chunks, has_se = jb.has_se, stage = grp.x[prob];
+  const SeArgs &se = jb.se;
+  const int cp = se_row_stride(c), mp = se_row_stride(se.mid);
+  float *mean = smem;         // cp
+  float *hid = mean + cp;     // mp
+  float *W = hid + mp;        // staged weights
   const int ln = (int)blockIdx.x - grp.first[prob], t = threadIdx.x;
-  // Both layers' weights are requested first, so that their loads overlap
-  // the partial sums' instead of following them.
-  constexpr int PER = kSeStage / 1024;
-  const int n1 = has_se ? c * se.mid : 0, n2 = has_se ? se.mid * se.cout : 0;
-  const bool st1 = n1 > 0 && n1 <= kSeStage, st2 = n2 > 0 && n2 <= kSeStage;
-  float r1[PER], r2[PER];
+  const int n1 = has_se ? se.mid * cp : 0, n2 = has_se ? se.cout * mp : 0;
+  const int first = stage == 1 ? n1 + n2 : (stage == 2 ? n1 : 0);
+  f32x4 r[kSePer];
 #pragma unroll
-  for (int k = 0; k < PER; k++) {
-    const int e = t + k * 1024;
-    r1[k] = st1 && e < n1 ? se.w1[e] : 0.0f;
-    r2[k] = st2 && e < n2 ? se.w2[e] : 0.0f;
+  for (int k = 0; k < kSePer; k++) {
+    const int e = 4 * (t + k * kSeThreads);
+    r[k] = e < first ? *reinterpret_cast<const f32x4 *>(e < n1 ? se.w1t + e : se.w2t + (e - n1))
+                     : f32x4{0.f, 0.f, 0.f, 0.f};
   }
   const double *pl = partial + (long)ln * chunks * c;
-  for (int c0 = 0; c0 < c; c0 += 1024) {
-    const int cw = min(1024, c - c0);
-    const int J = 1024 / cw;
+  for (int c0 = 0; c0 < c; c0 += kSeThreads) {
+    const int cw = min(kSeThreads, c - c0);
+    const int J = kSeThreads / cw;
     const int ch = t % cw, j = t / cw;
     double s = 0.0;
     if (j < J) {
       const double *p = pl + c0 + ch;
-      int r = j;
-      for (; r + 7 * J < chunks; r += 8 * J) {
+      int rr = j;
+      for (; rr + 7 * J < chunks; rr += 8 * J) {
         double v[8];
 #pragma unroll
-        for (int k = 0; k < 8; k++) v[k] = p[(long)(r + k * J) * c];
+        for (int k = 0; k < 8; k++) v[k] = p[(long)(rr + k * J) * c];
 #pragma unroll
         for (int k = 0; k < 8; k++) s += v[k];
       }
-      for (; r < chunks; r += J) s += p[(long)r * c];
+      for (; rr < chunks; rr += J) s += p[(long)rr * c];
     }
     red[t] = s;
     __syncthreads();
@@ -591,30 +601,45 @@ __global__ __launch_bounds__(1024) void mean_finish(Group<MeanJob> grp) {
     }
     __syncthreads();
   }
-  float *yl = y + (long)ln * y_lane_stride;
+  float *yl = jb.y + (long)ln * jb.y_lane_stride;
   if (!has_se) {
-    for (int ch = threadIdx.x; ch < c; ch += blockDim.x) yl[ch] = mean[ch];
+    for (int ch = t; ch < c; ch += kSeThreads) yl[ch] = mean[ch];
     return;
   }
+  if (t < cp - c) mean[c + t] = 0.0f;
 #pragma unroll
-  for (int k = 0; k < PER; k++) {
-    const int e = t + k * 1024;
-    if (st1 && e < n1) w1s[e] = r1[k];
-    if (st2 && e < n2) w2s[e] = r2[k];
+  for (int k = 0; k < kSePer; k++) {
+    const int e = 4 * (t + k * kSeThreads);
+    if (e < first) *reinterpret_cast<f32x4 *>(W + e) = r[k];
+  }
+  if (stage == 2) {
+#pragma unroll
+    for (int k = 0; k < kSePer; k++) {
+      const int e = 4 * (t + k * kSeThreads);
+      r[k] = e < n2 ? *reinterpret_cast<const f32x4 *>(se.w2t + e) : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
   }
   __syncthreads();
-  // Columns below co / 8 * 8 fuse their multiply-adds; the tail columns
-  // multiply and add separately (the engine's pointwise rule for one pixel).
-  for (int j = threadIdx.x; j < se.mid; j += blockDim.x) {
-    const bool f = j < se.mid / 8 * 8;
-    float acc = st1 ? se_column(w1s + j, se.mid, mean, c, f) : se_column(se.w1 + j, se.mid, mean, c, f);
+  const float *w1 = stage ? W : se.w1t;
+  for (int j = t; j < se.mid; j += kSeThreads) {
+    float acc = j < se.mid / 8 * 8 ? se_row<true>(w1 + (long)j * cp, mean, c) : se_row<false>(w1 + (long)j * cp, mean, c);
     if (se.b1) acc = acc + se.b1[j];
     hid[j] = act(acc, se.act1);
   }
+  if (t < mp - se.mid) hid[se.mid + t] = 0.0f;
   __syncthreads();
-  for (int j = threadIdx.x; j < se.cout; j += blockDim.x) {
-    const bool f = j < se.cout / 8 * 8;
-    float acc = st2 ? se_column(w2s + j, se.cout, hid, se.mid, f) : se_column(se.w2 + j, se.cout, hid, se.mid, f);
+  if (stage == 2) {
+#pragma unroll
+    for (int k = 0; k < kSePer; k++) {
+      const int e = 4 * (t + k * kSeThreads);
+      if (e < n2) *reinterpret_cast<f32x4 *>(W + e) = r[k];
+    }
+    __syncthreads();
+  }
+  const float *w2 = stage == 1 ? W + n1 : (stage == 2 ? W : se.w2t);
+  for (int j = t; j < se.cout; j += kSeThreads) {
+    float acc = j < se.cout / 8 * 8 ? se_row<true>(w2 + (long)j * mp, hid, se.mid)
+                                    : se_row<false>(w2 + (long)j * mp, hid, se.mid);
     if (se.b2) acc = acc + se.b2[j];
     yl[j] = act(acc, se.act2);
   }
@@ -652,12 +677,29 @@ hipError_t launch_mean_group(const MeanJob *jobs, int n, hipStream_t s) {
     second.first[p] = (int)b2;
     second.a[p] = j;
     b2 += j.lanes;
-    shm = std::max(shm, (size_t)(j.c + (j.has_se ? j.se.mid + 2 * kSeStage : 0)) * sizeof(float));
+    // LDS: the mean and the hidden layer (rounded up to 4), then the staged
+    // weights: both layers, the larger one (one after the other), or none.
+    const size_t cp = size_t(se_row_stride(j.c)), mp = size_t(se_row_stride(j.se.mid));
+    const size_t base = cp + (j.has_se ? mp : 0);
+    const size_t dyn = (kMaxLds - kSeThreads * sizeof(double)) / sizeof(float);
+    if (base > dyn) return hipErrorInvalidValue;
+    int stage = 0;
+    size_t staged = 0;
+    if (j.has_se) {
+      if (!j.se.w1t || !j.se.w2t) return hipErrorInvalidValue;
+      const size_t n1 = size_t(j.se.mid) * cp, n2 = size_t(j.se.cout) * mp;
+      const size_t room = std::min(dyn - base, size_t(kSeStaged));
+      if (n1 + n2 <= room)
+        stage = 1, staged = n1 + n2;
+      else if (std::max(n1, n2) <= room)
+        stage = 2, staged = std::max(n1, n2);
+    }
+    second.x[p] = stage;
+    shm = std::max(shm, (base + staged) * sizeof(float));
   }
   second.n = n;
   first.first[first.n] = (int)b1;
   second.first[n] = (int)b2;
-  if (shm > (size_t)kMaxLds - 1024 * sizeof(double)) return hipErrorInvalidValue;
   if (first.n) {
     hipLaunchKernelGGL(mean_partial, dim3((unsigned)b1), dim3(256), 0, s, first);
     hipError_t e = hipGetLastError();
@@ -667,7 +709,7 @@ hipError_t launch_mean_group(const MeanJob *jobs, int n, hipStream_t s) {
   if (!raised) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(mean_finish),
                                        hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       (int)(kMaxLds - 1024 * sizeof(double)));
+                                       (int)(kMaxLds - kSeThreads * sizeof(double)));
     if (e != hipSuccess) return e;
     raised = true;
   }

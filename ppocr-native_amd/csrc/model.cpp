@@ -88,6 +88,7 @@ struct Step {
   GemmTile tile{};
   int gemm_n = 0, chunks = 0, ctot = 0, cpt = 0;
   size_t wt_off = 0, wt_k = 0;
+  size_t se_w1t = 0, se_w2t = 0;  // S_MEAN with an SE: the transposed 1x1 weights in the packed arena
 };
 
 enum GroupKind { GK_NONE = 0, GK_RING, GK_PATCH, GK_MEAN, GK_ELT };
@@ -517,6 +518,22 @@ bool Model::pack(std::string &err) {
   std::vector<float> packed;
   const auto &ops = plan.ops;
   for (Step &s : steps) {
+    if (s.kind == S_MEAN && s.fc1 >= 0) {
+      // The squeeze-and-excite's two 1x1 layers, each output's weights in a
+      // contiguous row of se_row_stride floats (zeros past the inputs).
+      const Op &f1 = ops[size_t(s.fc1)], &f2 = ops[size_t(s.fc2)];
+      const size_t c = f1.ic, mid = f1.oc, cout = f2.oc;
+      const size_t cp = size_t(se_row_stride(int(c))), mp = size_t(se_row_stride(int(mid)));
+      s.se_w1t = round_up(packed.size(), 64);
+      packed.resize(s.se_w1t + mid * cp, 0.0f);
+      for (size_t j = 0; j < mid; j++)
+        for (size_t i = 0; i < c; i++) packed[s.se_w1t + j * cp + i] = weights[f1.w0 + i * mid + j];
+      s.se_w2t = round_up(packed.size(), 64);
+      packed.resize(s.se_w2t + cout * mp, 0.0f);
+      for (size_t j = 0; j < cout; j++)
+        for (size_t i = 0; i < mid; i++) packed[s.se_w2t + j * mp + i] = weights[f2.w0 + i * cout + j];
+      continue;
+    }
     if (s.kind != S_GEMM && s.kind != S_CTC) continue;
     const Op &op = ops[s.op];
     int taps = 1, N;
@@ -976,7 +993,8 @@ void Model::build_launches(Batch &b) {
         if (se) {
           const Op &f1 = p.ops[s.fc1], &f2 = p.ops[s.fc2];
           sa = SeArgs{W + f1.w0, f1.b1 ? W + f1.b0 : nullptr, int(f1.oc), f1.fused,
-                      W + f2.w0, f2.b1 ? W + f2.b0 : nullptr, int(f2.oc), f2.fused};
+                      W + f2.w0, f2.b1 ? W + f2.b0 : nullptr, int(f2.oc), f2.fused,
+                      dpacked + s.se_w1t, dpacked + s.se_w2t};
         }
         if (s.mean_of_dw >= 0) {
           DwArgs d = dw_shape(p.ops[s.mean_of_dw]);
