@@ -47,16 +47,6 @@ struct CtcState {
   float m, s, b;
 };
 
-__device__ __forceinline__ void ctc_push(CtcState &st, float v, float col) {
-  if (v > st.m) {
-    st.s = st.s * exp_neg(st.m - v) + 1.0f;
-    st.m = v;
-    st.b = col;
-  } else {
-    st.s += exp_neg(v - st.m);
-  }
-}
-
 __device__ __forceinline__ CtcState ctc_join(CtcState x, CtcState y) {
   const float ninf = -__builtin_inff();
   CtcState r;
@@ -309,29 +299,42 @@ __global__ __launch_bounds__(256) void conv_mfma(ConvArgs a) {
   }
 
   if constexpr (CTC) {
-    // Per row: the tile's (max, sum of exp, first column of the max).
+    // Per row: the tile's (max, sum of exp, first column of the max). Each
+    // lane takes the maximum of its NT columns (the first among equals:
+    // its columns rise with j); the 16 lanes of the row then join the
+    // maximum, the sum of exp(v - max) (hardware exp2, within 1 ulp: the
+    // sum is a probability's denominator, held to a tolerance) and the
+    // lowest column holding the maximum.
+    constexpr float L = 1.44269504088896341f;  // log2(e)
 #pragma unroll
     for (int i = 0; i < MT; i++) {
 #pragma unroll
       for (int r = 0; r < 4; r++) {
-        int m = m0 + wave * WM + i * 16 + lg * 4 + r;
-        CtcState st{-__builtin_inff(), 0.0f, __builtin_inff()};
+        const int m = m0 + wave * WM + i * 16 + lg * 4 + r;
+        float v[NT];
+        float lm = -__builtin_inff(), lb = __builtin_inff();
 #pragma unroll
         for (int j = 0; j < NT; j++) {
-          int n = n0 + j * 16 + li;
-          if (n < a.vocab) ctc_push(st, acc[i][j][r] + a.bias[n], (float)n);
+          const int n = n0 + j * 16 + li;
+          v[j] = n < a.vocab ? acc[i][j][r] + a.bias[n] : -__builtin_inff();
+          if (v[j] > lm) lm = v[j], lb = (float)n;
         }
+        float gm = lm;
+#pragma unroll
+        for (int d = 1; d < 16; d <<= 1) gm = fmaxf(gm, __shfl_xor(gm, d, 64));
+        const float c = gm * L;
+        float sum = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NT; j++) sum += __builtin_amdgcn_exp2f(fmaf(v[j], L, -c));
+        float b = lm == gm ? lb : __builtin_inff();
 #pragma unroll
         for (int d = 1; d < 16; d <<= 1) {
-          CtcState o;
-          o.m = __shfl_xor(st.m, d, 64);
-          o.s = __shfl_xor(st.s, d, 64);
-          o.b = __shfl_xor(st.b, d, 64);
-          st = ctc_join(st, o);
+          sum += __shfl_xor(sum, d, 64);
+          b = fminf(b, __shfl_xor(b, d, 64));
         }
         if (li == 0 && m < M) {
           float4 *p = reinterpret_cast<float4 *>(a.part) + (long)m * ntn + tn;
-          *p = make_float4(st.m, st.s, st.b, 0.0f);
+          *p = make_float4(gm, sum, b, 0.0f);
         }
       }
     }

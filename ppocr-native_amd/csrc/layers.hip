@@ -1044,48 +1044,80 @@ __device__ __forceinline__ Best best_join(Best x, Best y) {
   return r;
 }
 
-// One block per row: each thread keeps a running (max, sum, first column)
-// over columns tid, tid + 256, ...; the block joins them in a fixed order.
-__global__ __launch_bounds__(256) void row_argmax_kernel(const float *x, float *y, int cols) {
-  __shared__ Best part[4];
+// Folds four values at columns c0 .. c0 + 3 into a running (max, sum, first
+// column): their maximum first (the lowest column among equals) rescales the
+// sum when it is a new maximum, then exp(v - max) of the four is added, with
+// the hardware exp2 (within 1 ulp; the sum is a probability's denominator,
+// held to a tolerance, while the argmax is exact).
+__device__ __forceinline__ void best_fold4(Best &st, f32x4 v, int c0) {
+  const float L = 1.44269504088896341f;  // log2(e)
+  const float m4 = fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3]));
+  if (m4 > st.m) {
+    const int b = v[0] == m4 ? c0 : (v[1] == m4 ? c0 + 1 : (v[2] == m4 ? c0 + 2 : c0 + 3));
+    st.s = st.m == -__builtin_inff() ? 0.0f : st.s * __builtin_amdgcn_exp2f((st.m - m4) * L);
+    st.m = m4;
+    st.b = (float)b;
+  }
+  const float c = st.m * L;
+  st.s += __builtin_amdgcn_exp2f(fmaf(v[0], L, -c)) + __builtin_amdgcn_exp2f(fmaf(v[1], L, -c)) +
+          (__builtin_amdgcn_exp2f(fmaf(v[2], L, -c)) + __builtin_amdgcn_exp2f(fmaf(v[3], L, -c)));
+}
+
+// One value at column c, as the engine's running update.
+__device__ __forceinline__ void best_fold1(Best &st, float v, int c) {
+  if (v > st.m) {
+    st.s = st.m == -__builtin_inff() ? 1.0f : st.s * exp_neg(st.m - v) + 1.0f;
+    st.m = v;
+    st.b = (float)c;
+  } else {
+    st.s = st.s + exp_neg(v - st.m);
+  }
+}
+
+// One block of 128 threads per row. The row's 16-byte aligned middle is read
+// as float4 (columns 4t .. 4t+3 of every 512-float stride), four of them in
+// flight per thread; the few columns before the first 16-byte boundary and
+// after the last go one per thread. Each thread's columns arrive in
+// increasing order, so its running state keeps the first maximum; the block
+// joins the threads in a fixed order, ties to the lowest column.
+constexpr int kArgmaxThreads = 128;
+
+__global__ __launch_bounds__(kArgmaxThreads) void row_argmax_kernel(const float *x, float *y, int cols) {
+  constexpr int T = kArgmaxThreads, U = 4;
+  __shared__ Best part[T / 64];
   const float *row = x + (long)blockIdx.x * cols;
+  const int tid = threadIdx.x;
   Best st{-__builtin_inff(), 0.0f, __builtin_inff()};
-  int col = threadIdx.x;
-  for (; col + 768 < cols; col += 1024) {
-    float v0 = row[col], v1 = row[col + 256], v2 = row[col + 512], v3 = row[col + 768];
-    float vs[4] = {v0, v1, v2, v3};
+  const int head = min((int)((4 - (((uintptr_t)row >> 2) & 3)) & 3), cols);
+  if (tid < head) best_fold1(st, row[tid], tid);
+  const int nv = (cols - head) >> 2;
+  const f32x4 *v4 = reinterpret_cast<const f32x4 *>(row + head);
+  for (int base = 0; base < nv; base += U * T) {
+    f32x4 v[U];
 #pragma unroll
-    for (int k = 0; k < 4; k++) {
-      float v = vs[k];
-      if (v > st.m) {
-        st.s = st.s * exp_neg(st.m - v) + 1.0f;
-        st.m = v;
-        st.b = (float)(col + 256 * k);
-      } else {
-        st.s = st.s + exp_neg(v - st.m);
-      }
+    for (int u = 0; u < U; u++) {
+      const int i = base + tid + T * u;
+      v[u] = i < nv ? v4[i] : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    __builtin_amdgcn_sched_barrier(0);  // all four loads issue before the first use
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int i = base + tid + T * u;
+      if (i < nv) best_fold4(st, v[u], head + 4 * i);
     }
   }
-  for (; col < cols; col += 256) {
-    float v = row[col];
-    if (v > st.m) {
-      st.s = st.s * exp_neg(st.m - v) + 1.0f;
-      st.m = v;
-      st.b = (float)col;
-    } else {
-      st.s = st.s + exp_neg(v - st.m);
-    }
-  }
+  const int t = head + 4 * nv + tid;
+  if (t < cols) best_fold1(st, row[t], t);
 #pragma unroll
   for (int d = 1; d < 64; d <<= 1) {
     Best o{__shfl_xor(st.m, d, 64), __shfl_xor(st.s, d, 64), __shfl_xor(st.b, d, 64)};
     st = best_join(st, o);
   }
-  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = st;
+  if ((tid & 63) == 0) part[tid >> 6] = st;
   __syncthreads();
-  if (threadIdx.x == 0) {
+  if (tid == 0) {
     Best r = part[0];
-    for (int k = 1; k < 4; k++) r = best_join(r, part[k]);
+    for (int k = 1; k < T / 64; k++) r = best_join(r, part[k]);
     y[2 * (long)blockIdx.x] = r.b;
     y[2 * (long)blockIdx.x + 1] = 1.0f / r.s;
   }
@@ -1093,7 +1125,7 @@ __global__ __launch_bounds__(256) void row_argmax_kernel(const float *x, float *
 
 hipError_t launch_row_argmax(const float *x, float *y, int rows, int cols, hipStream_t s) {
   if (rows <= 0 || cols <= 0) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(row_argmax_kernel, dim3(rows), dim3(256), 0, s, x, y, cols);
+  hipLaunchKernelGGL(row_argmax_kernel, dim3(rows), dim3(kArgmaxThreads), 0, s, x, y, cols);
   return hipGetLastError();
 }
 

@@ -88,6 +88,26 @@ def test_row_argmax(oracle):
     np.testing.assert_allclose(got[:, 1], want[:, 1], rtol=1e-5, atol=1e-5)
 
 
+@pytest.mark.parametrize("rows,cols", [(7, 1), (5, 3), (9, 6), (11, 101), (6, 8199), (3, 20000)])
+def test_row_argmax_ragged(oracle, rows, cols):
+    # Rows whose starts fall on every 4-byte phase of a 16-byte boundary, so
+    # the aligned middle, the head and the tail each take every length; a tie
+    # in the head, the middle and the tail of three rows.
+    rng = np.random.default_rng(cols)
+    x = rng.normal(0, 3, rows * cols).astype(np.float32)
+    for r, c in ((0, 0), (1, cols // 2), (2, cols - 1)):
+        x[r * cols + c] = x[r * cols + max(0, c - 1)] = 40.0
+    dx, dy = DeviceArray.of(x), DeviceArray(8 * rows)
+    P.hip_row_argmax(dx.addr, dy.addr, rows, cols)
+    synchronize()
+    got = dy.download(2 * rows).reshape(rows, 2)
+    want = oracle.row_argmax(x, rows, cols).reshape(rows, 2)
+    assert np.array_equal(got[:, 0], want[:, 0])
+    for r, c in ((0, 0), (1, cols // 2), (2, cols - 1)):
+        assert got[r, 0] == max(0, c - 1)
+    np.testing.assert_allclose(got[:, 1], want[:, 1], rtol=1e-5, atol=1e-5)
+
+
 @pytest.mark.parametrize("n", [320 * 320, 1001])
 def test_db_mask_gives_the_boxes(n):
     # The DB threshold on the GPU, bytes out; on the reference's own map it
