@@ -507,8 +507,9 @@ __global__ __launch_bounds__(256) void conv_patch(Group<ConvArgs> grp) {
     store();
     __syncthreads();
     if (cc + 1 < a.cpt) fetch(cc + 1);
-    for (int tp = 0; tp < taps; tp++) {
-      const int ky = tp / a.kw, kx = tp - ky * a.kw;
+    // One tap: the window offset (ky, kx) into the staged patch. A 3 x 3
+    // window runs its nine taps unrolled.
+    auto tap = [&](int tp, int ky, int kx) {
 #pragma unroll
       for (int r = 0; r < KR; r++) {
         typedef typename VecT<KW>::T KT;
@@ -541,6 +542,12 @@ __global__ __launch_bounds__(256) void conv_patch(Group<ConvArgs> grp) {
           }
         }
       }
+    };
+    if (a.kh == 3 && a.kw == 3) {
+#pragma unroll
+      for (int tp = 0; tp < 9; tp++) tap(tp, tp / 3, tp % 3);
+    } else {
+      for (int tp = 0; tp < taps; tp++) tap(tp, tp / a.kw, tp % a.kw);
     }
   }
 
