@@ -299,6 +299,77 @@ def bench_stages(P, nets, repeats: int = 20) -> dict:
     return out
 
 
+def page_plans(nets):
+    """The page pipeline's networks: the detector graph at 736 x 960 with
+    its ink path set (the boxes land on the page's lines) and the
+    recogniser with scaled seeded weights (non-trivial text)."""
+    return nets.detector_plan(h=960, w=736, init="ink"), nets.recognizer_plan(init="scaled")
+
+
+def bench_page(P, nets, repeats: int = 10) -> dict:
+    """The page pipeline on a 2550 x 3300 letter page with 44 text lines:
+    detector input, detector, DB boxes (host), crops, recogniser inputs,
+    recogniser in batches of 16 and CTC text (host)."""
+    from ppocr_native_amd import post
+    from ppocr_native_amd.devmem import DeviceArray
+    from ppocr_native_amd.pipeline import PagePipeline
+    gold = ROOT / "tests" / "golden"
+    d = post.Dictionary.from_metadata((gold / "characters.txt").read_text(encoding="utf-8"))
+    page = nets.letter_page()
+    H, W = page.shape[:2]
+    det_plan, rec_plan = page_plans(nets)
+    pipe = PagePipeline(det_plan, rec_plan, d)
+    dpage = DeviceArray.of(page.reshape(-1))
+    for _ in range(3):
+        lines = pipe.read_device(dpage.addr, W, H)
+    stages = {"detect": 0.0, "boxes": 0.0, "read": 0.0, "decode": 0.0}
+    t0 = time.perf_counter()
+    for _ in range(repeats):
+        lines = pipe.read_device(dpage.addr, W, H)
+        for k in stages:
+            stages[k] += getattr(pipe.times, k) / repeats
+    ms = (time.perf_counter() - t0) * 1e3 / repeats
+    t0 = time.perf_counter()
+    for _ in range(3):
+        pipe.read(page)
+    up_ms = (time.perf_counter() - t0) * 1e3 / 3
+    out = {"metric": "pages/s and lines/s, 2550x3300 letter page, 44 lines, detector at 736x960, "
+                     "recogniser 48x320 in batches of 16",
+           "pages_per_s": round(1e3 / ms, 2), "lines_per_s": round(len(lines) * 1e3 / ms, 1),
+           "ms_per_page": round(ms, 3), "lines": len(lines), "batches": pipe.times.batches,
+           "stages_ms": {k: round(v, 3) for k, v in stages.items()},
+           "with_page_upload_pages_per_s": round(1e3 / up_ms, 2),
+           "text_chars": sum(len(x.text) for x in lines)}
+    pipe.close()
+    return out
+
+
+def cpu_page(nets, threads: int) -> dict:
+    """The same page on the CPU path: the oracle's stages, host boxes and
+    decode; one page."""
+    sys.path.insert(0, str(ROOT))
+    import oracle
+    from ppocr_native_amd import post
+    gold = ROOT / "tests" / "golden"
+    d = post.Dictionary.from_metadata((gold / "characters.txt").read_text(encoding="utf-8"))
+    page = nets.letter_page()
+    H, W = page.shape[:2]
+    det_plan, rec_plan = page_plans(nets)
+    det, rec = oracle.OracleModel(det_plan), oracle.OracleModel(rec_plan)
+    det.set_size(960, 736)
+    rec.set_size(48, 320)
+    mean, std = (0.485, 0.456, 0.406), (0.229, 0.224, 0.225)
+    t0 = time.perf_counter()
+    prob = det.run(oracle.det_input(page, 736, 960, mean, std), threads)[0]
+    quads = post.boxes_from_prob(prob, 736, 960, W, H)
+    for q in quads:
+        post.ctc_decode_pairs(rec.run(oracle.rec_input(oracle.crop_text(page, q), 320), threads)[0], d)
+    s = time.perf_counter() - t0
+    return {"value": round(1 / s, 4), "unit": "pages/s", "lines_per_s": round(len(quads) / s, 2),
+            "cores": threads, "kind": "port",
+            "sample": f"one page of {len(quads)} lines through the C oracle's stages, {threads} threads"}
+
+
 def cpu_baseline(nets, det_plan, rec_plan, budget_s: float) -> tuple[dict, dict]:
     sys.path.insert(0, str(ROOT))
     import oracle
@@ -395,6 +466,8 @@ def main() -> int:
         result["micro"] = bench_micro(P)
         log("bench: stages either side of the networks")
         result["stages"] = bench_stages(P, nets)
+        log("bench: page pipeline 2550x3300")
+        result["page"] = bench_page(P, nets)
     else:
         rec_plan = nets.recognizer_plan(init="baseline")
     if not args.no_cpu:
@@ -403,6 +476,9 @@ def main() -> int:
         result["cpu_baseline"] = det_cpu
         if "rec" in result:
             result["rec"]["cpu_baseline"] = rec_cpu
+        if "page" in result:
+            log("bench: CPU page")
+            result["page"]["cpu_baseline"] = cpu_page(nets, det_cpu["cores"])
     print(json.dumps(result), flush=True)
     return 0
 

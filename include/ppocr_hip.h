@@ -99,6 +99,18 @@ int ppocr_gpu_download(ppocr_gpu_model *model, char *err, size_t err_len);
 /* The model's HIP stream, as a hipStream_t. */
 void *ppocr_gpu_stream(ppocr_gpu_model *model);
 
+/* Device-resident input, for a caller that prepares the input on the GPU
+ * (no Vulkan counterpart: there the worker writes `lane_input_mut`'s mapped
+ * memory on the CPU, ocr.rs:227). The device address of `lane`'s input
+ * (`*len` floats, HWC, the layout of `ppocr_gpu_lane_input`), valid until
+ * the next set_sizes; write it in order on `ppocr_gpu_stream`. */
+float *ppocr_gpu_lane_input_device(ppocr_gpu_model *model, size_t lane, size_t *len);
+
+/* `ppocr_gpu_run` without the host-to-device copy: the forward over the
+ * device-resident inputs, then every lane's results to the host buffers of
+ * `ppocr_gpu_lane_output`; synchronous. */
+int ppocr_gpu_run_device(ppocr_gpu_model *model, char *err, size_t err_len);
+
 /* Runs record their launches in a HIP graph from the second run after the
  * lanes were set, and replay it (default, `enable` 1); with 0 every run
  * launches each kernel itself. Returns 0, or 1 for a NULL model. */
@@ -255,6 +267,26 @@ size_t ppocr_rec_width(size_t w, size_t h, size_t *resized_w);
  * receives the tensor width. */
 int ppocr_hip_rec_input(const uint8_t *crop, size_t w, size_t h, float *out, size_t out_cap, size_t *width,
                         void *stream);
+
+/* The recogniser input with the tensor width capped at `max_width` (no
+ * reference counterpart: the page pipeline's crops "resized to height 48
+ * with padded width <= 320"): a crop whose `ppocr_rec_width` exceeds the cap
+ * is resized to max_width x 48 (squeezed), any other gives exactly
+ * `ppocr_hip_rec_input`'s tensor. `max_width` 0 means no cap. */
+size_t ppocr_rec_width_fit(size_t w, size_t h, size_t max_width, size_t *resized_w);
+int ppocr_hip_rec_input_fit(const uint8_t *crop, size_t w, size_t h, size_t max_width, float *out,
+                            size_t out_cap, size_t *width, void *stream);
+
+/* The recogniser inputs of n boxes of a page, 16 lines per launch, without
+ * the crops in memory (no reference counterpart: the worker crops each box
+ * and then makes its input, ocr.rs:472-477): quads n x (x, y) x 4 as
+ * `ppocr_hip_crop_text` takes them; line i's 48 x widths[i] tensor (HWC,
+ * `out_caps[i]` floats at the device address outs[i]) gets exactly what
+ * `ppocr_hip_crop_text` followed by `ppocr_hip_rec_input_fit` with
+ * `max_width` would write. */
+int ppocr_hip_crop_rec_inputs(const uint8_t *page, size_t w, size_t h, const float *quads, size_t n,
+                              size_t max_width, float *const *outs, const size_t *out_caps, size_t *widths,
+                              void *stream);
 
 /* The size `ppocr_hip_crop_text` gives a quad's crop, after any turn. */
 int ppocr_crop_size(const float *quad, size_t *width, size_t *height);

@@ -256,17 +256,27 @@ def rec_width(w: int, h: int) -> tuple[int, int]:
     return width, rw.value
 
 
-def rec_input(crop) -> np.ndarray:
-    """HWC f32, 48 x width x 3."""
+def rec_width_fit(w: int, h: int, max_width: int) -> tuple[int, int]:
+    """(tensor width, resized width) with the tensor capped at max_width."""
+    L = lib()
+    L.oracle_rec_width_fit.argtypes = [C.c_size_t, C.c_size_t, C.c_size_t, C.POINTER(C.c_size_t)]
+    L.oracle_rec_width_fit.restype = C.c_size_t
+    rw = C.c_size_t()
+    width = L.oracle_rec_width_fit(w, h, max_width, C.byref(rw))
+    return width, rw.value
+
+
+def rec_input(crop, max_width: int = 0) -> np.ndarray:
+    """HWC f32, 48 x width x 3 (width capped at max_width unless 0)."""
     src = _img(crop)
-    width, _ = rec_width(src.shape[1], src.shape[0])
+    width, _ = rec_width_fit(src.shape[1], src.shape[0], max_width)
     out = np.empty((48, width, 3), np.float32)
     L = lib()
-    L.oracle_rec_input.argtypes = [C.POINTER(C.c_uint8), C.c_size_t, C.c_size_t, C.POINTER(C.c_float),
-                                   C.c_size_t]
-    L.oracle_rec_input.restype = C.c_size_t
-    got = L.oracle_rec_input(_u8p(src), src.shape[1], src.shape[0],
-                             out.ctypes.data_as(C.POINTER(C.c_float)), out.size)
+    L.oracle_rec_input_fit.argtypes = [C.POINTER(C.c_uint8), C.c_size_t, C.c_size_t, C.c_size_t,
+                                       C.POINTER(C.c_float), C.c_size_t]
+    L.oracle_rec_input_fit.restype = C.c_size_t
+    got = L.oracle_rec_input_fit(_u8p(src), src.shape[1], src.shape[0], max_width,
+                                 out.ctypes.data_as(C.POINTER(C.c_float)), out.size)
     assert got == width
     return out
 

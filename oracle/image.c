@@ -95,11 +95,24 @@ size_t oracle_rec_width(size_t w, size_t h, size_t *resized_w) {
     return width;
 }
 
+/* The width with the tensor capped at max_width (0: no cap): a crop wider
+ * than the cap is resized to exactly max_width columns, any other keeps
+ * rec.rs's widths. */
+size_t oracle_rec_width_fit(size_t w, size_t h, size_t max_width, size_t *resized_w) {
+    size_t width = oracle_rec_width(w, h, resized_w);
+    if (max_width && width > max_width) {
+        *resized_w = max_width;
+        return max_width;
+    }
+    return width;
+}
+
 /* The recogniser input, HWC, 48 x width (rec.rs:19-43): resized to 48 rows
- * of resized_w, (v / 255 - 0.5) / 0.5 in f32, zeros to the right. */
-size_t oracle_rec_input(const uint8_t *src, size_t w, size_t h, float *out, size_t cap) {
+ * of resized_w, (v / 255 - 0.5) / 0.5 in f32, zeros to the right; the
+ * widths of oracle_rec_width_fit. */
+size_t oracle_rec_input_fit(const uint8_t *src, size_t w, size_t h, size_t max_width, float *out, size_t cap) {
     size_t rw;
-    size_t width = oracle_rec_width(w, h, &rw);
+    size_t width = oracle_rec_width_fit(w, h, max_width, &rw);
     if (48 * width * 3 > cap) return 0;
     uint8_t *r = malloc(rw * 48 * 3);
     oracle_resize_linear(src, w, h, r, rw, 48);
@@ -110,6 +123,10 @@ size_t oracle_rec_input(const uint8_t *src, size_t w, size_t h, float *out, size
                 out[(y * width + x) * 3 + c] = ((float)r[(y * rw + x) * 3 + c] / 255.0f - 0.5f) / 0.5f;
     free(r);
     return width;
+}
+
+size_t oracle_rec_input(const uint8_t *src, size_t w, size_t h, float *out, size_t cap) {
+    return oracle_rec_input_fit(src, w, h, 0, out, cap);
 }
 
 /* The projective map of the width x height rectangle's corners onto the

@@ -62,6 +62,8 @@ def lib() -> C.CDLL:
         "ppocr_gpu_run_resident": ([vp, C.c_int, fp, cp, sz], C.c_int),
         "ppocr_gpu_download": ([vp, cp, sz], C.c_int),
         "ppocr_gpu_stream": ([vp], vp),
+        "ppocr_gpu_lane_input_device": ([vp, sz, szp], vp),
+        "ppocr_gpu_run_device": ([vp, cp, sz], C.c_int),
         "ppocr_gpu_set_graphs": ([vp, C.c_int], C.c_int),
         "ppocr_gpu_launch_count": ([vp], sz),
         "ppocr_gpu_launch_name": ([vp, sz, szp], cp),
@@ -171,6 +173,19 @@ class GpuModel:
 
     def run(self) -> None:
         _call(lib().ppocr_gpu_run, self._h)
+
+    def lane_input_device(self, lane: int) -> tuple[int, int]:
+        """(device address, floats) of lane `lane`'s input, for inputs
+        prepared on the GPU in order on `stream()`; valid until set_sizes."""
+        n = C.c_size_t()
+        p = lib().ppocr_gpu_lane_input_device(self._h, lane, C.byref(n))
+        if not p:
+            raise GpuError(f"lane {lane} does not exist")
+        return p, n.value
+
+    def run_device(self) -> None:
+        """`run` over inputs already written on the device."""
+        _call(lib().ppocr_gpu_run_device, self._h)
 
     # Measurement helpers.
     def upload(self) -> None:

@@ -33,14 +33,21 @@ __device__ __forceinline__ Tap tap_at(int src, int dst, int d) {
   return t;
 }
 
-// Channel c of output pixel (x, y): horizontal products kept whole, then 4
-// bits off each row before its weight, 16 after, the sum rounded by 2 bits.
-__device__ __forceinline__ int resize_at(const uint8_t *src, int sw, const Tap &tx, const Tap &ty, int c) {
-  const uint8_t *rn = src + (long)ty.near_i * sw * 3, *rf = src + (long)ty.far_i * sw * 3;
-  const int a = (int)rn[tx.near_i * 3 + c] * tx.near_w + (int)rn[tx.far_i * 3 + c] * tx.far_w;
-  const int b = (int)rf[tx.near_i * 3 + c] * tx.near_w + (int)rf[tx.far_i * 3 + c] * tx.far_w;
+// One output value from its four source values (near / far row, near / far
+// column): horizontal products kept whole, then 4 bits off each row before
+// its weight, 16 after, the sum rounded by 2 bits.
+__device__ __forceinline__ int resize_mix(int nn, int nf, int fn, int ff, const Tap &tx, const Tap &ty) {
+  const int a = nn * tx.near_w + nf * tx.far_w;
+  const int b = fn * tx.near_w + ff * tx.far_w;
   const int v = (((a >> 4) * ty.near_w) >> 16) + (((b >> 4) * ty.far_w) >> 16);
   return min(max((v + 2) >> 2, 0), 255);
+}
+
+// Channel c of output pixel (x, y) of a resize of `src`.
+__device__ __forceinline__ int resize_at(const uint8_t *src, int sw, const Tap &tx, const Tap &ty, int c) {
+  const uint8_t *rn = src + (long)ty.near_i * sw * 3, *rf = src + (long)ty.far_i * sw * 3;
+  return resize_mix(rn[tx.near_i * 3 + c], rn[tx.far_i * 3 + c], rf[tx.near_i * 3 + c], rf[tx.far_i * 3 + c],
+                    tx, ty);
 }
 
 __global__ __launch_bounds__(256) void resize_kernel(const uint8_t *src, int sw, int sh, uint8_t *dst, int dw,
@@ -97,15 +104,11 @@ __device__ __forceinline__ void cubic(float t, float *w) {
   w[3] = 1.0f - w[0] - w[1] - w[2];
 }
 
-// One crop pixel (x, y) of the width x height rectangle: its source point
-// through the projective map m (f64, then f32), the 4 x 4 bicubic window with
-// edge pixels repeated, each row of four summed before the rows; written
-// turned a quarter counter-clockwise when `turn`.
-__global__ __launch_bounds__(256) void crop_kernel(const uint8_t *img, int iw, int ih, CropMap m, uint8_t *out,
-                                                   int width, int height, int turn) {
-  const long g = (long)blockIdx.x * 256 + threadIdx.x;
-  if (g >= (long)width * height) return;
-  const int y = (int)(g / width), x = (int)(g - (long)y * width);
+// Pixel (x, y) of a crop rectangle: its source point through the
+// projective map m (f64, then f32), the 4 x 4 bicubic window with edge pixels
+// repeated, each row of four summed before the rows, rounded to 8 bits.
+__device__ __forceinline__ void crop_pixel(const uint8_t *img, int iw, int ih, const CropMap &m, int x, int y,
+                                           int v[3]) {
   const double xf = x, yf = y;
   double w = m.v[6] * xf + m.v[7] * yf + m.v[8];
   w = w == 0.0 ? 0.0 : 1.0 / w;
@@ -135,9 +138,58 @@ __global__ __launch_bounds__(256) void crop_kernel(const uint8_t *img, int iw, i
 #pragma unroll
     for (int c = 0; c < 3; c++) acc[c] += line[c] * wy[j];
   }
+#pragma unroll
+  for (int c = 0; c < 3; c++) v[c] = (int)fminf(fmaxf(rintf(acc[c]), 0.0f), 255.0f);
+}
+
+// One crop pixel (x, y) of the width x height rectangle, written turned a
+// quarter counter-clockwise when `turn`.
+__global__ __launch_bounds__(256) void crop_kernel(const uint8_t *img, int iw, int ih, CropMap m, uint8_t *out,
+                                                   int width, int height, int turn) {
+  const long g = (long)blockIdx.x * 256 + threadIdx.x;
+  if (g >= (long)width * height) return;
+  const int y = (int)(g / width), x = (int)(g - (long)y * width);
+  int v[3];
+  crop_pixel(img, iw, ih, m, x, y, v);
   const long at = turn ? ((long)(width - 1 - x) * height + y) : g;
 #pragma unroll
-  for (int c = 0; c < 3; c++) out[at * 3 + c] = (uint8_t)fminf(fmaxf(rintf(acc[c]), 0.0f), 255.0f);
+  for (int c = 0; c < 3; c++) out[at * 3 + c] = (uint8_t)v[c];
+}
+
+// The recogniser inputs of up to kCropLines crops in one launch, without the
+// crops in memory: line blockIdx.y, output pixel (x, y) of its 48 x width
+// tensor takes the four crop pixels its resize taps name, each computed as
+// crop_kernel computes it (through the turn when the crop is turned), then
+// the resize and the [-1, 1] scaling of rec_input_kernel: the same values
+// as crop_text then rec_input.
+__global__ __launch_bounds__(256) void crop_rec_kernel(const uint8_t *img, int iw, int ih, CropLines b) {
+  const CropLine &L = b.l[blockIdx.y];
+  const long g = (long)blockIdx.x * 256 + threadIdx.x;
+  if (g >= 48L * L.width) return;
+  const int y = (int)(g / L.width), x = (int)(g - (long)y * L.width);
+  float *o = L.out + g * 3;
+  if (x >= L.rw) {
+#pragma unroll
+    for (int c = 0; c < 3; c++) o[c] = 0.0f;
+    return;
+  }
+  const int sw = L.turn ? L.ch : L.cw, sh = L.turn ? L.cw : L.ch;  // the crop image's sides
+  const Tap tx = tap_at(sw, L.rw, x), ty = tap_at(sh, 48, y);
+  // Crop image pixel (cx, cy) is rectangle pixel (cw - 1 - cy, cx) when turned.
+  auto px = [&](int cx, int cy, int v[3]) {
+    if (L.turn)
+      crop_pixel(img, iw, ih, L.m, L.cw - 1 - cy, cx, v);
+    else
+      crop_pixel(img, iw, ih, L.m, cx, cy, v);
+  };
+  int nn[3], nf[3], fn[3], ff[3];
+  px(tx.near_i, ty.near_i, nn);
+  px(tx.far_i, ty.near_i, nf);
+  px(tx.near_i, ty.far_i, fn);
+  px(tx.far_i, ty.far_i, ff);
+#pragma unroll
+  for (int c = 0; c < 3; c++)
+    o[c] = ((float)resize_mix(nn[c], nf[c], fn[c], ff[c], tx, ty) / 255.0f - 0.5f) / 0.5f;
 }
 
 static unsigned blocks(long n) { return (unsigned)((n + 255) / 256); }
@@ -156,6 +208,14 @@ hipError_t launch_det_input(const uint8_t *src, int sw, int sh, float *out, int 
 
 hipError_t launch_rec_input(const uint8_t *src, int sw, int sh, float *out, int width, int rw, hipStream_t s) {
   hipLaunchKernelGGL(rec_input_kernel, dim3(blocks(48L * width)), dim3(256), 0, s, src, sw, sh, out, width, rw);
+  return hipGetLastError();
+}
+
+hipError_t launch_crop_rec(const uint8_t *img, int iw, int ih, const CropLines &b, hipStream_t s) {
+  if (b.n <= 0 || b.n > kCropLines) return hipErrorInvalidValue;
+  int widest = 0;
+  for (int i = 0; i < b.n; i++) widest = max(widest, b.l[i].width);
+  hipLaunchKernelGGL(crop_rec_kernel, dim3(blocks(48L * widest), (unsigned)b.n), dim3(256), 0, s, img, iw, ih, b);
   return hipGetLastError();
 }
 

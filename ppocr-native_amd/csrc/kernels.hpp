@@ -288,5 +288,19 @@ hipError_t launch_det_input(const uint8_t *src, int sw, int sh, float *out, int 
 hipError_t launch_rec_input(const uint8_t *src, int sw, int sh, float *out, int width, int rw, hipStream_t s);
 hipError_t launch_crop(const uint8_t *img, int iw, int ih, const CropMap &m, uint8_t *out, int width, int height,
                        bool turn, hipStream_t s);
+// One line of a batched crop + recogniser input: the cw x ch rectangle's
+// map, turned when `turn`, into a 48 x width tensor of which the first rw
+// columns hold the resized crop.
+struct CropLine {
+  CropMap m;
+  float *out;
+  int cw, ch, turn, width, rw;
+};
+constexpr int kCropLines = 16;
+struct CropLines {
+  int n;
+  CropLine l[kCropLines];
+};
+hipError_t launch_crop_rec(const uint8_t *img, int iw, int ih, const CropLines &b, hipStream_t s);
 
 }  // namespace ppocr

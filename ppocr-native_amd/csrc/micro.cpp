@@ -199,6 +199,57 @@ int ppocr_hip_rec_input(const uint8_t *crop, size_t w, size_t h, float *out, siz
   return code(launch_rec_input(crop, int(w), int(h), out, int(wd), int(rw), hipStream_t(stream)));
 }
 
+size_t ppocr_rec_width_fit(size_t w, size_t h, size_t max_width, size_t *resized_w) {
+  size_t rw = 0;
+  const size_t width = ppocr_rec_width(w, h, &rw);
+  if (width && max_width && width > max_width) {
+    if (resized_w) *resized_w = max_width;
+    return max_width;
+  }
+  if (resized_w) *resized_w = rw;
+  return width;
+}
+
+int ppocr_hip_rec_input_fit(const uint8_t *crop, size_t w, size_t h, size_t max_width, float *out,
+                            size_t out_cap, size_t *width, void *stream) {
+  size_t rw = 0;
+  const size_t wd = ppocr_rec_width_fit(w, h, max_width, &rw);
+  if (width) *width = wd;
+  if (!wd || !crop || !out || w > kMaxSide || h > kMaxSide || wd > kMaxSide || rw == 0) return int(hipErrorInvalidValue);
+  if (48 * wd * 3 > out_cap) return int(hipErrorInvalidValue);
+  return code(launch_rec_input(crop, int(w), int(h), out, int(wd), int(rw), hipStream_t(stream)));
+}
+
+int ppocr_hip_crop_rec_inputs(const uint8_t *page, size_t w, size_t h, const float *quads, size_t n,
+                              size_t max_width, float *const *outs, const size_t *out_caps, size_t *widths,
+                              void *stream) {
+  if (!page || !w || !h || w > kMaxSide || h > kMaxSide || (n && (!quads || !outs || !out_caps)))
+    return int(hipErrorInvalidValue);
+  CropLines b{};
+  for (size_t i = 0; i < n; i++) {
+    const float *q = quads + 8 * i;
+    size_t cw, ch;
+    crop_size(q, &cw, &ch);
+    const bool turn = cw && double(ch) / double(cw) >= 1.5;
+    const size_t iw = turn ? ch : cw, ih = turn ? cw : ch;
+    size_t rw = 0;
+    const size_t wd = ppocr_rec_width_fit(iw, ih, max_width, &rw);
+    if (widths) widths[i] = wd;
+    if (!wd || !rw || cw > kMaxSide || ch > kMaxSide || wd > kMaxSide || !outs[i] || 48 * wd * 3 > out_caps[i])
+      return int(hipErrorInvalidValue);
+    CropLine &l = b.l[b.n++];
+    l.m = rect_to_quad(double(cw), double(ch), q);
+    l.out = outs[i];
+    l.cw = int(cw), l.ch = int(ch), l.turn = turn ? 1 : 0, l.width = int(wd), l.rw = int(rw);
+    if (b.n == kCropLines || i + 1 == n) {
+      const int rc = code(launch_crop_rec(page, int(w), int(h), b, hipStream_t(stream)));
+      if (rc) return rc;
+      b.n = 0;
+    }
+  }
+  return 0;
+}
+
 int ppocr_crop_size(const float *quad, size_t *width, size_t *height) {
   if (!quad) return 1;
   size_t w, h;

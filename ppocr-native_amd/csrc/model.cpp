@@ -1651,6 +1651,21 @@ int ppocr_gpu_run(ppocr_gpu_model *model, char *err, size_t err_len) {
   return 0;
 }
 
+float *ppocr_gpu_lane_input_device(ppocr_gpu_model *model, size_t lane, size_t *len) {
+  if (!model || lane >= model->m.lane_at.size()) return nullptr;
+  auto [g, i] = model->m.lane_at[lane];
+  Batch &b = *model->m.batches[g];
+  if (len) *len = b.in_len;
+  return b.dev(b.plan.in_slot) + i * b.stride(b.plan.in_slot);
+}
+
+int ppocr_gpu_run_device(ppocr_gpu_model *model, char *err, size_t err_len) {
+  if (!model) return put_err("no model", err, err_len), 1;
+  std::string e;
+  if (!model->m.run(false, true, e)) return put_err(e, err, err_len), 1;
+  return 0;
+}
+
 int ppocr_gpu_upload(ppocr_gpu_model *model, char *err, size_t err_len) {
   if (!model) return put_err("no model", err, err_len), 1;
   ppocr::Model &m = model->m;

@@ -26,6 +26,9 @@ def _sig():
         ("ppocr_hip_det_input", [vp, sz, sz, vp, sz, sz, dp, dp, vp], C.c_int),
         ("ppocr_rec_width", [sz, sz, szp], sz),
         ("ppocr_hip_rec_input", [vp, sz, sz, vp, sz, szp, vp], C.c_int),
+        ("ppocr_rec_width_fit", [sz, sz, sz, szp], sz),
+        ("ppocr_hip_rec_input_fit", [vp, sz, sz, sz, vp, sz, szp, vp], C.c_int),
+        ("ppocr_hip_crop_rec_inputs", [vp, sz, sz, fp, sz, sz, C.POINTER(vp), szp, szp, vp], C.c_int),
         ("ppocr_crop_size", [fp, szp, szp], C.c_int),
         ("ppocr_hip_crop_text", [vp, sz, sz, fp, vp, sz, szp, szp, vp], C.c_int),
     ]:
@@ -70,13 +73,24 @@ def rec_width(w: int, h: int) -> tuple[int, int]:
     return _sig().ppocr_rec_width(w, h, C.byref(rw)), rw.value
 
 
-def rec_input(crop) -> np.ndarray:
+def rec_width_fit(w: int, h: int, max_width: int) -> tuple[int, int]:
+    rw = C.c_size_t()
+    return _sig().ppocr_rec_width_fit(w, h, max_width, C.byref(rw)), rw.value
+
+
+def rec_input(crop, max_width: int = 0) -> np.ndarray:
+    """The recogniser tensor of a crop; with `max_width` the tensor is at
+    most that wide (wider crops squeezed), as the page pipeline feeds it."""
     L = _sig()
     src, w, h = _upload(crop)
-    width, _ = rec_width(w, h)
+    width, _ = rec_width_fit(w, h, max_width)
     out = DeviceArray(4 * 48 * width * 3)
     got = C.c_size_t()
-    _check(L.ppocr_hip_rec_input(src.addr, w, h, out.addr, 48 * width * 3, C.byref(got), None), "rec_input")
+    if max_width:
+        rc = L.ppocr_hip_rec_input_fit(src.addr, w, h, max_width, out.addr, 48 * width * 3, C.byref(got), None)
+    else:
+        rc = L.ppocr_hip_rec_input(src.addr, w, h, out.addr, 48 * width * 3, C.byref(got), None)
+    _check(rc, "rec_input")
     synchronize()
     return out.download(48 * width * 3).reshape(48, width, 3)
 

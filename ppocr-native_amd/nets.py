@@ -29,22 +29,86 @@ from .planfile import PlanBuilder, Tensor
 
 
 class Init:
+    """Seeded weights. `role` names what a layer does in the graph; these
+    draws ignore it (the ink detector below uses it)."""
+
     def __init__(self, seed: int, init: str, sigma: float, gain: float = 1.3):
         self.rng = np.random.default_rng(seed)
         self.init = init
         self.sigma = sigma
         self.gain = gain
 
-    def w(self, shape, fan_in: int, gain: float | None = None) -> np.ndarray:
+    def w(self, shape, fan_in: int, gain: float | None = None, role: str = "") -> np.ndarray:
         if self.init == "baseline":
             std = self.sigma
         else:
             std = (self.gain if gain is None else gain) / np.sqrt(fan_in)
         return self.rng.normal(0.0, std, size=shape).astype(np.float32)
 
-    def b(self, n: int) -> np.ndarray:
+    def b(self, n: int, role: str = "") -> np.ndarray:
         std = self.sigma if self.init == "baseline" else 0.05
         return self.rng.normal(0.0, std, size=n).astype(np.float32)
+
+
+class InkInit(Init):
+    """The detector's weights for the page pipeline: every weight seeded
+    N(0, sigma) as in the baseline, except what feeds output channel 0 of
+    each layer on the path from the input to the map, which carries an ink
+    signal: the stem's channel 0 is 5.5 minus the mean of the normalised
+    RGB over its 3 x 3 window (about 3.06 on white paper, up to 7.5 on
+    black ink, so that hard swish passes it unchanged), later layers copy it
+    (centre tap 1) or average it (3 x 3 box, `box` roles), the 1/4-scale
+    branch of the neck carries it to the head while the coarser branches
+    give channel 0 nothing, squeeze-and-excite gates on channel 0 are held
+    open (1, 'se') or shut (0, 'rse'), and the last transposed convolution
+    maps it to gain * (v - level) before the sigmoid. The map is then high
+    over ink and low over paper, so the DB boxes fall on the page's lines.
+    Layers off that path keep their seeded weights in every channel."""
+
+    GAIN = 6.0
+    LEVEL = 3.6
+
+    def w(self, shape, fan_in: int, gain: float | None = None, role: str = "") -> np.ndarray:
+        a = super().w(shape, fan_in, gain, role)
+        if not role:
+            return a
+        if role.startswith("convt"):  # [ic][kh][kw][oc]
+            a[..., 0] = 0.0
+            a[0, :, :, 0] = self.GAIN if role == "convt_out" else 1.0
+            return a
+        if len(shape) == 3:  # depthwise [kh][kw][c]
+            kh, kw, _ = shape
+            a[:, :, 0] = 0.0
+            if role == "box":
+                a[:, :, 0] = 1.0 / (kh * kw)
+            elif role == "hbox":
+                a[kh // 2, :, 0] = 1.0 / kw
+            else:
+                a[kh // 2, kw // 2, 0] = 1.0
+            return a
+        kh, kw, ci, _ = shape  # dense [kh][kw][ci][oc]
+        a[..., 0] = 0.0
+        src = 0  # "carry@72": from input channel 72
+        if "@" in role:
+            role, at = role.split("@")
+            src = int(at)
+        if role == "stem":
+            a[..., 0] = -1.0 / (kh * kw * ci)
+        elif role == "box":
+            a[:, :, src, 0] = 1.0 / (kh * kw)
+        elif role == "hbox":
+            a[kh // 2, :, src, 0] = 1.0 / kw
+        elif role == "carry":
+            a[kh // 2, kw // 2, src, 0] = 1.0
+        # "zero", "se", "rse": nothing reaches channel 0
+        return a
+
+    def b(self, n: int, role: str = "") -> np.ndarray:
+        a = super().b(n, role)
+        if role:
+            a[0] = {"stem": 5.5, "se": 10.0, "rse": -10.0,
+                    "convt_out": -self.GAIN * self.LEVEL}.get(role, 0.0)
+        return a
 
 
 def se_gate(b: PlanBuilder, x: Tensor, r: Init, *, reduce: int = 4,
@@ -53,21 +117,23 @@ def se_gate(b: PlanBuilder, x: Tensor, r: Init, *, reduce: int = 4,
     mid = max(1, x.c // reduce)
     m = b.mean(x)
     h = b.conv(m, r.w((1, 1, x.c, mid), x.c), r.b(mid), fused="relu")
-    return b.conv(h, r.w((1, 1, mid, x.c), mid), r.b(x.c), fused=gate)
+    role = "se" if gate == "hardsigmoid" else "rse"
+    return b.conv(h, r.w((1, 1, mid, x.c), mid, role=role), r.b(x.c, role=role), fused=gate)
 
 
 def dw_block(b: PlanBuilder, x: Tensor, r: Init, *, k: int, s=(1, 1), cout: int,
-             se: bool = False, act: str = "hardswish") -> Tensor:
+             se: bool = False, act: str = "hardswish", dw_role: str = "carry") -> Tensor:
     """Depthwise k x k (+bias, act) [-> SE gate] -> pointwise 1x1 (+bias);
     with stride 1 and equal channels the pointwise output is added to the
     block input (no activation after), else it takes the activation."""
     p = (k - 1) // 2
-    d = b.dwconv(x, r.w((k, k, x.c), k * k), r.b(x.c), k=(k, k), s=s, pad=(p, p, p, p),
-                 fused=act)
+    d = b.dwconv(x, r.w((k, k, x.c), k * k, role=dw_role), r.b(x.c, role=dw_role), k=(k, k), s=s,
+                 pad=(p, p, p, p), fused=act)
     if se:
         d = b.channelmul(d, se_gate(b, d, r))
     residual = s == (1, 1) and cout == x.c
-    y = b.conv(d, r.w((1, 1, x.c, cout), x.c), r.b(cout), fused="none" if residual else act)
+    y = b.conv(d, r.w((1, 1, x.c, cout), x.c, role="carry"), r.b(cout, role="carry"),
+               fused="none" if residual else act)
     return b.add(y, x) if residual else y
 
 
@@ -82,11 +148,12 @@ def fused_block_plan(*, h: int = 160, w: int = 160, c: int = 96, seed: int = 1,
     return b.to_bytes([y])
 
 
-def rse(b: PlanBuilder, x: Tensor, r: Init, *, cout: int, k: int) -> Tensor:
+def rse(b: PlanBuilder, x: Tensor, r: Init, *, cout: int, k: int, role: str = "zero") -> Tensor:
     """Residual SE layer of the neck: conv, then y + y * gate with the 0.2
     hard sigmoid (plan.rs:160-163)."""
     p = (k - 1) // 2
-    y = b.conv(x, r.w((k, k, x.c, cout), k * k * x.c), r.b(cout), k=(k, k), pad=(p, p, p, p))
+    y = b.conv(x, r.w((k, k, x.c, cout), k * k * x.c, role=role), r.b(cout, role=role), k=(k, k),
+               pad=(p, p, p, p))
     g = se_gate(b, y, r, gate="hardsigmoidfifth")
     return b.add(y, b.channelmul(y, g))
 
@@ -95,20 +162,24 @@ def detector_plan(*, h: int = 960, w: int = 960, seed: int = 3, init: str = "bas
                   sigma: float = 0.05) -> bytes:
     """A PP-OCR mobile-style DB detector: LCNet-style backbone, RSE-FPN neck
     of 96 channels, DB head to a 1-channel sigmoid map at the input size.
-    Input sides must be multiples of 32."""
-    r = Init(seed, init, sigma)
+    Input sides must be multiples of 32. ``init="ink"`` draws the baseline
+    weights and then sets those feeding channel 0 on the path to the map so
+    that the map finds dark ink on light paper (`InkInit`)."""
+    r = InkInit(seed, "baseline", sigma) if init == "ink" else Init(seed, init, sigma)
     b = PlanBuilder(h, w, 3)
     x = b.input
     act = "hardswish"
-    s1 = b.conv(x, r.w((3, 3, 3, 24), 27), r.b(24), k=(3, 3), s=(2, 2), pad=(1, 1, 1, 1),
-                fused=act)
-    s2a = b.conv(s1, r.w((2, 2, 24, 12), 96), r.b(12), k=(2, 2), pad=(0, 1, 0, 1), fused=act)
-    s2b = b.conv(s2a, r.w((2, 2, 12, 24), 48), r.b(24), k=(2, 2), pad=(0, 1, 0, 1), fused=act)
+    s1 = b.conv(x, r.w((3, 3, 3, 24), 27, role="stem"), r.b(24, role="stem"), k=(3, 3), s=(2, 2),
+                pad=(1, 1, 1, 1), fused=act)
+    s2a = b.conv(s1, r.w((2, 2, 24, 12), 96, role="carry"), r.b(12, role="carry"), k=(2, 2),
+                 pad=(0, 1, 0, 1), fused=act)
+    s2b = b.conv(s2a, r.w((2, 2, 12, 24), 48, role="carry"), r.b(24, role="carry"), k=(2, 2),
+                 pad=(0, 1, 0, 1), fused=act)
     pool = b.maxpool(s1)
-    s3 = b.conv(pool, r.w((3, 3, 48, 32), 9 * 48), r.b(32), k=(3, 3), s=(2, 2),
-                pad=(1, 1, 1, 1), fused=act, x2=s2b)
-    z = b.conv(s3, r.w((1, 1, 32, 32), 32), r.b(32), fused=act)
-    c2 = dw_block(b, z, r, k=3, cout=48)
+    s3 = b.conv(pool, r.w((3, 3, 48, 32), 9 * 48, role="box"), r.b(32, role="box"), k=(3, 3),
+                s=(2, 2), pad=(1, 1, 1, 1), fused=act, x2=s2b)
+    z = b.conv(s3, r.w((1, 1, 32, 32), 32, role="carry"), r.b(32, role="carry"), fused=act)
+    c2 = dw_block(b, z, r, k=3, cout=48, dw_role="hbox")
     z = dw_block(b, c2, r, k=3, s=(2, 2), cout=96)
     c3 = dw_block(b, z, r, k=3, cout=96)
     z = dw_block(b, c3, r, k=5, s=(2, 2), cout=192)
@@ -123,12 +194,12 @@ def detector_plan(*, h: int = 960, w: int = 960, seed: int = 3, init: str = "bas
     out4 = b.upsampleadd(in5, in4, 2)
     in3 = rse(b, c3, r, cout=96, k=1)
     out3 = b.upsampleadd(out4, in3, 2)
-    in2 = rse(b, c2, r, cout=96, k=1)
+    in2 = rse(b, c2, r, cout=96, k=1, role="carry")
     out2 = b.upsampleadd(out3, in2, 2)
     p5 = rse(b, in5, r, cout=24, k=3)
     p4 = rse(b, out4, r, cout=24, k=3)
     p3 = rse(b, out3, r, cout=24, k=3)
-    p2 = rse(b, out2, r, cout=24, k=3)
+    p2 = rse(b, out2, r, cout=24, k=3, role="hbox")
     up5 = b.upsample(p5, 8)
     up4 = b.upsample(p4, 4)
     cat = b.concat(up5, up4)
@@ -136,10 +207,12 @@ def detector_plan(*, h: int = 960, w: int = 960, seed: int = 3, init: str = "bas
     cat = b.concat(cat, up3)
     # DB head: 3x3 conv over [p5 x8 | p4 x4 | p3 x2] and p2, ReLU; two 2x2
     # transposed convolutions, ReLU then the sigmoid.
-    hd = b.conv(cat, r.w((3, 3, 96, 24), 9 * 96), r.b(24), k=(3, 3), pad=(1, 1, 1, 1),
-                fused="relu", x2=p2)
-    hd = b.convtranspose(hd, r.w((24, 2, 2, 24), 24), r.b(24), k=(2, 2), fused="relu")
-    prob = b.convtranspose(hd, r.w((24, 2, 2, 1), 24), r.b(1), k=(2, 2), fused="sigmoid")
+    hd = b.conv(cat, r.w((3, 3, 96, 24), 9 * 96, role="hbox@72"), r.b(24, role="carry"), k=(3, 3),
+                pad=(1, 1, 1, 1), fused="relu", x2=p2)
+    hd = b.convtranspose(hd, r.w((24, 2, 2, 24), 24, role="convt"), r.b(24, role="convt"), k=(2, 2),
+                         fused="relu")
+    prob = b.convtranspose(hd, r.w((24, 2, 2, 1), 24, role="convt_out"), r.b(1, role="convt_out"),
+                           k=(2, 2), fused="sigmoid")
     return b.to_bytes([prob])
 
 
@@ -202,6 +275,29 @@ def page_image(h: int = 960, w: int = 960, seed: int = 7) -> np.ndarray:
         region[strokes] = shade[strokes][:, None]
         y += band + int(rng.integers(12, 40))
     return ((img / 255.0 - 0.5) / 0.5).astype(np.float32)
+
+
+def letter_page(lines: int = 44, seed: int = 5, width: int = 2550, height: int = 3300) -> np.ndarray:
+    """A letter page at 300 dpi, HWC uint8 RGB: white paper with `lines`
+    seeded text-like lines of dark glyph blocks (24-30 px tall, word gaps),
+    one every (height - 300) / lines pixels between 150 px margins."""
+    rng = np.random.default_rng(seed)
+    img = np.full((height, width, 3), 255, np.uint8)
+    top, bottom = 150, height - 150
+    pitch = (bottom - top) / lines
+    for i in range(lines):
+        y0 = int(top + i * pitch + rng.integers(0, 8))
+        lh = int(rng.integers(24, 31))
+        x = int(rng.integers(150, 260))
+        end = int(rng.integers(width // 3, width - 150))
+        while x < end:
+            cw = int(rng.integers(14, 34))
+            glyph = rng.random((lh, cw)) < 0.4
+            img[y0:y0 + lh, x:x + cw][glyph] = int(rng.integers(0, 80))
+            x += cw + int(rng.integers(4, 12))
+            if rng.random() < 0.12:
+                x += int(rng.integers(20, 40))
+    return img
 
 
 def line_images(n: int = 16, h: int = 48, w: int = 320, seed: int = 11) -> np.ndarray:

@@ -1,0 +1,173 @@
+"""The worker's page path on one GPU: a page in, its text lines out.
+
+It follows the worker's `detect` and `read` (src/bin/ppocr-native/ocr.rs:
+202-261) as the page benchmark states them: the page's long side limited to
+960 (the `Limit::Max` rule of src/det.rs:166-193 with the side fixed at the
+limit, `scaled_size` and `snap32` of src/det.rs:10-27), the detector input
+made on the GPU from the uploaded page (`det_input_hwc`, src/det.rs:228-289)
+straight into the detector's input, the detector, the DB boxes on the host
+(`boxes_from_prob`, src/det.rs:291-452, reading order), then for each box
+the perspective crop (`crop_text`, src/crop.rs:84-127) and the recogniser
+input (`rec_input`, src/rec.rs:19-43, the tensor at most 320 wide: wider
+crops are squeezed to 320) made on the GPU straight into the recogniser's
+lanes, batches of 16 lanes (`recognise_all`, ocr.rs:436-530), and each
+lane's text and score (`ctc_decode`, src/rec.rs:112-161).
+
+Left out, as the benchmark leaves them out: RapidOCR's page fitting and
+padding (`prepare_page`), the text-score filter, and the vertical re-read.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import time
+from dataclasses import dataclass, field
+
+import numpy as np
+
+from . import GpuError, GpuModel, lib
+from .devmem import DeviceArray
+from .images import MEAN, STD, _check, _sig
+from .post import DbOptions, Dictionary, boxes_from_prob, ctc_decode_pairs
+
+REC_HEIGHT = 48
+
+
+def _snap32(x: int) -> int:
+    """Python's int(round(x / 32) * 32): halves to the even multiple."""
+    return int(round(x / 32.0)) * 32
+
+
+def det_size(width: int, height: int, limit: int = 960) -> tuple[int, int] | None:
+    """The detector input (width, height) for a page: both sides scaled by
+    limit / long side when the long side exceeds `limit`, truncated, then
+    snapped to multiples of 32 (src/det.rs:16-27); None when a side would
+    vanish."""
+    if width == 0 or height == 0:
+        return None
+    long = max(width, height)
+    ratio = limit / long if long > limit else 1.0
+    w, h = _snap32(int(width * ratio)), _snap32(int(height * ratio))
+    return (w, h) if w > 0 and h > 0 else None
+
+
+@dataclass
+class Line:
+    quad: np.ndarray  # [4][2] f32, page pixels: top-left, top-right, bottom-right, bottom-left
+    text: str
+    score: float
+
+
+@dataclass
+class PageTimes:
+    """Host wall time of each stage of the last page, milliseconds."""
+    detect: float = 0.0    # detector input + detector forward + map to the host
+    boxes: float = 0.0     # DB boxes on the host
+    read: float = 0.0      # crops + recogniser inputs + recogniser forwards
+    decode: float = 0.0    # CTC text on the host
+    lines: int = 0
+    batches: list[int] = field(default_factory=list)
+
+
+class PagePipeline:
+    """A detector and a recogniser (PPOCRPL1 plans) on the GPU and the
+    dictionary of the recogniser's classes."""
+
+    def __init__(self, det_plan: bytes, rec_plan: bytes, dictionary: Dictionary, *, limit: int = 960,
+                 batch: int = 16, max_width: int = 320, options: DbOptions | None = None):
+        self.det = GpuModel.load(det_plan)
+        self.rec = GpuModel.load(rec_plan)
+        self.dictionary = dictionary
+        self.limit, self.batch, self.max_width = limit, batch, max_width
+        self.options = options or DbOptions()
+        self._det_hw: tuple[int, int] | None = None
+        self._rec_sizes: list[tuple[int, int]] = []
+        self.times = PageTimes()
+        L = _sig()
+        self._L = L
+        self._mean = (C.c_double * 3)(*MEAN)
+        self._std = (C.c_double * 3)(*STD)
+
+    def close(self) -> None:
+        self.det.close()
+        self.rec.close()
+
+    def read(self, page: np.ndarray) -> list[Line]:
+        """The text lines of a uint8 H x W x 3 page on the host."""
+        a = np.ascontiguousarray(page, np.uint8)
+        if a.ndim != 3 or a.shape[2] != 3:
+            raise ValueError("an H x W x 3 page")
+        d = DeviceArray.of(a.reshape(-1))
+        try:
+            return self.read_device(d.addr, a.shape[1], a.shape[0])
+        finally:
+            d.free()
+
+    def read_device(self, page: int, width: int, height: int) -> list[Line]:
+        """The text lines of a page already on the device (uint8 HWC)."""
+        t = self.times = PageTimes()
+        t0 = time.perf_counter()
+        size = det_size(width, height, self.limit)
+        if size is None:
+            return []
+        w, h = size
+        if self._det_hw != (h, w):
+            self.det.set_input_size(h, w)
+            self._det_hw = (h, w)
+        dst, n = self.det.lane_input_device(0)
+        assert n == w * h * 3
+        _check(self._L.ppocr_hip_det_input(page, width, height, dst, w, h, self._mean, self._std,
+                                           self.det.stream() or None), "det_input")
+        self.det.run_device()
+        prob = self.det.lane_output(0, 0)
+        t1 = time.perf_counter()
+        quads = boxes_from_prob(prob, w, h, width, height, self.options)
+        t2 = time.perf_counter()
+        pairs = []
+        for s in range(0, len(quads), self.batch):
+            pairs += self._recognise(page, width, height, quads[s:s + self.batch])
+        t3 = time.perf_counter()
+        lines = [Line(q, *ctc_decode_pairs(p, self.dictionary)) for q, p in zip(quads, pairs)]
+        t4 = time.perf_counter()
+        t.detect, t.boxes, t.read, t.decode = ((t1 - t0) * 1e3, (t2 - t1) * 1e3, (t3 - t2) * 1e3,
+                                               (t4 - t3) * 1e3)
+        t.lines = len(lines)
+        return lines
+
+    def _recognise(self, page: int, width: int, height: int, quads: np.ndarray) -> list[np.ndarray]:
+        """One batch: the recogniser inputs of its boxes made from the page
+        in one launch on the recogniser's stream, one lane per box (48 rows,
+        the width `rec_input` gives the crop, capped), then the forward; the
+        [T][2] output of each lane."""
+        L = self._L
+        self.times.batches.append(len(quads))
+        qs = [np.ascontiguousarray(q, np.float32).reshape(8) for q in quads]
+        lanes = []
+        for q in qs:
+            cw, ch = C.c_size_t(), C.c_size_t()
+            if L.ppocr_crop_size(q.ctypes.data_as(C.POINTER(C.c_float)), C.byref(cw), C.byref(ch)):
+                raise GpuError("crop size")
+            rw = C.c_size_t()
+            tw = L.ppocr_rec_width_fit(cw.value, ch.value, self.max_width, C.byref(rw))
+            if tw == 0:
+                raise GpuError(f"an empty crop ({cw.value} x {ch.value})")
+            lanes.append((REC_HEIGHT, tw))
+        # A short last batch of lanes that all have one size keeps the full
+        # batch's lanes (their extra lanes compute on stale inputs and are not
+        # read: a lane's result does not depend on the others), so that the
+        # lanes are not set again for it and again for the next page.
+        if len(set(lanes)) == 1 and len(lanes) < self.batch:
+            lanes = lanes + [lanes[0]] * (self.batch - len(lanes))
+        if self._rec_sizes != lanes:
+            self.rec.set_sizes(lanes)
+            self._rec_sizes = lanes
+        outs = (C.c_void_p * len(qs))()
+        caps = (C.c_size_t * len(qs))()
+        for lane in range(len(qs)):
+            outs[lane], caps[lane] = self.rec.lane_input_device(lane)
+        flat = np.ascontiguousarray(np.stack(qs), np.float32)
+        got = (C.c_size_t * len(qs))()
+        _check(L.ppocr_hip_crop_rec_inputs(page, width, height, flat.ctypes.data_as(C.POINTER(C.c_float)),
+                                           len(qs), self.max_width, outs, caps, got,
+                                           self.rec.stream() or None), "crop_rec_inputs")
+        self.rec.run_device()
+        return [self.rec.lane_output(i, 0) for i in range(len(quads))]
