@@ -546,7 +546,7 @@ __device__ __forceinline__ float se_row(const float *w, const float *in, int n) 
 // grp.x says how the weights travel: 1 both layers at once, 2 the first,
 // then the second while the first is summed, 0 neither (each output reads
 // its row from global memory, when a layer is larger than LDS). Each
-// channel's partials are split between J threads (a fixed split, eight
+// channel's partials are split between J threads (a fixed split, sixteen
 // independent loads in flight per thread), joined in LDS in thread order.
 constexpr int kSePer = 9;
 constexpr int kSeThreads = 1024;
@@ -582,15 +582,13 @@ __global__ __launch_bounds__(1024) void mean_finish(Group<MeanJob> grp) {
     double s = 0.0;
     if (j < J) {
       const double *p = pl + c0 + ch;
-      int rr = j;
-      for (; rr + 7 * J < chunks; rr += 8 * J) {
-        double v[8];
+      for (int rr = j; rr < chunks; rr += 16 * J) {
+        double v[16];
 #pragma unroll
-        for (int k = 0; k < 8; k++) v[k] = p[(long)(rr + k * J) * c];
+        for (int k = 0; k < 16; k++) v[k] = rr + k * J < chunks ? p[(long)(rr + k * J) * c] : 0.0;
 #pragma unroll
-        for (int k = 0; k < 8; k++) s += v[k];
+        for (int k = 0; k < 16; k++) s += v[k];
       }
-      for (; rr < chunks; rr += J) s += p[(long)rr * c];
     }
     red[t] = s;
     __syncthreads();

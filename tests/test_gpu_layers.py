@@ -236,6 +236,36 @@ def test_upsampled_concat_sources(oracle):
     near(got, want)
 
 
+@pytest.mark.parametrize("co,hw,lanes", [(24, (40, 48), 2), (16, (13, 21), 3), (32, (30, 17), 1),
+                                         (20, (8, 8), 5)])
+def test_halo_conv_head_sources(oracle, co, hw, lanes):
+    # Halo tiles over 96 channels from four sources of 24, three of them
+    # upsampled by 8, 4 and 2 as in the DB head, maps whose sides are not
+    # multiples of the 16 x 4 tile, several lanes, and 16-column tiles when
+    # co <= 16.
+    c = 24
+    wq = RNG.normal(0, 0.3, (1, 1, 4, c)).astype(np.float32)
+    wh = RNG.normal(0, 0.2, (3, 3, 4 * c, co)).astype(np.float32)
+    bias = RNG.normal(0, 0.3, co).astype(np.float32)
+    h, w = hw
+    up = 8 if h % 8 == 0 and w % 8 == 0 else 1
+
+    def build(b, t):
+        full = b.conv(t, wq, None)
+        if up == 8:
+            half = b.avgpool(full, (2, 2), (2, 2))
+            quarter = b.avgpool(half, (2, 2), (2, 2))
+            eighth = b.avgpool(quarter, (2, 2), (2, 2))
+            cat = b.concat(b.upsample(eighth, 8), b.upsample(quarter, 4))
+            cat = b.concat(cat, b.upsample(half, 2))
+        else:
+            cat = b.concat(b.concat(full, b.conv(t, wq, None)), b.conv(t, wq, None))
+        return b.conv(cat, wh, bias, k=(3, 3), pad=(1, 1, 1, 1), fused="relu", x2=full)
+
+    got, want = both(build, (h, w, 4), oracle, lanes=lanes)
+    near(got, want)
+
+
 @pytest.mark.parametrize("mode", ["add", "resgate", "upsampleadd_resgate", "concat", "upsample"])
 def test_elementwise_exact(oracle, mode):
     c = 12
