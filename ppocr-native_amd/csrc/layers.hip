@@ -780,53 +780,65 @@ __global__ __launch_bounds__(64) void layernorm_kernel(const float *x, long x_la
   }
 }
 
-// One thread per row with the row in registers (MAXV float4s): the loads of
-// a row are independent and all in flight at once; the sums then run in
-// sequence as the CPU's do.
+// Blocks of 256 threads over kLnRows rows: first one thread per row with the
+// row in registers (MAXV float4s: the loads of a row are independent and all
+// in flight at once) runs the two sums in sequence as the CPU's do and keeps
+// the row's mean and root in LDS; then the whole block writes the outputs,
+// four values a thread at a time, each (x - mean) / root * gamma + beta.
+constexpr int kLnRows = 16;
+
 template <int MAXV>
-__global__ __launch_bounds__(64) void layernorm_rows(const float *x, long x_lane_stride,
-                                                    const float *w, int rows, int c, int lanes,
-                                                    float *y, long y_lane_stride) {
-  long row = (long)blockIdx.x * 64 + threadIdx.x;
-  if (row >= (long)rows * lanes) return;
-  int ln = (int)(row / rows);
-  long rl = row - (long)ln * rows;
-  const int nv = c / 4;
-  const f32x4 *xr = reinterpret_cast<const f32x4 *>(x + (long)ln * x_lane_stride + rl * c);
-  f32x4 v[MAXV];
+__global__ __launch_bounds__(256) void layernorm_rows(const float *x, long x_lane_stride,
+                                                     const float *w, int rows, int c, int lanes,
+                                                     float *y, long y_lane_stride) {
+  __shared__ float stat[2 * kLnRows];
+  const long total = (long)rows * lanes;
+  const long r0 = (long)blockIdx.x * kLnRows;
+  const int nv = c / 4, tid = threadIdx.x;
+  auto row_ptr = [&](long row, const float *base, long stride) {
+    const int ln = (int)(row / rows);
+    return base + (long)ln * stride + (row - (long)ln * rows) * c;
+  };
+  if (tid < kLnRows && r0 + tid < total) {
+    const f32x4 *xr = reinterpret_cast<const f32x4 *>(row_ptr(r0 + tid, x, x_lane_stride));
+    f32x4 v[MAXV];
 #pragma unroll
-  for (int k = 0; k < MAXV; k++)
-    if (k < nv) v[k] = xr[k];
-  float s = 0.0f;
+    for (int k = 0; k < MAXV; k++)
+      if (k < nv) v[k] = xr[k];
+    float s = 0.0f;
 #pragma unroll
-  for (int k = 0; k < MAXV; k++)
-    if (k < nv) s = (((s + v[k].x) + v[k].y) + v[k].z) + v[k].w;
-  const float mean = s / (float)c;
-  float q = 0.0f;
+    for (int k = 0; k < MAXV; k++)
+      if (k < nv) s = (((s + v[k].x) + v[k].y) + v[k].z) + v[k].w;
+    const float mean = s / (float)c;
+    float q = 0.0f;
 #pragma unroll
-  for (int k = 0; k < MAXV; k++) {
-    if (k < nv) {
-      float d0 = v[k].x - mean, d1 = v[k].y - mean, d2 = v[k].z - mean, d3 = v[k].w - mean;
-      q = q + d0 * d0;
-      q = q + d1 * d1;
-      q = q + d2 * d2;
-      q = q + d3 * d3;
+    for (int k = 0; k < MAXV; k++) {
+      if (k < nv) {
+        float d0 = v[k].x - mean, d1 = v[k].y - mean, d2 = v[k].z - mean, d3 = v[k].w - mean;
+        q = q + d0 * d0;
+        q = q + d1 * d1;
+        q = q + d2 * d2;
+        q = q + d3 * d3;
+      }
     }
+    stat[2 * tid] = mean;
+    stat[2 * tid + 1] = sqrtf(q / (float)c + w[2 * c]);
   }
-  const float r = sqrtf(q / (float)c + w[2 * c]);
+  __syncthreads();
   const f32x4 *g4 = reinterpret_cast<const f32x4 *>(w);
   const f32x4 *b4 = reinterpret_cast<const f32x4 *>(w + c);
-  f32x4 *yr = reinterpret_cast<f32x4 *>(y + (long)ln * y_lane_stride + rl * c);
-#pragma unroll
-  for (int k = 0; k < MAXV; k++) {
-    if (k < nv) {
-      f32x4 g = g4[k], b = b4[k], o;
-      o.x = (v[k].x - mean) / r * g.x + b.x;
-      o.y = (v[k].y - mean) / r * g.y + b.y;
-      o.z = (v[k].z - mean) / r * g.z + b.z;
-      o.w = (v[k].w - mean) / r * g.w + b.w;
-      yr[k] = o;
-    }
+  for (int e = tid; e < kLnRows * nv; e += 256) {
+    const int rr = e / nv, k = e - rr * nv;
+    if (r0 + rr >= total) break;
+    const f32x4 xv = reinterpret_cast<const f32x4 *>(row_ptr(r0 + rr, x, x_lane_stride))[k];
+    const float mean = stat[2 * rr], r = stat[2 * rr + 1];
+    const f32x4 g = g4[k], bb = b4[k];
+    f32x4 o;
+    o.x = (xv.x - mean) / r * g.x + bb.x;
+    o.y = (xv.y - mean) / r * g.y + bb.y;
+    o.z = (xv.z - mean) / r * g.z + bb.z;
+    o.w = (xv.w - mean) / r * g.w + bb.w;
+    reinterpret_cast<f32x4 *>(const_cast<float *>(row_ptr(r0 + rr, y, y_lane_stride)))[k] = o;
   }
 }
 
@@ -836,7 +848,7 @@ hipError_t launch_layernorm(const float *x, long x_lane_stride, const float *w, 
   auto a16 = [](const void *p) { return (uintptr_t(p) & 15) == 0; };
   if (c % 4 == 0 && c <= 128 && a16(x) && a16(y) && a16(w) && a16(w + c) &&
       x_lane_stride % 4 == 0 && y_lane_stride % 4 == 0) {
-    hipLaunchKernelGGL(layernorm_rows<32>, dim3(blocks_for(total, 64)), dim3(64), 0, s, x,
+    hipLaunchKernelGGL(layernorm_rows<32>, dim3(blocks_for(total, kLnRows)), dim3(256), 0, s, x,
                        x_lane_stride, w, rows, c, lanes, y, y_lane_stride);
     return hipGetLastError();
   }
@@ -978,6 +990,143 @@ __global__ __launch_bounds__(NT) void attention_kernel(const float *x, long x_la
   }
 }
 
+// The same three phases for a run of TQ query rows of one (lane, head):
+// blocks of 256 threads over (lane, head, run), so that a batch of short
+// lines still fills the GPU. K and V of the head (every row), the run's
+// pre-scaled queries and its scores sit in LDS with rows padded to HDV
+// floats, read as float4: a score's query and key rows as HDV / 4 vector
+// reads, an output thread's four dimensions of V per key as one. Every
+// value keeps the order above (the products and sums of a score over
+// d < hd only, each output's keys in order).
+template <int HDV>
+__global__ __launch_bounds__(256) void attention_rows(const float *x, long x_lane_stride, float scale, int t,
+                                                      int c, int heads, int runs, float *y, long y_lane_stride) {
+  extern __shared__ __attribute__((aligned(16))) float sm[];
+  const int hd = c / heads;
+  const int tq = (t + runs - 1) / runs;
+  const int blk = blockIdx.x;
+  const int run = blk % runs, lh = blk / runs;
+  const int ln = lh / heads, h = lh % heads;
+  const int q0 = run * tq, nq = min(tq, t - q0);
+  if (nq <= 0) return;
+  const int tid = threadIdx.x, ts = t + 1;
+  float *ks = sm;                      // t x HDV
+  float *vs = ks + t * HDV;            // t x HDV
+  float *qs = vs + t * HDV;            // tq x HDV, pre-scaled
+  float *sc = qs + tq * HDV;           // tq x ts
+  float *lane_max = sc + tq * ts;      // tq x 8
+  float *lane_sum = lane_max + tq * 8; // tq x 8
+  float *rmax = lane_sum + tq * 8;     // tq
+  float *rinv = rmax + tq;             // tq
+  const float *xl = x + (long)ln * x_lane_stride + h * hd;
+  for (int e = tid; e < t * HDV; e += 256) {
+    const int j = e / HDV, d = e - j * HDV;
+    const float *px = xl + (long)j * 3 * c + d;
+    ks[e] = d < hd ? px[c] : 0.0f;
+    vs[e] = d < hd ? px[2 * c] : 0.0f;
+  }
+  for (int e = tid; e < nq * HDV; e += 256) {
+    const int s = e / HDV, d = e - s * HDV;
+    qs[e] = d < hd ? xl[(long)(q0 + s) * 3 * c + d] * scale : 0.0f;
+  }
+  __syncthreads();
+  const int fused = t / 8 * 8;  // keys past it multiply and add separately
+  for (int e = tid; e < nq * t; e += 256) {
+    const int s = e / t, j = e - s * t;
+    f32x4 qv[HDV / 4], kv[HDV / 4];
+#pragma unroll
+    for (int u = 0; u < HDV / 4; u++) {
+      qv[u] = *reinterpret_cast<const f32x4 *>(qs + s * HDV + 4 * u);
+      kv[u] = *reinterpret_cast<const f32x4 *>(ks + j * HDV + 4 * u);
+    }
+    float acc = 0.0f;
+    if (j < fused) {
+#pragma unroll
+      for (int d = 0; d < HDV; d++)
+        if (d < hd) acc = fmaf(kv[d / 4][d % 4], qv[d / 4][d % 4], acc);
+    } else {
+#pragma unroll
+      for (int d = 0; d < HDV; d++)
+        if (d < hd) acc = acc + qv[d / 4][d % 4] * kv[d / 4][d % 4];
+    }
+    sc[s * ts + j] = acc;
+  }
+  __syncthreads();
+  const int body = t / 8 * 8;
+  const float ninf = -__builtin_inff();
+  for (int e = tid; e < nq * 8; e += 256) {
+    const int s = e >> 3, l = e & 7;
+    const float *row = sc + s * ts;
+    float m = ninf;
+    for (int j = l; j < body; j += 8) m = row[j] > m ? row[j] : m;
+    lane_max[e] = m;
+  }
+  __syncthreads();
+  for (int s = tid; s < nq; s += 256) {
+    const float *row = sc + s * ts;
+    float m = ninf;
+    for (int l = 0; l < 8; l++) m = fmaxf(m, lane_max[s * 8 + l]);
+    for (int j = body; j < t; j++) m = fmaxf(m, row[j]);
+    rmax[s] = m;
+  }
+  __syncthreads();
+  for (int e = tid; e < nq * 8; e += 256) {
+    const int s = e >> 3, l = e & 7;
+    float *row = sc + s * ts;
+    const float m = rmax[s];
+    float sum = 0.0f;
+    for (int j = l; j < body; j += 8) {
+      const float ex = exp_neg(row[j] - m);
+      row[j] = ex;
+      sum = sum + ex;
+    }
+    lane_sum[e] = sum;
+  }
+  __syncthreads();
+  for (int s = tid; s < nq; s += 256) {
+    float *row = sc + s * ts;
+    const float m = rmax[s];
+    float sum = 0.0f;
+    for (int l = 0; l < 8; l++) sum = sum + lane_sum[s * 8 + l];
+    for (int j = body; j < t; j++) {
+      const float ex = exp_neg(row[j] - m);
+      row[j] = ex;
+      sum = sum + ex;
+    }
+    rinv[s] = 1.0f / sum;
+  }
+  __syncthreads();
+  for (int e = tid; e < nq * t; e += 256) {
+    const int s = e / t, j = e - s * t;
+    sc[s * ts + j] = sc[s * ts + j] * rinv[s];
+  }
+  __syncthreads();
+  float *yl = y + (long)ln * y_lane_stride + h * hd;
+  for (int e = tid; e < nq * (HDV / 4); e += 256) {
+    const int s = e / (HDV / 4), d4 = e - s * (HDV / 4);
+    const float *p = sc + s * ts;
+    const float *v = vs + 4 * d4;
+    f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < t; j++) {
+      const f32x4 vv = *reinterpret_cast<const f32x4 *>(v + j * HDV);
+      const float pp = p[j];
+      acc.x = fmaf(vv.x, pp, acc.x);
+      acc.y = fmaf(vv.y, pp, acc.y);
+      acc.z = fmaf(vv.z, pp, acc.z);
+      acc.w = fmaf(vv.w, pp, acc.w);
+    }
+    float *o = yl + (long)(q0 + s) * c + 4 * d4;
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+      if (4 * d4 + k < hd) o[k] = acc[k];
+  }
+}
+
+static size_t attention_rows_floats(int t, int hdv, int runs) {
+  const size_t tq = (size_t)(t + runs - 1) / runs;
+  return (size_t)2 * t * hdv + tq * hdv + tq * (t + 1) + tq * 18;
+}
+
 static size_t attention_lds_floats(int t, int hd, bool scores) {
   return (size_t)3 * t * hd + (size_t)t * 18 + (scores ? (size_t)t * (t + 1) : 0);
 }
@@ -1020,6 +1169,24 @@ hipError_t launch_attention(const float *x, long x_lane_stride, float scale, int
                        c, heads, y, y_lane_stride, g);
     return hipGetLastError();
   };
+  // Lines whose K, V and a run's scores fit LDS: runs of query rows, enough
+  // blocks for two per CU.
+  const int hdv = hd <= 16 ? 16 : (hd <= 32 ? 32 : 64);
+  const int runs = std::max(1, std::min(t, (512 + lanes * heads - 1) / (lanes * heads)));
+  const size_t rshm = attention_rows_floats(t, hdv, runs) * sizeof(float);
+  if (rshm <= 64 * 1024) {
+    const long blocks = (long)lanes * heads * runs;
+    if (hdv == 16)
+      hipLaunchKernelGGL(attention_rows<16>, dim3((unsigned)blocks), dim3(256), rshm, s, x, x_lane_stride, scale, t,
+                         c, heads, runs, y, y_lane_stride);
+    else if (hdv == 32)
+      hipLaunchKernelGGL(attention_rows<32>, dim3((unsigned)blocks), dim3(256), rshm, s, x, x_lane_stride, scale, t,
+                         c, heads, runs, y, y_lane_stride);
+    else
+      hipLaunchKernelGGL(attention_rows<64>, dim3((unsigned)blocks), dim3(256), rshm, s, x, x_lane_stride, scale, t,
+                         c, heads, runs, y, y_lane_stride);
+    return hipGetLastError();
+  }
   if (hd <= 16) return go(attention_kernel<16, 1024>, 1024);
   if (hd <= 32) return go(attention_kernel<32, 512>, 512);
   return go(attention_kernel<64, 256>, 256);
