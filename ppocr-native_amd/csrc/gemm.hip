@@ -312,16 +312,26 @@ __global__ __launch_bounds__(256) void conv_mfma(ConvArgs a) {
       for (int r = 0; r < 4; r++) {
         const int m = m0 + wave * WM + i * 16 + lg * 4 + r;
         float v[NT];
-        float lm = -__builtin_inff(), lb = __builtin_inff();
+        float lm = -__builtin_inff(), lb = __builtin_inff(), ls = -__builtin_inff();
 #pragma unroll
         for (int j = 0; j < NT; j++) {
           const int n = n0 + j * 16 + li;
           v[j] = n < a.vocab ? acc[i][j][r] + a.bias[n] : -__builtin_inff();
-          if (v[j] > lm) lm = v[j], lb = (float)n;
+          if (v[j] > lm)
+            ls = lm, lm = v[j], lb = (float)n;
+          else if (v[j] > ls)
+            ls = v[j];
         }
         float gm = lm;
 #pragma unroll
         for (int d = 1; d < 16; d <<= 1) gm = fmaxf(gm, __shfl_xor(gm, d, 64));
+        // The tile's second value (the maximum again when two columns hold
+        // it), for the near-tie check of ctc_merge.
+        float g2 = lm == gm ? ls : lm;
+#pragma unroll
+        for (int d = 1; d < 16; d <<= 1) g2 = fmaxf(g2, __shfl_xor(g2, d, 64));
+        const unsigned long long held = __ballot(lm == gm);
+        if (__popcll((held >> (lane & 48)) & 0xffffull) >= 2) g2 = gm;
         const float c = gm * L;
         float sum = 0.0f;
 #pragma unroll
@@ -334,7 +344,7 @@ __global__ __launch_bounds__(256) void conv_mfma(ConvArgs a) {
         }
         if (li == 0 && m < M) {
           float4 *p = reinterpret_cast<float4 *>(a.part) + (long)m * ntn + tn;
-          *p = make_float4(gm, sum, b, 0.0f);
+          *p = make_float4(gm, sum, b, g2);
         }
       }
     }
@@ -575,14 +585,33 @@ __global__ __launch_bounds__(256) void conv_patch(Group<ConvArgs> grp) {
 }
 
 // One wave per row: join the row's tile partials, then y = (best, 1 / sum).
-__global__ __launch_bounds__(256) void ctc_merge(const float4 *part, int rows, int ntiles,
-                                                 float *y, long y_lane_stride, int rows_per_lane) {
+// The tiles also carry their second value: when the row's two largest
+// values lie within kCtcTie * max(1, |max|) of each other, the GPU's
+// summation order could have decided the argmax, so the wave recomputes the
+// logits of every column of every tile whose maximum is that close, in the
+// CPU's order (the bias, then a fused multiply-add per input in order,
+// src/engine/layers.rs:770-776), and takes the first column of their
+// maximum. Columns of the other tiles lie more than kCtcTie below on the GPU,
+// further than the two orders ever differ.
+constexpr float kCtcTie = 1.0f / 1024.0f;
+
+__device__ __forceinline__ void top2(float a1, float a2, float b1, float b2, float &m1, float &m2) {
+  m1 = fmaxf(a1, b1);
+  m2 = a1 > b1 ? fmaxf(a2, b1) : (b1 > a1 ? fmaxf(b2, a1) : a1);
+}
+
+__global__ __launch_bounds__(256) void ctc_merge(const float4 *part, int rows, int ntiles, float *y,
+                                                 long y_lane_stride, int rows_per_lane, CtcExact ex) {
   int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   int lane = threadIdx.x & 63;
   if (row >= rows) return;
   CtcState st{-__builtin_inff(), 0.0f, __builtin_inff()};
+  float m2 = -__builtin_inff();
   for (int t = lane; t < ntiles; t += 64) {
     float4 p = part[(long)row * ntiles + t];
+    float n1, n2;
+    top2(st.m, m2, p.x, p.w, n1, n2);
+    m2 = n2;
     st = ctc_join(st, CtcState{p.x, p.y, p.z});
   }
 #pragma unroll
@@ -591,13 +620,45 @@ __global__ __launch_bounds__(256) void ctc_merge(const float4 *part, int rows, i
     o.m = __shfl_xor(st.m, d, 64);
     o.s = __shfl_xor(st.s, d, 64);
     o.b = __shfl_xor(st.b, d, 64);
+    const float o2 = __shfl_xor(m2, d, 64);
+    float n1, n2;
+    top2(st.m, m2, o.m, o2, n1, n2);
+    m2 = n2;
     st = ctc_join(st, o);
   }
+  // Every lane holds the row's joined values: the check is uniform.
+  const int ln = row / rows_per_lane, tr = row - ln * rows_per_lane;
+  float best = st.b;
+  const float tie = kCtcTie * fmaxf(1.0f, fabsf(st.m));
+  if (ex.wt && st.m - m2 <= tie) {
+    const float *x = ex.x + (long)ln * ex.x_lane_stride + (long)tr * ex.ci;
+    float bm = -__builtin_inff(), bb = __builtin_inff();
+    for (int t = 0; t < ntiles; t++) {
+      if (part[(long)row * ntiles + t].x < st.m - tie) continue;
+      const int c1 = min((t + 1) * ex.tile_n, ex.vocab);
+      for (int c0 = t * ex.tile_n; c0 < c1; c0 += 64) {
+        const int col = c0 + lane;
+        float v = -__builtin_inff(), cb = __builtin_inff();
+        if (col < c1) {
+          const float *w = ex.wt + (long)col * ex.wt_k;
+          v = ex.bias[col];
+          for (int i = 0; i < ex.ci; i++) v = fmaf(w[i], x[i], v);
+          cb = (float)col;
+        }
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+          const float ov = __shfl_xor(v, d, 64), ob = __shfl_xor(cb, d, 64);
+          if (ov > v || (ov == v && ob < cb)) v = ov, cb = ob;
+        }
+        if (v > bm || (v == bm && cb < bb)) bm = v, bb = cb;
+      }
+    }
+    best = bb;
+  }
   if (lane == 0) {
-    int ln = row / rows_per_lane, t = row - ln * rows_per_lane;
-    float *out = y + (long)ln * y_lane_stride + 2 * t;
-    out[0] = st.b;
-    out[1] = 1.0f / st.s;
+    float *yp = y + (long)ln * y_lane_stride + 2L * tr;
+    yp[0] = best;
+    yp[1] = 1.0f / st.s;
   }
 }
 
@@ -1187,11 +1248,11 @@ hipError_t launch_conv_patch_group(const ConvArgs *as, int n, int wr, int bk, in
 }
 
 hipError_t launch_ctc_merge(const float *part, int rows, int ntiles, float *y, long y_lane_stride,
-                            int rows_per_lane, hipStream_t s) {
+                            int rows_per_lane, const CtcExact &ex, hipStream_t s) {
   if (rows <= 0) return hipSuccess;
   hipLaunchKernelGGL(ctc_merge, dim3((rows + 3) / 4), dim3(256), 0, s,
                      reinterpret_cast<const float4 *>(part), rows, ntiles, y, y_lane_stride,
-                     rows_per_lane);
+                     rows_per_lane, ex);
   return hipGetLastError();
 }
 

@@ -110,8 +110,21 @@ hipError_t launch_conv_patch(const ConvArgs &a, int wr, int bk, int bn, hipStrea
 hipError_t launch_conv_patch_group(const ConvArgs *a, int n, int wr, int bk, int bn, hipStream_t s);
 
 // CTC choice from the GEMM's per-tile partials: y[2m] = best, y[2m+1] = 1/sum.
+// `ex` names the head's input rows and weights, for rows whose two largest
+// logits are too close for the GPU's summation order to decide (wt null:
+// no such check).
+struct CtcExact {
+  const float *x;      // the head's input: rows_per_lane rows of ci per lane
+  long x_lane_stride;
+  int ci;
+  const float *wt;     // packed weights: column n's ci inputs at wt + n * wt_k
+  long wt_k;
+  const float *bias;   // per column
+  int vocab;
+  int tile_n;          // columns per GEMM tile (the partials' width)
+};
 hipError_t launch_ctc_merge(const float *part, int rows, int ntiles, float *y, long y_lane_stride,
-                            int rows_per_lane, hipStream_t s);
+                            int rows_per_lane, const CtcExact &ex, hipStream_t s);
 
 // ---------------------------------------------------------------- depthwise
 

@@ -922,8 +922,9 @@ void Model::build_launches(Batch &b) {
         int ntn = (a.n + t.bn - 1) / t.bn;
         int rows = L * int(op.iw), T = int(op.iw);
         b.launches.push_back({"ctc_gemm", s.op, [a, t](hipStream_t st) { return launch_conv(a, t, st); }});
-        b.launches.push_back({"ctc_merge", s.op, [part, rows, ntn, Y, ys, T](hipStream_t st) {
-                                return launch_ctc_merge(part, rows, ntn, Y, ys, T, st);
+        const CtcExact ex{a.src[0].p, a.src[0].lane_stride, int(op.ic), a.wt, a.wt_k, a.bias, a.vocab, t.bn};
+        b.launches.push_back({"ctc_merge", s.op, [part, rows, ntn, Y, ys, T, ex](hipStream_t st) {
+                                return launch_ctc_merge(part, rows, ntn, Y, ys, T, ex, st);
                               }});
         break;
       }

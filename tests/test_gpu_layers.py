@@ -398,3 +398,33 @@ def test_ctc_argmax(oracle, vocab):
         a, b = gl[0].reshape(-1, 2), wl[0].reshape(-1, 2)
         assert np.array_equal(a[:, 0], b[:, 0])
         np.testing.assert_allclose(a[:, 1], b[:, 1], rtol=1e-5, atol=1e-5)
+
+
+def test_ctc_argmax_near_ties(oracle):
+    # Groups of ten columns that differ by one ulp in a few weights: within a
+    # group the logits differ by less than the rounding of a 120-term sum, so
+    # the summation order decides the argmax among them, the CPU's one way,
+    # the GPU's (MFMA) another. The near-tie check recomputes such rows in
+    # the CPU's order, so the indices match the oracle's exactly. Also two
+    # identical columns (an exact tie: the first one wins).
+    c, vocab, group = 120, 700, 10
+    w = np.empty((c, vocab), np.float32)
+    for g in range(vocab // group):
+        base = RNG.normal(0, 1 / np.sqrt(c), c).astype(np.float32)
+        for k in range(group):
+            col = base.copy()
+            for i in RNG.choice(c, 3, replace=False):
+                col[i] = np.nextafter(col[i], np.float32(np.inf) if RNG.random() < 0.5 else np.float32(-np.inf))
+            w[:, g * group + k] = col
+    bias = np.repeat(RNG.normal(0, 0.5, vocab // group).astype(np.float32), group)
+    w[:, 401], bias[401] = w[:, 77], bias[77]
+
+    def build(b, t):
+        return b.ctcargmax(t, w, bias)
+
+    got, want = both(build, (1, 40, c), oracle, lanes=3, seed=5)
+    for gl, wl in zip(got, want):
+        a, b = gl[0].reshape(-1, 2), wl[0].reshape(-1, 2)
+        assert np.array_equal(a[:, 0], b[:, 0]), np.flatnonzero(a[:, 0] != b[:, 0])
+        np.testing.assert_allclose(a[:, 1], b[:, 1], rtol=1e-5, atol=1e-5)
+    assert 401 not in {int(v) for gl in got for v in gl[0].reshape(-1, 2)[:, 0]}
