@@ -1037,12 +1037,9 @@ static hipError_t go_ring1(const ConvArgs *as, int n, hipStream_t s) {
   }
   grp.first[n] = (int)total;
   if (lds > kMaxLdsBytes) return hipErrorInvalidValue;
-  static bool raised = false;  // once per instantiation: the limit is a property of the kernel
-  if (!raised) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(conv_ring<MT, NT, ST, BK, GATE, WIN>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxLdsBytes);
+  if (lds > 64 * 1024) {
+    hipError_t e = allow_lds(reinterpret_cast<const void *>(conv_ring<MT, NT, ST, BK, GATE, WIN>), (int)kMaxLdsBytes);
     if (e != hipSuccess) return e;
-    raised = true;
   }
   hipLaunchKernelGGL((conv_ring<MT, NT, ST, BK, GATE, WIN>), dim3((unsigned)total), dim3(256), lds, s, grp);
   return hipGetLastError();
@@ -1210,13 +1207,8 @@ static hipError_t go_patch(const ConvArgs *as, int n, hipStream_t s) {
   grp.first[n] = (int)blocks;
   if (shm > 160 * 1024) return hipErrorInvalidValue;
   if (shm > 64 * 1024) {
-    static bool raised = false;  // once per process: the limit is a property of the kernel
-    if (!raised) {
-      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(conv_patch<WR, BN, CB>),
-                                         hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-      if (e != hipSuccess) return e;
-      raised = true;
-    }
+    hipError_t e = allow_lds(reinterpret_cast<const void *>(conv_patch<WR, BN, CB>), 160 * 1024);
+    if (e != hipSuccess) return e;
   }
   hipLaunchKernelGGL((conv_patch<WR, BN, CB>), dim3((unsigned)blocks), dim3(256), shm, s, grp);
   return hipGetLastError();

@@ -9,7 +9,28 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include <mutex>
+#include <set>
+#include <tuple>
+
 namespace ppocr {
+
+// Lets `kernel` take up to `bytes` of dynamic LDS on the current device: the
+// attribute is set once per device, kernel and size (several handles may
+// launch from several threads, on several devices).
+inline hipError_t allow_lds(const void *kernel, int bytes) {
+  static std::mutex mu;
+  static std::set<std::tuple<int, const void *, int>> done;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  std::lock_guard<std::mutex> lock(mu);
+  const auto key = std::make_tuple(dev, kernel, bytes);
+  if (done.count(key)) return hipSuccess;
+  e = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  if (e == hipSuccess) done.insert(key);
+  return e;
+}
 
 // ---------------------------------------------------------------- GEMM conv
 

@@ -703,13 +703,9 @@ hipError_t launch_mean_group(const MeanJob *jobs, int n, hipStream_t s) {
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
-  static bool raised = false;  // once per process: the limit is a property of the kernel
-  if (!raised) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(mean_finish),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       (int)(kMaxLds - kSeThreads * sizeof(double)));
+  if (shm > 64 * 1024 - kSeThreads * sizeof(double)) {
+    hipError_t e = allow_lds(reinterpret_cast<const void *>(mean_finish), (int)(kMaxLds - kSeThreads * sizeof(double)));
     if (e != hipSuccess) return e;
-    raised = true;
   }
   hipLaunchKernelGGL(mean_finish, dim3((unsigned)b2), dim3(1024), shm, s, second);
   return hipGetLastError();
@@ -1155,15 +1151,11 @@ hipError_t launch_attention(const float *x, long x_lane_stride, float scale, int
   if (shm > kMaxLds) return hipErrorInvalidValue;
   float *g = lds ? nullptr : scratch;
   auto go = [&](auto kernel, int nt) {
-    // Allowed once per kernel, before any use beyond 64 KiB (and so before a
-    // graph capture records such a launch).
-    static bool allowed[3] = {false, false, false};
-    bool &done = allowed[nt == 1024 ? 0 : (nt == 512 ? 1 : 2)];
-    if (shm > 64 * 1024 && !done) {
-      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
-                                         hipFuncAttributeMaxDynamicSharedMemorySize, int(kMaxLds));
+    // Allowed before any use beyond 64 KiB (and so before a graph capture
+    // records such a launch).
+    if (shm > 64 * 1024) {
+      hipError_t e = allow_lds(reinterpret_cast<const void *>(kernel), int(kMaxLds));
       if (e != hipSuccess) return e;
-      done = true;
     }
     hipLaunchKernelGGL(kernel, dim3(lanes * heads), dim3(nt), shm, s, x, x_lane_stride, scale, t,
                        c, heads, y, y_lane_stride, g);
