@@ -111,6 +111,14 @@ float *ppocr_gpu_lane_input_device(ppocr_gpu_model *model, size_t lane, size_t *
  * `ppocr_gpu_lane_output`; synchronous. */
 int ppocr_gpu_run_device(ppocr_gpu_model *model, char *err, size_t err_len);
 
+/* The same, returning once the forward and the copies of the results are
+ * queued on the model's stream; `ppocr_gpu_wait` then waits for them. The
+ * host output buffers and the device inputs are in use until then. Lets one
+ * thread keep several handles (a page's detector, several recogniser
+ * batches) busy at once. */
+int ppocr_gpu_run_device_async(ppocr_gpu_model *model, char *err, size_t err_len);
+int ppocr_gpu_wait(ppocr_gpu_model *model, char *err, size_t err_len);
+
 /* Runs record their launches in a HIP graph from the second run after the
  * lanes were set, and replay it (default, `enable` 1); with 0 every run
  * launches each kernel itself. Returns 0, or 1 for a NULL model. */

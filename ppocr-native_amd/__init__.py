@@ -64,6 +64,8 @@ def lib() -> C.CDLL:
         "ppocr_gpu_stream": ([vp], vp),
         "ppocr_gpu_lane_input_device": ([vp, sz, szp], vp),
         "ppocr_gpu_run_device": ([vp, cp, sz], C.c_int),
+        "ppocr_gpu_run_device_async": ([vp, cp, sz], C.c_int),
+        "ppocr_gpu_wait": ([vp, cp, sz], C.c_int),
         "ppocr_gpu_set_graphs": ([vp, C.c_int], C.c_int),
         "ppocr_gpu_launch_count": ([vp], sz),
         "ppocr_gpu_launch_name": ([vp, sz, szp], cp),
@@ -186,6 +188,13 @@ class GpuModel:
     def run_device(self) -> None:
         """`run` over inputs already written on the device."""
         _call(lib().ppocr_gpu_run_device, self._h)
+
+    def run_device_async(self) -> None:
+        """`run_device` queued on the model's stream; `wait()` ends it."""
+        _call(lib().ppocr_gpu_run_device_async, self._h)
+
+    def wait(self) -> None:
+        _call(lib().ppocr_gpu_wait, self._h)
 
     # Measurement helpers.
     def upload(self) -> None:

@@ -199,7 +199,7 @@ struct Model {
   void build_launches(Batch &b);
   void account(Batch &b) const;
   void group(Batch &b) const;
-  bool run(bool copy_in, bool copy_out, std::string &err);
+  bool run(bool copy_in, bool copy_out, std::string &err, bool sync = true);
   std::vector<size_t> step_reads(const Step &s) const;
   size_t step_writes(const Step &s) const;
 };
@@ -1534,7 +1534,7 @@ bool Model::launch_all(std::string &err) {
   return true;
 }
 
-bool Model::run(bool copy_in, bool copy_out, std::string &err) {
+bool Model::run(bool copy_in, bool copy_out, std::string &err, bool sync) {
   HIPTRY(hipSetDevice(device), "selecting the GPU");
   if (lane_at.empty()) return err = "no lanes are set", false;
   if (copy_in) {
@@ -1559,7 +1559,7 @@ bool Model::run(bool copy_in, bool copy_out, std::string &err) {
                "copying the results");
     }
   }
-  HIPTRY(hipStreamSynchronize(stream), "running the plan");
+  if (sync) HIPTRY(hipStreamSynchronize(stream), "running the plan");
   return true;
 }
 
@@ -1664,6 +1664,21 @@ int ppocr_gpu_run_device(ppocr_gpu_model *model, char *err, size_t err_len) {
   if (!model) return put_err("no model", err, err_len), 1;
   std::string e;
   if (!model->m.run(false, true, e)) return put_err(e, err, err_len), 1;
+  return 0;
+}
+
+int ppocr_gpu_run_device_async(ppocr_gpu_model *model, char *err, size_t err_len) {
+  if (!model) return put_err("no model", err, err_len), 1;
+  std::string e;
+  if (!model->m.run(false, true, e, false)) return put_err(e, err, err_len), 1;
+  return 0;
+}
+
+int ppocr_gpu_wait(ppocr_gpu_model *model, char *err, size_t err_len) {
+  if (!model) return put_err("no model", err, err_len), 1;
+  hipSetDevice(model->m.device);
+  const hipError_t r = hipStreamSynchronize(model->m.stream);
+  if (r != hipSuccess) return put_err(std::string("running the plan: ") + hipGetErrorString(r), err, err_len), 1;
   return 0;
 }
 

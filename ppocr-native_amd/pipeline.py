@@ -10,8 +10,10 @@ straight into the detector's input, the detector, the DB boxes on the host
 the perspective crop (`crop_text`, src/crop.rs:84-127) and the recogniser
 input (`rec_input`, src/rec.rs:19-43, the tensor at most 320 wide: wider
 crops are squeezed to 320) made on the GPU straight into the recogniser's
-lanes, batches of 16 lanes (`recognise_all`, ocr.rs:436-530), and each
-lane's text and score (`ctc_decode`, src/rec.rs:112-161).
+lanes, batches of 16 lanes (`recognise_all`, ocr.rs:436-530) on up to three
+recogniser handles at once, and each lane's text and score (`ctc_decode`,
+src/rec.rs:112-161). Over several pages the next page's detector runs while
+the host finds this page's boxes.
 
 Left out, as the benchmark leaves them out: RapidOCR's page fitting and
 padding (`prepare_page`), the text-score filter, and the vertical re-read.
@@ -69,18 +71,25 @@ class PageTimes:
 
 
 class PagePipeline:
-    """A detector and a recogniser (PPOCRPL1 plans) on the GPU and the
-    dictionary of the recogniser's classes."""
+    """A detector and `recognisers` recogniser handles (PPOCRPL1 plans) on
+    the GPU, and the dictionary of the recogniser's classes.
+
+    A page's recogniser batches go to the handles in turn and run at the
+    same time on their own streams; over several pages (`read_pages`) the
+    next page's detector runs on the GPU while this page's boxes are found
+    on the host."""
 
     def __init__(self, det_plan: bytes, rec_plan: bytes, dictionary: Dictionary, *, limit: int = 960,
-                 batch: int = 16, max_width: int = 320, options: DbOptions | None = None):
+                 batch: int = 16, max_width: int = 320, options: DbOptions | None = None,
+                 recognisers: int = 3):
         self.det = GpuModel.load(det_plan)
-        self.rec = GpuModel.load(rec_plan)
+        self.recs = [GpuModel.load(rec_plan) for _ in range(max(1, recognisers))]
+        self.rec = self.recs[0]
         self.dictionary = dictionary
         self.limit, self.batch, self.max_width = limit, batch, max_width
         self.options = options or DbOptions()
         self._det_hw: tuple[int, int] | None = None
-        self._rec_sizes: list[tuple[int, int]] = []
+        self._rec_sizes: list[list[tuple[int, int]]] = [[] for _ in self.recs]
         self.times = PageTimes()
         L = _sig()
         self._L = L
@@ -89,7 +98,8 @@ class PagePipeline:
 
     def close(self) -> None:
         self.det.close()
-        self.rec.close()
+        for r in self.recs:
+            r.close()
 
     def read(self, page: np.ndarray) -> list[Line]:
         """The text lines of a uint8 H x W x 3 page on the host."""
@@ -104,11 +114,50 @@ class PagePipeline:
 
     def read_device(self, page: int, width: int, height: int) -> list[Line]:
         """The text lines of a page already on the device (uint8 HWC)."""
+        return self.read_pages([(page, width, height)])[0]
+
+    def read_pages(self, pages: list[tuple[int, int, int]]) -> list[list[Line]]:
+        """The text lines of each page (device address, width, height), in
+        order; each page's detector runs while the page before is read."""
+        out: list[list[Line]] = []
+        if not pages:
+            return out
         t = self.times = PageTimes()
         t0 = time.perf_counter()
+        sizes = [None] * len(pages)
+        sizes[0] = self._detect(*pages[0])
+        for k, (page, width, height) in enumerate(pages):
+            if sizes[k] is None:
+                out.append([])
+                if k + 1 < len(pages):
+                    sizes[k + 1] = self._detect(*pages[k + 1])
+                continue
+            self.det.wait()
+            prob = self.det.lane_output(0, 0)
+            if k + 1 < len(pages):
+                sizes[k + 1] = self._detect(*pages[k + 1])
+            t1 = time.perf_counter()
+            w, h = sizes[k]
+            quads = boxes_from_prob(prob, w, h, width, height, self.options)
+            t2 = time.perf_counter()
+            pairs = self._recognise(page, width, height, quads)
+            t3 = time.perf_counter()
+            out.append([Line(q, *ctc_decode_pairs(p, self.dictionary)) for q, p in zip(quads, pairs)])
+            t4 = time.perf_counter()
+            t.detect += (t1 - t0) * 1e3
+            t.boxes += (t2 - t1) * 1e3
+            t.read += (t3 - t2) * 1e3
+            t.decode += (t4 - t3) * 1e3
+            t.lines += len(out[-1])
+            t0 = t4
+        return out
+
+    def _detect(self, page: int, width: int, height: int) -> tuple[int, int] | None:
+        """Queues the page's detector input and forward on the detector's
+        stream; the detector input size, or None for a page too thin."""
         size = det_size(width, height, self.limit)
         if size is None:
-            return []
+            return None
         w, h = size
         if self._det_hw != (h, w):
             self.det.set_input_size(h, w)
@@ -117,29 +166,39 @@ class PagePipeline:
         assert n == w * h * 3
         _check(self._L.ppocr_hip_det_input(page, width, height, dst, w, h, self._mean, self._std,
                                            self.det.stream() or None), "det_input")
-        self.det.run_device()
-        prob = self.det.lane_output(0, 0)
-        t1 = time.perf_counter()
-        quads = boxes_from_prob(prob, w, h, width, height, self.options)
-        t2 = time.perf_counter()
-        pairs = []
-        for s in range(0, len(quads), self.batch):
-            pairs += self._recognise(page, width, height, quads[s:s + self.batch])
-        t3 = time.perf_counter()
-        lines = [Line(q, *ctc_decode_pairs(p, self.dictionary)) for q, p in zip(quads, pairs)]
-        t4 = time.perf_counter()
-        t.detect, t.boxes, t.read, t.decode = ((t1 - t0) * 1e3, (t2 - t1) * 1e3, (t3 - t2) * 1e3,
-                                               (t4 - t3) * 1e3)
-        t.lines = len(lines)
-        return lines
+        self.det.run_device_async()
+        return size
 
     def _recognise(self, page: int, width: int, height: int, quads: np.ndarray) -> list[np.ndarray]:
-        """One batch: the recogniser inputs of its boxes made from the page
-        in one launch on the recogniser's stream, one lane per box (48 rows,
-        the width `rec_input` gives the crop, capped), then the forward; the
-        [T][2] output of each lane."""
+        """The [T][2] recogniser output of each box: batches of `batch` boxes
+        on the recogniser handles in turn, each queued (inputs made from the
+        page in one launch, then the forward) before the first is waited for."""
         L = self._L
-        self.times.batches.append(len(quads))
+        groups = [quads[s:s + self.batch] for s in range(0, len(quads), self.batch)]
+        out: list[np.ndarray | None] = [None] * len(quads)
+        busy: dict[int, tuple[int, int]] = {}  # handle -> (first box, boxes)
+
+        def collect(r: int) -> None:
+            first, n = busy.pop(r)
+            self.recs[r].wait()
+            for i in range(n):
+                out[first + i] = self.recs[r].lane_output(i, 0)
+
+        for g, group in enumerate(groups):
+            r = g % len(self.recs)
+            if r in busy:
+                collect(r)
+            self.times.batches.append(len(group))
+            self._queue_batch(r, page, width, height, group)
+            busy[r] = (g * self.batch, len(group))
+        for r in list(busy):
+            collect(r)
+        return out
+
+    def _queue_batch(self, r: int, page: int, width: int, height: int, quads: np.ndarray) -> None:
+        """Recogniser handle r's lanes for one batch: 48 rows, the width
+        `rec_input` gives the crop (capped); inputs and forward queued."""
+        L, rec = self._L, self.recs[r]
         qs = [np.ascontiguousarray(q, np.float32).reshape(8) for q in quads]
         lanes = []
         for q in qs:
@@ -157,17 +216,16 @@ class PagePipeline:
         # lanes are not set again for it and again for the next page.
         if len(set(lanes)) == 1 and len(lanes) < self.batch:
             lanes = lanes + [lanes[0]] * (self.batch - len(lanes))
-        if self._rec_sizes != lanes:
-            self.rec.set_sizes(lanes)
-            self._rec_sizes = lanes
+        if self._rec_sizes[r] != lanes:
+            rec.set_sizes(lanes)
+            self._rec_sizes[r] = lanes
         outs = (C.c_void_p * len(qs))()
         caps = (C.c_size_t * len(qs))()
         for lane in range(len(qs)):
-            outs[lane], caps[lane] = self.rec.lane_input_device(lane)
+            outs[lane], caps[lane] = rec.lane_input_device(lane)
         flat = np.ascontiguousarray(np.stack(qs), np.float32)
         got = (C.c_size_t * len(qs))()
         _check(L.ppocr_hip_crop_rec_inputs(page, width, height, flat.ctypes.data_as(C.POINTER(C.c_float)),
                                            len(qs), self.max_width, outs, caps, got,
-                                           self.rec.stream() or None), "crop_rec_inputs")
-        self.rec.run_device()
-        return [self.rec.lane_output(i, 0) for i in range(len(quads))]
+                                           rec.stream() or None), "crop_rec_inputs")
+        rec.run_device_async()

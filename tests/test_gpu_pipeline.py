@@ -159,3 +159,24 @@ def test_page_pipeline_again_and_other_sizes(dictionary):
     assert len(second) >= 15
     a.close()
     b.close()
+
+
+def test_read_pages_equals_single_reads(dictionary):
+    # Several pages through read_pages (each page's detector queued while
+    # the page before is read, recogniser batches on three handles at once)
+    # give what one read per page gives, through one recogniser handle.
+    det_plan = nets.detector_plan(h=960, w=736, init="ink")
+    rec_plan = nets.recognizer_plan(init="scaled")
+    pages = [nets.letter_page(seed=5), nets.letter_page(lines=20, seed=9, width=2200, height=1700),
+             nets.letter_page(lines=30, seed=13)]
+    one = PagePipeline(det_plan, rec_plan, dictionary, recognisers=1)
+    want = [one.read(p) for p in pages]
+    many = PagePipeline(det_plan, rec_plan, dictionary)
+    dev = [DeviceArray.of(p.reshape(-1)) for p in pages]
+    got = many.read_pages([(d.addr, p.shape[1], p.shape[0]) for d, p in zip(dev, pages)])
+    assert len(got) == 3
+    for g, w in zip(got, want):
+        assert [(x.text, x.quad.tolist(), x.score) for x in g] == [(x.text, x.quad.tolist(), x.score) for x in w]
+    assert sum(len(g) for g in got) >= 80
+    one.close()
+    many.close()
