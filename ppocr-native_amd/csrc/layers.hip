@@ -102,8 +102,8 @@ __global__ __launch_bounds__(256) void dwconv_kernel(DwArgs a) {
 // Threads of a block of the depthwise kernel that also sums its outputs.
 constexpr int kDwMeanThreads = 256;
 
-template <int K, int S, int DX, bool MEAN>
-__global__ __launch_bounds__(MEAN ? kDwMeanThreads : 256) void dwconv_fixed(DwArgs a) {
+template <int K, int S, int DX, bool MEAN, int TB = 256>
+__global__ __launch_bounds__(MEAN ? TB : 256) void dwconv_fixed(DwArgs a) {
   constexpr int SPAN = (DX - 1) * S + K;
   const int cv = a.c / 4;
   const int runs = (a.ow + DX - 1) / DX;
@@ -112,7 +112,7 @@ __global__ __launch_bounds__(MEAN ? kDwMeanThreads : 256) void dwconv_fixed(DwAr
   if constexpr (MEAN) {
     // Block = R runs of one lane x every channel group, so that the block
     // can sum its outputs per channel (dw_mean_blocks blocks per lane).
-    const int R = kDwMeanThreads / cv;
+    const int R = TB / cv;
     const int r = threadIdx.x / cv;
     ch = (threadIdx.x - r * cv) * 4;
     const int rg = blockIdx.x * R + r;
@@ -191,11 +191,11 @@ __global__ __launch_bounds__(MEAN ? kDwMeanThreads : 256) void dwconv_fixed(DwAr
   }
   if constexpr (MEAN) {
     // The block's f64 sums per channel, its runs joined in order.
-    __shared__ double red[kDwMeanThreads * 4];
+    __shared__ double red[TB * 4];
 #pragma unroll
     for (int k = 0; k < 4; k++) red[threadIdx.x * 4 + k] = sum[k];
     __syncthreads();
-    const int R = kDwMeanThreads / cv;
+    const int R = TB / cv;
     if ((int)threadIdx.x < cv) {
       double tot[4] = {0.0, 0.0, 0.0, 0.0};
       for (int r = 0; r < R; r++)
@@ -215,6 +215,15 @@ static hipError_t launch_fixed(F kernel, dim3 grid, dim3 block, const DwArgs &a,
 }
 
 static constexpr int kDwRun = 4;  // outputs per thread along a row
+
+// Outputs per thread along a row: four, or one when the layer is small (a
+// few thread-rows of float4 per SIMD), so that its threads fill the GPU.
+// With the channel sums the block count is the count of partial rows the
+// mean joins, so those layers keep four (one output a thread in blocks four
+// times as wide, to keep that count, ran slower: fewer blocks than CUs).
+static int dw_run(const DwArgs &a) {
+  return (long)a.lanes * a.oh * a.ow * (a.c / 4) < (1L << 18) && !a.mean_part ? 1 : kDwRun;
+}
 
 // The fixed-window variants: (kernel, stride) pairs with a template, the
 // height-only strides (the recogniser's (2, 1) stages) run as stride 1.
@@ -238,26 +247,32 @@ bool dw_mean_supported(const DwArgs &a) { return a.c % 4 == 0 && a.c <= 1024 && 
 
 int dw_mean_blocks(const DwArgs &a) {
   const int cv = a.c / 4, R = kDwMeanThreads / cv;
-  const int runs = (a.ow + kDwRun - 1) / kDwRun;
+  const int runs = (a.ow + kDwRun - 1) / kDwRun;  // the run with the sums (dw_run)
   return (a.oh * runs + R - 1) / R;
 }
 
-template <bool MEAN>
+template <bool MEAN, int DX, int TB>
 static hipError_t launch_dw_fixed(int kind, dim3 grid, const DwArgs &a, hipStream_t s) {
-  constexpr int DX = kDwRun;
-  const dim3 block(MEAN ? kDwMeanThreads : 256);
+  const dim3 block(MEAN ? TB : 256);
   switch (kind) {
-    case 31: return launch_fixed(dwconv_fixed<3, 1, DX, MEAN>, grid, block, a, s);
-    case 32: return launch_fixed(dwconv_fixed<3, 2, DX, MEAN>, grid, block, a, s);
-    case 51: return launch_fixed(dwconv_fixed<5, 1, DX, MEAN>, grid, block, a, s);
-    case 52: return launch_fixed(dwconv_fixed<5, 2, DX, MEAN>, grid, block, a, s);
-    case 71: return launch_fixed(dwconv_fixed<7, 1, DX, MEAN>, grid, block, a, s);
+    case 31: return launch_fixed(dwconv_fixed<3, 1, DX, MEAN, TB>, grid, block, a, s);
+    case 32: return launch_fixed(dwconv_fixed<3, 2, DX, MEAN, TB>, grid, block, a, s);
+    case 51: return launch_fixed(dwconv_fixed<5, 1, DX, MEAN, TB>, grid, block, a, s);
+    case 52: return launch_fixed(dwconv_fixed<5, 2, DX, MEAN, TB>, grid, block, a, s);
+    case 71: return launch_fixed(dwconv_fixed<7, 1, DX, MEAN, TB>, grid, block, a, s);
   }
   return hipErrorInvalidValue;
 }
 
+template <bool MEAN>
+static hipError_t launch_dw_fixed(int kind, dim3 grid, const DwArgs &a, hipStream_t s) {
+  if (MEAN) return launch_dw_fixed<true, kDwRun, kDwMeanThreads>(kind, grid, a, s);
+  return dw_run(a) == 1 ? launch_dw_fixed<false, 1, 256>(kind, grid, a, s)
+                        : launch_dw_fixed<false, kDwRun, 256>(kind, grid, a, s);
+}
+
 hipError_t launch_dwconv(const DwArgs &a, hipStream_t s) {
-  constexpr int DX = kDwRun;
+  const int DX = dw_run(a);
   auto aligned = [](const void *p) { return p == nullptr || (uintptr_t(p) & 15) == 0; };
   bool vec = a.c % 4 == 0 && aligned(a.x) && aligned(a.y) && aligned(a.w) && aligned(a.bias) &&
              a.x_lane_stride % 4 == 0 && a.y_lane_stride % 4 == 0;
@@ -271,10 +286,14 @@ hipError_t launch_dwconv(const DwArgs &a, hipStream_t s) {
   long total = (long)a.lanes * a.oh * runs * (vec ? a.c / 4 : a.c);
   dim3 grid(blocks_for(total, 256));
   if (vec && kind) return launch_dw_fixed<false>(kind, grid, a, s);
-  if (vec)
-    hipLaunchKernelGGL((dwconv_kernel<4, DX>), grid, dim3(256), 0, s, a);
+  if (vec && DX == 1)
+    hipLaunchKernelGGL((dwconv_kernel<4, 1>), grid, dim3(256), 0, s, a);
+  else if (vec)
+    hipLaunchKernelGGL((dwconv_kernel<4, kDwRun>), grid, dim3(256), 0, s, a);
+  else if (DX == 1)
+    hipLaunchKernelGGL((dwconv_kernel<1, 1>), grid, dim3(256), 0, s, a);
   else
-    hipLaunchKernelGGL((dwconv_kernel<1, DX>), grid, dim3(256), 0, s, a);
+    hipLaunchKernelGGL((dwconv_kernel<1, kDwRun>), grid, dim3(256), 0, s, a);
   return hipGetLastError();
 }
 
