@@ -631,27 +631,61 @@ __global__ __launch_bounds__(256) void ctc_merge(const float4 *part, int rows, i
   float best = st.b;
   const float tie = kCtcTie * fmaxf(1.0f, fabsf(st.m));
   if (ex.wt && st.m - m2 <= tie) {
+    // The candidate tiles' logits again, each column's multiply-adds in
+    // channel order from its bias: 64-column chunks of the candidate tiles,
+    // four at a time so that each lane runs four independent chains. The
+    // lane keeps the greatest logit (the lowest column among equal ones);
+    // the wave joins the lanes once at the end, the same total order.
     const float *x = ex.x + (long)ln * ex.x_lane_stride + (long)tr * ex.ci;
     float bm = -__builtin_inff(), bb = __builtin_inff();
+    int c0s[4] = {0, 0, 0, 0}, c1s[4] = {0, 0, 0, 0}, nq = 0;
+    auto run = [&]() {
+      float v[4];
+      const float *w[4];
+      bool ok[4];
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        const int col = c0s[k] + lane;
+        ok[k] = k < nq && col < c1s[k];
+        const int cc = ok[k] ? col : 0;  // a valid row to read; the value is dropped
+        w[k] = ex.wt + (long)cc * ex.wt_k;
+        v[k] = ex.bias[cc];
+      }
+      int i = 0;
+      for (; i + 4 <= ex.ci; i += 4) {
+        const float x0 = x[i], x1 = x[i + 1], x2 = x[i + 2], x3 = x[i + 3];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+          const float4 wv = *reinterpret_cast<const float4 *>(w[k] + i);
+          v[k] = fmaf(wv.x, x0, v[k]);
+          v[k] = fmaf(wv.y, x1, v[k]);
+          v[k] = fmaf(wv.z, x2, v[k]);
+          v[k] = fmaf(wv.w, x3, v[k]);
+        }
+      }
+      for (; i < ex.ci; i++)
+#pragma unroll
+        for (int k = 0; k < 4; k++) v[k] = fmaf(w[k][i], x[i], v[k]);
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        const float cb = (float)(c0s[k] + lane);
+        if (ok[k] && (v[k] > bm || (v[k] == bm && cb < bb))) bm = v[k], bb = cb;
+      }
+      nq = 0;
+    };
     for (int t = 0; t < ntiles; t++) {
       if (part[(long)row * ntiles + t].x < st.m - tie) continue;
       const int c1 = min((t + 1) * ex.tile_n, ex.vocab);
       for (int c0 = t * ex.tile_n; c0 < c1; c0 += 64) {
-        const int col = c0 + lane;
-        float v = -__builtin_inff(), cb = __builtin_inff();
-        if (col < c1) {
-          const float *w = ex.wt + (long)col * ex.wt_k;
-          v = ex.bias[col];
-          for (int i = 0; i < ex.ci; i++) v = fmaf(w[i], x[i], v);
-          cb = (float)col;
-        }
-#pragma unroll
-        for (int d = 1; d < 64; d <<= 1) {
-          const float ov = __shfl_xor(v, d, 64), ob = __shfl_xor(cb, d, 64);
-          if (ov > v || (ov == v && ob < cb)) v = ov, cb = ob;
-        }
-        if (v > bm || (v == bm && cb < bb)) bm = v, bb = cb;
+        c0s[nq] = c0, c1s[nq] = c1, nq++;
+        if (nq == 4) run();
       }
+    }
+    if (nq) run();
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const float ov = __shfl_xor(bm, d, 64), ob = __shfl_xor(bb, d, 64);
+      if (ov > bm || (ov == bm && ob < bb)) bm = ov, bb = ob;
     }
     best = bb;
   }
@@ -1242,6 +1276,8 @@ hipError_t launch_conv_patch_group(const ConvArgs *as, int n, int wr, int bk, in
 hipError_t launch_ctc_merge(const float *part, int rows, int ntiles, float *y, long y_lane_stride,
                             int rows_per_lane, const CtcExact &ex, hipStream_t s) {
   if (rows <= 0) return hipSuccess;
+  // The recompute reads packed rows as float4.
+  if (ex.wt && (ex.wt_k % 4 || (uintptr_t(ex.wt) & 15))) return hipErrorInvalidValue;
   hipLaunchKernelGGL(ctc_merge, dim3((rows + 3) / 4), dim3(256), 0, s,
                      reinterpret_cast<const float4 *>(part), rows, ntiles, y, y_lane_stride,
                      rows_per_lane, ex);
