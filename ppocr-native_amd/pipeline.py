@@ -13,7 +13,8 @@ crops are squeezed to 320) made on the GPU straight into the recogniser's
 lanes, batches of 16 lanes (`recognise_all`, ocr.rs:436-530) on up to three
 recogniser handles at once, and each lane's text and score (`ctc_decode`,
 src/rec.rs:112-161). Over several pages the next page's detector runs while
-the host finds this page's boxes.
+the host finds this page's boxes, and the host finds the next page's boxes
+while the GPU reads this page's lines.
 
 Left out, as the benchmark leaves them out: RapidOCR's page fitting and
 padding (`prepare_page`), the text-score filter, and the vertical re-read.
@@ -118,39 +119,85 @@ class PagePipeline:
 
     def read_pages(self, pages: list[tuple[int, int, int]]) -> list[list[Line]]:
         """The text lines of each page (device address, width, height), in
-        order; each page's detector runs while the page before is read."""
+        order. While the GPU reads a page's lines, the host finds the next
+        page's boxes (its detector queued meanwhile), so that host and GPU
+        work overlap."""
         out: list[list[Line]] = []
         if not pages:
             return out
-        t = self.times = PageTimes()
-        t0 = time.perf_counter()
-        sizes = [None] * len(pages)
+        self.times = PageTimes()
+        sizes: list[tuple[int, int] | None] = [None] * len(pages)
         sizes[0] = self._detect(*pages[0])
+        quads = self._boxes(0, pages, sizes)
         for k, (page, width, height) in enumerate(pages):
-            if sizes[k] is None:
-                out.append([])
-                if k + 1 < len(pages):
-                    sizes[k + 1] = self._detect(*pages[k + 1])
-                continue
+            job = self._queue_page(page, width, height, quads)
+            following = self._boxes(k + 1, pages, sizes) if k + 1 < len(pages) else None
+            pairs = self._finish_page(job)
+            t0 = time.perf_counter()
+            out.append([Line(q, *ctc_decode_pairs(p, self.dictionary)) for q, p in zip(quads, pairs)])
+            self.times.decode += (time.perf_counter() - t0) * 1e3
+            self.times.lines += len(out[-1])
+            quads = following
+        return out
+
+    def _boxes(self, k: int, pages: list[tuple[int, int, int]], sizes: list) -> np.ndarray:
+        """Page k's boxes: waits for its detector, queues page k + 1's, then
+        the DB boxes on the host (none for a page too thin)."""
+        t0 = time.perf_counter()
+        prob = None
+        if sizes[k] is not None:
             self.det.wait()
             prob = self.det.lane_output(0, 0)
-            if k + 1 < len(pages):
-                sizes[k + 1] = self._detect(*pages[k + 1])
-            t1 = time.perf_counter()
-            w, h = sizes[k]
-            quads = boxes_from_prob(prob, w, h, width, height, self.options)
-            t2 = time.perf_counter()
-            pairs = self._recognise(page, width, height, quads)
-            t3 = time.perf_counter()
-            out.append([Line(q, *ctc_decode_pairs(p, self.dictionary)) for q, p in zip(quads, pairs)])
-            t4 = time.perf_counter()
-            t.detect += (t1 - t0) * 1e3
-            t.boxes += (t2 - t1) * 1e3
-            t.read += (t3 - t2) * 1e3
-            t.decode += (t4 - t3) * 1e3
-            t.lines += len(out[-1])
-            t0 = t4
-        return out
+        if k + 1 < len(pages):
+            sizes[k + 1] = self._detect(*pages[k + 1])
+        t1 = time.perf_counter()
+        self.times.detect += (t1 - t0) * 1e3
+        if prob is None:
+            return np.zeros((0, 4, 2), np.float32)
+        w, h = sizes[k]
+        _, width, height = pages[k]
+        quads = boxes_from_prob(prob, w, h, width, height, self.options)
+        self.times.boxes += (time.perf_counter() - t1) * 1e3
+        return quads
+
+    def _queue_page(self, page: int, width: int, height: int, quads: np.ndarray) -> dict:
+        """Queues the page's first recogniser batches, one per handle."""
+        t0 = time.perf_counter()
+        groups = [quads[s:s + self.batch] for s in range(0, len(quads), self.batch)]
+        job = {"page": (page, width, height), "groups": groups, "next": 0, "busy": {},
+               "out": [None] * len(quads)}
+        while job["next"] < min(len(groups), len(self.recs)):
+            self._queue_group(job)
+        self.times.read += (time.perf_counter() - t0) * 1e3
+        return job
+
+    def _queue_group(self, job: dict) -> None:
+        g = job["next"]
+        r = g % len(self.recs)
+        if r in job["busy"]:
+            self._collect(job, r)
+        group = job["groups"][g]
+        self.times.batches.append(len(group))
+        self._queue_batch(r, *job["page"], group)
+        job["busy"][r] = (g * self.batch, len(group))
+        job["next"] = g + 1
+
+    def _collect(self, job: dict, r: int) -> None:
+        first, n = job["busy"].pop(r)
+        self.recs[r].wait()
+        for i in range(n):
+            job["out"][first + i] = self.recs[r].lane_output(i, 0)
+
+    def _finish_page(self, job: dict) -> list[np.ndarray]:
+        """The [T][2] recogniser output of each box: the page's remaining
+        batches queued as handles come free, then every batch collected."""
+        t0 = time.perf_counter()
+        while job["next"] < len(job["groups"]):
+            self._queue_group(job)
+        for r in list(job["busy"]):
+            self._collect(job, r)
+        self.times.read += (time.perf_counter() - t0) * 1e3
+        return job["out"]
 
     def _detect(self, page: int, width: int, height: int) -> tuple[int, int] | None:
         """Queues the page's detector input and forward on the detector's
@@ -168,32 +215,6 @@ class PagePipeline:
                                            self.det.stream() or None), "det_input")
         self.det.run_device_async()
         return size
-
-    def _recognise(self, page: int, width: int, height: int, quads: np.ndarray) -> list[np.ndarray]:
-        """The [T][2] recogniser output of each box: batches of `batch` boxes
-        on the recogniser handles in turn, each queued (inputs made from the
-        page in one launch, then the forward) before the first is waited for."""
-        L = self._L
-        groups = [quads[s:s + self.batch] for s in range(0, len(quads), self.batch)]
-        out: list[np.ndarray | None] = [None] * len(quads)
-        busy: dict[int, tuple[int, int]] = {}  # handle -> (first box, boxes)
-
-        def collect(r: int) -> None:
-            first, n = busy.pop(r)
-            self.recs[r].wait()
-            for i in range(n):
-                out[first + i] = self.recs[r].lane_output(i, 0)
-
-        for g, group in enumerate(groups):
-            r = g % len(self.recs)
-            if r in busy:
-                collect(r)
-            self.times.batches.append(len(group))
-            self._queue_batch(r, page, width, height, group)
-            busy[r] = (g * self.batch, len(group))
-        for r in list(busy):
-            collect(r)
-        return out
 
     def _queue_batch(self, r: int, page: int, width: int, height: int, quads: np.ndarray) -> None:
         """Recogniser handle r's lanes for one batch: 48 rows, the width
