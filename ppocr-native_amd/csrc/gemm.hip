@@ -403,7 +403,13 @@ constexpr int kWeightPer = 9;
 
 template <int WR, int BN, int CB>
 __global__ __launch_bounds__(256) void conv_patch(Group<ConvArgs> grp) {
-  const int prob = group_problem(grp);
+  // Each XCD takes a contiguous run of tiles (xcd_tile): neighbouring tiles
+  // share halo rows and columns, which then meet in one L2.
+  const int bid = xcd_tile((int)blockIdx.x, (int)gridDim.x);
+  int prob = 0;
+#pragma unroll
+  for (int k = 1; k < kGroupMax; k++)
+    if (k < grp.n && bid >= grp.first[k]) prob = k;
   const ConvArgs &a = grp.a[prob];
   const int tiles_x = grp.x[prob], tiles_y = grp.y[prob];
   constexpr int S = CB + 4;        // LDS row of one pixel / one (n, tap)
@@ -420,7 +426,7 @@ __global__ __launch_bounds__(256) void conv_patch(Group<ConvArgs> grp) {
   float *Bs = lds + PR * PC * S;       // nr x taps x S, then one zero row of S
 
   const int ntn = (a.n + BN - 1) / BN;
-  int t = (int)blockIdx.x - grp.first[prob];
+  int t = bid - grp.first[prob];
   const int tn = t % ntn;
   t /= ntn;
   const int tx0 = (t % tiles_x) * TW;
