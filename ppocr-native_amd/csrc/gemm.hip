@@ -67,19 +67,6 @@ __device__ __forceinline__ ConvSrc pick_src(const ConvArgs &a, int c) {
   return s;
 }
 
-// Workgroup i of a launch runs on XCD i % 8 (the dispatcher deals them round
-// robin) and each XCD has its own L2. Renumber so that each XCD takes one
-// contiguous run of tiles: neighbouring row tiles, which share input rows of
-// a window (and, with several column tiles, the same A rows), then meet in
-// the same L2 instead of each XCD fetching them from HBM. A bijection on
-// [0, groups): the first groups % 8 XCDs take one tile more.
-__device__ __forceinline__ int xcd_tile(int i, int groups) {
-  const int per = (groups + 7) >> 3;
-  const int tall = (groups & 7) ? (groups & 7) : 8;
-  const int xcd = i & 7, local = i >> 3;
-  return xcd < tall ? xcd * per + local : tall * per + (xcd - tall) * (per - 1) + local;
-}
-
 // How a tile's A operand (the input patch of each row) is read.
 //  L_FLAT: any channel count, one float at a time over taps * channels.
 //  L_SOURCES: up to four sources (upsampled by 2^shift), four channels at a

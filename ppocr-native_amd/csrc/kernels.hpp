@@ -60,6 +60,19 @@ struct Group {
   A a[kGroupMax];
 };
 
+// Workgroup i of a launch runs on XCD i % 8 (the dispatcher deals them round
+// robin) and each XCD has its own L2. Renumber so that each XCD takes one
+// contiguous run of tiles: neighbouring row tiles, which share input rows of
+// a window (and, with several column tiles, the same A rows), then meet in
+// the same L2 instead of each XCD fetching them from HBM. A bijection on
+// [0, groups): the first groups % 8 XCDs take one tile more.
+__device__ __forceinline__ int xcd_tile(int i, int groups) {
+  const int per = (groups + 7) >> 3;
+  const int tall = (groups & 7) ? (groups & 7) : 8;
+  const int xcd = i & 7, local = i >> 3;
+  return xcd < tall ? xcd * per + local : tall * per + (xcd - tall) * (per - 1) + local;
+}
+
 // The problem of a grouped launch that workgroup blockIdx.x belongs to.
 template <typename A>
 __device__ __forceinline__ int group_problem(const Group<A> &g) {

@@ -121,7 +121,9 @@ __global__ __launch_bounds__(MEAN ? TB : 256) void dwconv_fixed(DwArgs a) {
     oy = rg / runs;
     run = rg - oy * runs;
   } else {
-    const long g = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    // Blocks numbered XCD by XCD (xcd_tile): neighbouring output rows, which
+    // read the same input rows, meet in one L2.
+    const long g = (long)xcd_tile((int)blockIdx.x, (int)gridDim.x) * blockDim.x + threadIdx.x;
     const long total = (long)a.lanes * a.oh * runs * cv;
     if (g >= total) return;
     ch = (int)(g % cv) * 4;
