@@ -107,16 +107,21 @@ __global__ __launch_bounds__(MEAN ? TB : 256) void dwconv_fixed(DwArgs a) {
   constexpr int SPAN = (DX - 1) * S + K;
   const int cv = a.c / 4;
   const int runs = (a.ow + DX - 1) / DX;
-  int ch, run, oy, ln;
+  int ch, run, oy, ln, bx = 0;
   bool live;
   if constexpr (MEAN) {
     // Block = R runs of one lane x every channel group, so that the block
     // can sum its outputs per channel (dw_mean_blocks blocks per lane).
+    // Blocks numbered XCD by XCD over the whole grid (xcd_tile); a block's
+    // sums go to the slot of the rows it computed, so the join order stays.
     const int R = TB / cv;
     const int r = threadIdx.x / cv;
     ch = (threadIdx.x - r * cv) * 4;
-    const int rg = blockIdx.x * R + r;
-    ln = blockIdx.y;
+    const int nbx = (int)gridDim.x;
+    const int lin = xcd_tile((int)(blockIdx.y * gridDim.x + blockIdx.x), (int)(gridDim.x * gridDim.y));
+    bx = lin % nbx;
+    const int rg = bx * R + r;
+    ln = lin / nbx;
     live = r < R && rg < a.oh * runs;
     oy = rg / runs;
     run = rg - oy * runs;
@@ -203,7 +208,7 @@ __global__ __launch_bounds__(MEAN ? TB : 256) void dwconv_fixed(DwArgs a) {
       for (int r = 0; r < R; r++)
 #pragma unroll
         for (int k = 0; k < 4; k++) tot[k] += red[(r * cv + threadIdx.x) * 4 + k];
-      double *out = a.mean_part + ((long)ln * gridDim.x + blockIdx.x) * a.c + threadIdx.x * 4;
+      double *out = a.mean_part + ((long)ln * gridDim.x + bx) * a.c + threadIdx.x * 4;
 #pragma unroll
       for (int k = 0; k < 4; k++) out[k] = tot[k];
     }
