@@ -123,7 +123,9 @@ __global__ __launch_bounds__(256) void conv_stem_kernel(DirectArgs a) {
   for (int e = threadIdx.x; e < K * OC; e += 256) ws[e] = a.w[e];
   __syncthreads();
   const int per = a.oh * a.ow, total = a.lanes * per;
-  const int g0 = blockIdx.x * 256, g = g0 + threadIdx.x;
+  // Blocks numbered XCD by XCD (xcd_tile): neighbouring output rows, which
+  // read the same input rows, meet in one L2.
+  const int g0 = xcd_tile((int)blockIdx.x, (int)gridDim.x) * 256, g = g0 + threadIdx.x;
   if (g < total) {
     const int ln = g / per, rem = g - ln * per;
     const int oy = rem / a.ow, ox = rem - oy * a.ow;
@@ -202,7 +204,9 @@ __global__ __launch_bounds__(256) void conv_direct_pix(DirectArgs a) {
   for (int e = threadIdx.x; e < K * OC; e += 256) ws[e] = a.w[e];
   __syncthreads();
   const int per = a.oh * a.ow, total = a.lanes * per;
-  const int g0 = blockIdx.x * 256, g = g0 + threadIdx.x;
+  // Blocks numbered XCD by XCD (xcd_tile): neighbouring output rows, which
+  // read the same input rows, meet in one L2.
+  const int g0 = xcd_tile((int)blockIdx.x, (int)gridDim.x) * 256, g = g0 + threadIdx.x;
   if (g < total) {
     const int ln = g / per, rem = g - ln * per;
     const int oy = rem / a.ow, ox = rem - oy * a.ow;

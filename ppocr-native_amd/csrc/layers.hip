@@ -439,7 +439,9 @@ template <int V>
 __global__ __launch_bounds__(256) void pool_kernel(PoolArgs a) {
   const int cv = a.c / V;
   long per = (long)a.oh * a.ow * cv;
-  long g = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  // Blocks numbered XCD by XCD (xcd_tile): neighbouring output rows, which
+  // read the same input rows, meet in one L2.
+  long g = (long)xcd_tile((int)blockIdx.x, (int)gridDim.x) * blockDim.x + threadIdx.x;
   if (g >= (long)a.lanes * per) return;
   int ln = (int)(g / per);
   long off = g - (long)ln * per;
