@@ -112,20 +112,23 @@ bool direct_supported(int kh, int kw, int ic) { return kh * kw * ic <= kDirectTa
 
 // The RGB stem, 3x3 over 3 channels to OC (a multiple of 8): every output
 // from its bias, every column fused (the stem rule, src/engine/conv.rs:
-// 146-236). Thread = one output pixel and all OC channels; the block's 256
-// pixels x OC outputs are one run of memory (within a lane), written back
-// from LDS as whole float4 rows instead of OC scattered floats per thread.
-template <int OC>
+// 146-236). A block holds 256 / QS pixels; wave-uniform quarter (or half) q
+// of the threads computes outputs q * OC / QS .. of every pixel, so that a
+// small map still fills the GPU. The block's pixels x OC outputs are one run
+// of memory (within a lane), written back from LDS as whole float4 rows.
+template <int OC, int QS>
 __global__ __launch_bounds__(256) void conv_stem_kernel(DirectArgs a) {
-  constexpr int K = 27;
+  constexpr int K = 27, PB = 256 / QS, OQ = OC / QS;
+  static_assert(OQ % 4 == 0 && PB % 64 == 0, "float4 columns, whole waves per part");
   __shared__ __attribute__((aligned(16))) float ws[K * OC];
-  __shared__ __attribute__((aligned(16))) float out[256 * OC];
+  __shared__ __attribute__((aligned(16))) float out[PB * OC];
   for (int e = threadIdx.x; e < K * OC; e += 256) ws[e] = a.w[e];
   __syncthreads();
   const int per = a.oh * a.ow, total = a.lanes * per;
+  const int pl = threadIdx.x % PB, q = threadIdx.x / PB;
   // Blocks numbered XCD by XCD (xcd_tile): neighbouring output rows, which
   // read the same input rows, meet in one L2.
-  const int g0 = xcd_tile((int)blockIdx.x, (int)gridDim.x) * 256, g = g0 + threadIdx.x;
+  const int g0 = xcd_tile((int)blockIdx.x, (int)gridDim.x) * PB, g = g0 + pl;
   if (g < total) {
     const int ln = g / per, rem = g - ln * per;
     const int oy = rem / a.ow, ox = rem - oy * a.ow;
@@ -144,18 +147,18 @@ __global__ __launch_bounds__(256) void conv_stem_kernel(DirectArgs a) {
         for (int i = 0; i < 3; i++) patch[(ky * 3 + kx) * 3 + i] = ok ? px[i] : 0.0f;
       }
     }
-    float acc[OC];
+    float acc[OQ];
 #pragma unroll
-    for (int j = 0; j < OC; j++) acc[j] = a.bias ? a.bias[j] : 0.0f;
+    for (int j = 0; j < OQ; j++) acc[j] = a.bias ? a.bias[q * OQ + j] : 0.0f;
 #pragma unroll
     for (int t = 0; t < 9; t++) {
       if (!in[t]) continue;
 #pragma unroll
       for (int i = 0; i < 3; i++) {
         const float v = patch[t * 3 + i];
-        const float *wr = ws + (t * 3 + i) * OC;
+        const float *wr = ws + (t * 3 + i) * OC + q * OQ;
 #pragma unroll
-        for (int j = 0; j < OC; j += 4) {
+        for (int j = 0; j < OQ; j += 4) {
           const float4 w = *reinterpret_cast<const float4 *>(wr + j);
           acc[j] = fmaf(w.x, v, acc[j]);
           acc[j + 1] = fmaf(w.y, v, acc[j + 1]);
@@ -164,14 +167,14 @@ __global__ __launch_bounds__(256) void conv_stem_kernel(DirectArgs a) {
         }
       }
     }
-    float *o = out + threadIdx.x * OC;
+    float *o = out + pl * OC + q * OQ;
 #pragma unroll
-    for (int j = 0; j < OC; j += 4)
+    for (int j = 0; j < OQ; j += 4)
       *reinterpret_cast<float4 *>(o + j) =
           make_float4(act(acc[j], a.act), act(acc[j + 1], a.act), act(acc[j + 2], a.act), act(acc[j + 3], a.act));
   }
   __syncthreads();
-  const int n = min(256, total - g0);
+  const int n = min(PB, total - g0);
   const int l0 = g0 / per, l1 = (g0 + n - 1) / per;
   if (l0 == l1) {
     float4 *dst = reinterpret_cast<float4 *>(a.y + (long)l0 * a.y_lane_stride + (long)(g0 - l0 * per) * OC);
@@ -291,21 +294,21 @@ hipError_t launch_conv_direct(const DirectArgs &a, hipStream_t s) {
   const bool stem = a.kh == 3 && a.kw == 3 && a.ic == 3 && a.first_end >= a.ow && a.fused >= a.oc &&
                     (reinterpret_cast<uintptr_t>(a.y) & 15) == 0 && a.y_lane_stride % 4 == 0;
   const unsigned blocks = (unsigned)((n + 255) / 256);
-  if (stem && a.oc == 16) {
-    hipLaunchKernelGGL(conv_stem_kernel<16>, dim3(blocks), dim3(256), 0, s, a);
-    return hipGetLastError();
-  }
-  if (stem && a.oc == 24) {
-    hipLaunchKernelGGL(conv_stem_kernel<24>, dim3(blocks), dim3(256), 0, s, a);
-    return hipGetLastError();
-  }
-  if (stem && a.oc == 32) {
-    hipLaunchKernelGGL(conv_stem_kernel<32>, dim3(blocks), dim3(256), 0, s, a);
-    return hipGetLastError();
-  }
-  if (stem && a.oc == 48) {
-    hipLaunchKernelGGL(conv_stem_kernel<48>, dim3(blocks), dim3(256), 0, s, a);
-    return hipGetLastError();
+  // The stem: 256 pixels a block, each thread all outputs of one pixel; on a
+  // map too small for that to fill the GPU (under two blocks a CU), 64
+  // pixels a block with a quarter of the outputs a wave, or 128 for 24
+  // outputs (halves of 12).
+  if (stem) {
+    const bool split = blocks < 512;
+    const unsigned b64 = (unsigned)((n + 63) / 64), b128 = (unsigned)((n + 127) / 128);
+    auto go = [&](auto kernel, unsigned nb) {
+      hipLaunchKernelGGL(kernel, dim3(nb), dim3(256), 0, s, a);
+      return hipGetLastError();
+    };
+    if (a.oc == 16) return split ? go(conv_stem_kernel<16, 4>, b64) : go(conv_stem_kernel<16, 1>, blocks);
+    if (a.oc == 24) return split ? go(conv_stem_kernel<24, 2>, b128) : go(conv_stem_kernel<24, 1>, blocks);
+    if (a.oc == 32) return split ? go(conv_stem_kernel<32, 4>, b64) : go(conv_stem_kernel<32, 1>, blocks);
+    if (a.oc == 48) return split ? go(conv_stem_kernel<48, 4>, b64) : go(conv_stem_kernel<48, 1>, blocks);
   }
   dim3 grid(blocks, (a.oc + 7) / 8), block(256);
   if (a.kh == 3 && a.kw == 3 && a.ic == 3)

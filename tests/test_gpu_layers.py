@@ -307,6 +307,10 @@ def test_pools_exact(oracle, c):
     (3, 24, 3, 2, 1, (19, 30)),   # RGB stem: every output from its bias
     (3, 24, 3, 2, 1, (64, 70)),   # blocks of 256 pixels inside one lane and across two
     (3, 48, 3, 2, 1, (16, 22)),
+    (3, 16, 3, 2, 1, (21, 37)),   # small maps: a quarter of the outputs a wave
+    (3, 32, 3, 2, 1, (33, 60)),
+    (3, 48, 3, 2, 1, (740, 720)),  # 133,200 pixels: one pixel and all outputs a thread
+    (3, 16, 3, 1, 1, (370, 360)),
     (3, 24, 2, 2, 0, (12, 14)),
     (6, 16, 3, 1, 1, (7, 14)),    # bias first except the row's last ow % 4 pixels
     (5, 12, 3, 1, 1, (8, 13)),    # bias last; columns 8..11 multiply and add apart
