@@ -315,6 +315,7 @@ def test_pools_exact(oracle, c):
     (6, 16, 3, 1, 1, (7, 14)),    # bias first except the row's last ow % 4 pixels
     (5, 12, 3, 1, 1, (8, 13)),    # bias last; columns 8..11 multiply and add apart
     (12, 24, 2, 1, (0, 1, 0, 1), (17, 40)),  # the stem's 12 -> 24 2 x 2: one thread per pixel
+    (12, 24, 2, 1, (0, 1, 0, 1), (400, 380)),  # the same over 152,000 pixels
 ])
 def test_direct_conv_exact(oracle, ci, co, k, s, pad, hw):
     w = RNG.normal(0, 0.3, (k, k, ci, co)).astype(np.float32)
