@@ -1,6 +1,6 @@
 """ctypes front of the CPU oracle (engine.c).
 
-TEST INFRASTRUCTURE ONLY: the checker the GPU backend is compared against.
+TEST INFRASTRUCTURE ONLY: the reference the GPU backend is compared against.
 Only tests/, __graft_entry__.smoke() and bench.py's CPU baseline import it.
 """
 

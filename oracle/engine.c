@@ -2,9 +2,9 @@
  * CPU oracle: a restatement, in C, of ppocr-native's plan reader and of the
  * CPU engine's arithmetic, operation by operation, at its AVX2+FMA tier.
  *
- * TEST INFRASTRUCTURE ONLY. This file is the checker the GPU backend is
- * compared against. Only tests/, __graft_entry__.smoke() and bench.py's CPU
- * baseline may load it; the product library never links or calls it.
+ * TEST INFRASTRUCTURE ONLY. The GPU backend is compared against this file.
+ * Only tests/, __graft_entry__.smoke() and bench.py's CPU baseline may load
+ * it; the product library never links or calls it.
  *
  * Reference files (paths relative to the ppocr-native source tree):
  *   plan layout and checks     src/engine/plan.rs:9-28, 296-842

@@ -5,7 +5,7 @@
  * the reference's CPU arithmetic, pinned against the reference's golden
  * data (tests/golden/: OpenCV 5.0 and RapidOCR outputs).
  *
- * TEST INFRASTRUCTURE ONLY: the checker for the GPU kernels; the product
+ * TEST INFRASTRUCTURE ONLY: the GPU kernels are compared against it; the product
  * library never links or calls it.
  *
  * Reference files (paths relative to the ppocr-native source tree):
