@@ -266,6 +266,23 @@ def test_halo_conv_head_sources(oracle, co, hw, lanes):
     near(got, want)
 
 
+@pytest.mark.parametrize("c", [480, 1024])
+def test_large_se_gate_exact(oracle, c):
+    # Squeeze-and-excite layers too large to stage in LDS (c -> c/4 -> c):
+    # each row's weights read from memory, every output in the CPU's order.
+    w1 = RNG.normal(0, 1 / np.sqrt(c), (1, 1, c, c // 4)).astype(np.float32)
+    b1 = RNG.normal(0, 0.3, c // 4).astype(np.float32)
+    w2 = RNG.normal(0, 2 / np.sqrt(c), (1, 1, c // 4, c)).astype(np.float32)
+    b2 = RNG.normal(0, 0.3, c).astype(np.float32)
+
+    def build(b, t):
+        h = b.conv(b.mean(t), w1, b1, fused="relu")
+        return b.channelmul(t, b.conv(h, w2, b2, fused="hardsigmoid"))
+
+    got, want = both(build, (5, 7, c), oracle)
+    exact(got, want)
+
+
 @pytest.mark.parametrize("mode", ["add", "resgate", "upsampleadd_resgate", "concat", "upsample"])
 def test_elementwise_exact(oracle, mode):
     c = 12
