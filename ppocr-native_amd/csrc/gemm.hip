@@ -721,44 +721,10 @@ static const size_t kMaxLdsBytes = 160 * 1024;
 // tap's channels out in chunks of this many floats.
 constexpr int kRingBK = 32;
 
-typedef __attribute__((address_space(3))) void lds_void;
-
 template <int BK>
 __device__ __forceinline__ int ring_swz(int row) {
   if constexpr (BK == 32) return (row & 7) ^ ((row >> 3) & 1);
   else return row & 15;
-}
-
-// Wait until at most n of this wave's vector memory operations are pending.
-template <int n>
-__device__ __forceinline__ void ring_wait() {
-  static_assert(n >= 0 && n < 64, "vmcnt holds 6 bits");
-  __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-
-// ring_wait<k * L>() for a runtime k in [0, KMAX].
-template <int L, int KMAX>
-__device__ __forceinline__ void ring_wait_chunks(int k) {
-  if constexpr (KMAX > 0) {
-    if (k >= KMAX) {
-      ring_wait<KMAX * L>();
-      return;
-    }
-    ring_wait_chunks<L, KMAX - 1>(k);
-  } else {
-    ring_wait<0>();
-  }
-}
-
-// A workgroup barrier without the memory fence __syncthreads() adds (whose
-// vmcnt(0) would wait out every chunk in flight): the direct loads a stage
-// needs are waited for explicitly, and a wave's LDS reads of a stage have
-// returned before its MFMAs, hence before it reaches the next barrier. The
-// empty asm keeps the compiler from moving memory accesses across it.
-__device__ __forceinline__ void ring_barrier() {
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
 }
 
 // Whether the ring's epilogue can store whole rows four floats at a time:

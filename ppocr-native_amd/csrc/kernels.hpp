@@ -32,6 +32,42 @@ inline hipError_t allow_lds(const void *kernel, int bytes) {
   return e;
 }
 
+// ------------------------------------------------- direct-to-LDS load helpers
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// Wait until at most n of this wave's vector memory operations are pending.
+template <int n>
+__device__ __forceinline__ void ring_wait() {
+  static_assert(n >= 0 && n < 64, "vmcnt holds 6 bits");
+  __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// ring_wait<k * L>() for a runtime k in [0, KMAX].
+template <int L, int KMAX>
+__device__ __forceinline__ void ring_wait_chunks(int k) {
+  if constexpr (KMAX > 0) {
+    if (k >= KMAX) {
+      ring_wait<KMAX * L>();
+      return;
+    }
+    ring_wait_chunks<L, KMAX - 1>(k);
+  } else {
+    ring_wait<0>();
+  }
+}
+
+// A workgroup barrier without the memory fence __syncthreads() adds (whose
+// vmcnt(0) would wait out every chunk in flight): the direct loads a stage
+// needs are waited for explicitly, and a wave's LDS reads of a stage have
+// returned before its MFMAs, hence before it reaches the next barrier. The
+// empty asm keeps the compiler from moving memory accesses across it.
+__device__ __forceinline__ void ring_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 // ---------------------------------------------------------------- GEMM conv
 
 // One input of an implicit-GEMM convolution: `c` channels starting at channel
@@ -173,7 +209,7 @@ struct DwArgs {
   long y_lane_stride;
   // When set: also the f64 sums of y per channel, one row of c per block,
   // dw_mean_blocks(a) blocks per lane ([lane][block][c]), for the channel
-  // mean that reads y (joined by launch_mean_finish).
+  // mean that reads y (joined by launch_mean_group with x null).
   double *mean_part;
 };
 hipError_t launch_dwconv(const DwArgs &a, hipStream_t s);
@@ -220,46 +256,56 @@ hipError_t launch_pool(const PoolArgs &a, hipStream_t s);
 
 // ---------------------------------------------------------------- reductions
 
-// Channel mean of every lane, two passes through `partial` (f64, at least
-// mean_partial_doubles(pixels, c, lanes) values). With `se` set, the squeeze
-// and excite that follows is computed too: y = act2(W2 act1(W1 mean + b1) + b2)
-// (two 1x1 convolutions of one pixel), written to `y` (c2 values per lane).
+// Channel mean of every lane, with the squeeze-and-excite that may follow it:
+// y = act2(W2 act1(W1 mean + b1) + b2), two 1x1 convolutions of one pixel.
+// `w1`, `w2` hold each layer's weights in groups of four inputs, an
+// output's four weights together (se_pack), 16-byte aligned.
 struct SeArgs {
   const float *w1, *b1; int mid, act1;
   const float *w2, *b2; int cout, act2;
-  // The same weights transposed, each output's inputs contiguous: w1t[j][i]
-  // (mid rows of se_row_stride(c) floats), w2t[j][i] (cout rows of
-  // se_row_stride(mid)), zero past the inputs.
-  const float *w1t, *w2t;
 };
-// Row stride of the transposed SE weights for n inputs: n rounded up to 4,
-// plus 4 when that is a multiple of 8 floats, so that sixteen rows read as
-// float4 at one column fall in distinct LDS banks.
-__host__ __device__ inline int se_row_stride(int n) {
-  const int p = (n + 3) & ~3;
-  return (p / 4) % 2 ? p : p + 4;
-}
-size_t mean_partial_doubles(int pixels, int c, int lanes);
-hipError_t launch_mean(const float *x, long x_lane_stride, int pixels, int c, int lanes,
-                       double *partial, const SeArgs *se, float *y, long y_lane_stride,
-                       hipStream_t s);
-// The second pass alone, over `chunks` partial rows of c per lane.
-hipError_t launch_mean_finish(const double *partial, int pixels, int c, int chunks, int lanes,
-                              const SeArgs *se, float *y, long y_lane_stride, hipStream_t s);
-// One channel mean (with its squeeze-and-excite when has_se) of a grouped
-// launch: the partial sums come from x by the first pass or, with x null,
-// are already in partial (chunks rows per lane, written by a depthwise
-// convolution).
+// One channel mean (with its squeeze-and-excite when has_se). One launch:
+// workgroups sum pixel chunks of channel slices in f64 (or, with x null,
+// join the `chunks` partial rows per lane a depthwise convolution wrote to
+// `work`); the last workgroup of a slice to finish joins the slice's partial
+// rows in a fixed order, and with an SE the last slice of a lane to finish
+// runs both 1x1 layers. `work` (mean_shape(...).floats floats, 16-byte
+// aligned) holds the partial rows (with x null: the depthwise convolution's
+// lanes * chunks * c doubles at its start) and the gathered means; `count`
+// (count_n ints) must be zero before the first launch, and every launch
+// leaves it zero again. Launches that share `work` or `count` must not
+// overlap.
 struct MeanJob {
   const float *x;
   long x_lane_stride;
   int pixels, c, lanes, chunks;
-  double *partial;
+  float *work;
+  int *count;
   SeArgs se;
   int has_se;
   float *y;
   long y_lane_stride;
 };
+// How a job is cut: slices of `cs` channels (S of them), `k` pixel chunks per
+// lane (1 when the partial rows come from a depthwise convolution); the
+// workspace's means start `means_off` floats in, and it holds `floats`; the
+// job needs `count_n` counters.
+struct MeanShape {
+  int cs, S, k;
+  size_t means_off, floats, count_n;
+};
+__host__ __device__ MeanShape mean_shape(bool has_x, int pixels, int c, int lanes, int dw_rows, bool has_se);
+// Whether the SE layers' shapes are ones the kernel takes.
+bool se_supported(int c, int mid, int cout);
+// The packed form of a 1x1 layer's plan weights w[i * n + j] (m inputs, n
+// outputs): out[((i / 4) * n + j) * 4 + i % 4], inputs past m zero;
+// se_pack_floats(m, n) floats.
+inline size_t se_pack_floats(int m, int n) { return size_t((m + 3) / 4) * 4 * size_t(n); }
+inline void se_pack(const float *w, int m, int n, float *out) {
+  for (int i = 0; i < (m + 3) / 4 * 4; i++)
+    for (int j = 0; j < n; j++)
+      out[(size_t(i / 4) * n + j) * 4 + i % 4] = i < m ? w[size_t(i) * n + j] : 0.0f;
+}
 hipError_t launch_mean_group(const MeanJob *j, int n, hipStream_t s);
 
 hipError_t launch_layernorm(const float *x, long x_lane_stride, const float *w, int rows, int c,

@@ -492,272 +492,426 @@ hipError_t launch_pool(const PoolArgs &a, hipStream_t s) {
 
 // ------------------------------------------------------------ mean and SE
 
-// Pass 1: a block sums a run of `chunk` pixels of one lane for every channel
-// in f64; threads split into `rows` pixel strides of `c` channels, joined in
-// a fixed order in LDS.
-__global__ __launch_bounds__(256) void mean_partial(Group<MeanJob> grp) {
-  __shared__ double sums[256];
+// One launch per channel mean (up to kGroupMax of them in one grid):
+//
+//  1. Sum: with an input x, workgroup (lane, chunk k, slice s) sums a run of
+//     pixels of the slice's 32 channels in f64, each thread a fixed stride of
+//     pixels, joined in LDS in thread order. With one chunk per lane that is
+//     the whole sum; else it is stored as the chunk's partial row and the
+//     workgroup counts itself in on the slice's counter.
+//  2. Join: the last workgroup of a slice to count in (or, when a depthwise
+//     convolution wrote the partial rows, every workgroup: one per slice)
+//     adds the lane's partial rows of its channels, row by row in a fixed
+//     split over the threads, joined in thread order, and divides by the
+//     pixels. Which workgroup is last does not change the order, so the
+//     result is the same on every run.
+//  3. SE: the last slice of a lane to count in runs both 1x1 layers of the
+//     squeeze-and-excite on the lane's means, each output from zero, inputs
+//     in order, fused multiply-adds for outputs below outputs / 8 * 8 and a
+//     separate product and sum past them, then the bias, then the activation
+//     (the engine's one-pixel 1x1 rule, src/engine/kernels/pointwise.rs:
+//     135-185), with the weights streamed through an LDS ring by direct
+//     loads (several chunks in flight: one workgroup moves them all).
+//
+// Counters go back to zero as soon as the last workgroup has read them, so
+// the next launch (or graph replay) finds them cleared. What workgroups hand
+// each other within the launch (partial rows, means) is stored and loaded as
+// device-scope atomics, which stay coherent across the XCDs' L2s; a
+// workgroup waits for its stores to complete before it counts in. (An
+// agent-scope fence instead writes the whole L2 back, and those writebacks
+// queue up: measured about 75 ns a workgroup.)
+//
+// The mean divides an f64 sum by the pixel count and rounds once to f32, as
+// the engine does (src/engine/layers.rs:391-406); the f64 sum runs in
+// another order.
+
+constexpr int kMeanSlice = 32;    // channels a summing workgroup covers
+constexpr int kMeanStrides = 8;   // loads in flight per thread while summing
+constexpr int kMeanMaxChunks = 64;
+constexpr int kSeBuf = 8192;      // floats of one LDS buffer of the SE ring
+constexpr int kSeLoads = kSeBuf / 1024;  // direct loads per thread per buffer
+constexpr int kSeRingMax = 4;
+// LDS floats for a layer's m inputs: read sixteen at a time from rows a
+// multiple of four, so up to fifteen past the last (loaded, never used).
+__host__ __device__ inline int se_in_floats(int m) { return ((m + 15) & ~15) + 16; }
+
+// One 1x1 layer over one pixel: out_j = act(sum_i in_i * w[i][j] + bias_j)
+// for j < n, inputs `in` (m floats, 16-byte aligned, readable 16 past m) in
+// LDS. The weights are packed in groups of four inputs, each output's four
+// weights together: w[((i / 4) * n + j) * 4 + i % 4], zero past m, so one
+// 16-byte LDS read gives a thread four inputs' weights. They travel in
+// chunks of whole groups (a multiple of 16 inputs, or of 4 for layers over
+// 512 wide, at most kSeBuf floats) through `nb` LDS buffers by direct loads,
+// nb - 1 chunks in flight; se_prefetch issues the first ones (the caller may
+// do so early), se_layer the rest. Each thread keeps NO outputs' sums
+// (j = t + 256 o) and reads sixteen inputs' weights while it sums the
+// previous sixteen. Reads past the chunk's last group are clamped to it and
+// their products dropped. FUSED: every output is below n / 8 * 8 (the
+// engine's fused columns); else each output picks fused or separate product
+// and sum. Outputs go to `out` (LDS or global memory).
+//
+// The waits count this wave's vector memory operations, which complete in
+// the order they were issued: any issued after a chunk's loads only make a
+// wait for that chunk more conservative.
+__host__ __device__ inline int se_rows(int n) {
+  const int r = kSeBuf / n;
+  return r >= 16 ? r & ~15 : r & ~3;
+}
+
+__device__ __forceinline__ void se_issue(const float *w, int m, int n, int q, float *ring, int nb) {
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const long total4 = (long)((m + 3) / 4) * n;  // float4 groups of the packed weights
+  const long g0 = (long)q * se_rows(n) * n / 4;
+  float *dst = ring + (q % nb) * kSeBuf;
+#pragma unroll
+  for (int l = 0; l < kSeLoads; l++) {
+    long g = g0 + (l * 4 + wave) * 64 + lane;
+    if (g >= total4) g = g0;  // past the weights: any valid group (never read)
+    __builtin_amdgcn_global_load_lds((const void *)(w + 4 * g), (lds_void *)(dst + (l * 4 + wave) * 256), 16, 0, 0);
+  }
+}
+
+// The chunks a layer's ring takes before its first multiply-add.
+__device__ __forceinline__ void se_prefetch(const float *w, int m, int n, float *ring, int nb) {
+  const int chunks = (m + se_rows(n) - 1) / se_rows(n);
+  for (int q = 0; q < nb - 1 && q < chunks; q++) se_issue(w, m, n, q, ring, nb);
+}
+
+template <int NO, bool FUSED>
+__device__ __forceinline__ void se_layer_n(const float *w, const float *bias, int m, int n, int code,
+                                           const float *in, float *out, float *ring, int nb,
+                                           const float *w_next, int n_next) {
+  const int t = threadIdx.x;
+  const int rows = se_rows(n);
+  const int chunks = (m + rows - 1) / rows;
+  const int fused_end = n / 8 * 8;
+  bool has[NO], fz[NO];
+  int col[NO];
+#pragma unroll
+  for (int o = 0; o < NO; o++) {
+    const int j = t + 256 * o;
+    has[o] = j < n, fz[o] = j < fused_end, col[o] = (j < n ? j : n - 1) * 4;
+  }
+  float acc[NO];
+#pragma unroll
+  for (int o = 0; o < NO; o++) acc[o] = 0.0f;
+  for (int q = 0; q < chunks; q++) {
+    if (q + nb - 1 < chunks) se_issue(w, m, n, q + nb - 1, ring, nb);
+    ring_wait_chunks<kSeLoads, kSeRingMax - 1>(min(nb - 1, chunks - 1 - q));
+    ring_barrier();
+    const float *buf = ring + (q % nb) * kSeBuf;
+    const float *xin = in + q * rows;
+    const int cnt = min(rows, m - q * rows), last = (cnt + 3) / 4 - 1;  // last group of the chunk
+    auto fetch = [&](int u0, f32x4 (&xv)[4], f32x4 (&wv)[4][NO]) {
+#pragma unroll
+      for (int v = 0; v < 4; v++) {
+        xv[v] = *reinterpret_cast<const f32x4 *>(xin + u0 + 4 * v);
+        const int g = min(u0 / 4 + v, last);
+#pragma unroll
+        for (int o = 0; o < NO; o++) wv[v][o] = *reinterpret_cast<const f32x4 *>(buf + g * 4 * n + col[o]);
+      }
+    };
+    // The multiply-adds of sixteen inputs in order (all, or the first `live`).
+    auto sum = [&](const f32x4 (&xv)[4], const f32x4 (&wv)[4][NO], int live) {
+#pragma unroll
+      for (int v = 0; v < 4; v++)
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+          if (live >= 16 || 4 * v + e < live)
+#pragma unroll
+            for (int o = 0; o < NO; o++) {
+              const float x = xv[v][e], wgt = wv[v][o][e];
+              acc[o] = FUSED || fz[o] ? fmaf(wgt, x, acc[o]) : acc[o] + x * wgt;
+            }
+    };
+    const int full = cnt / 16;  // whole batches of sixteen inputs
+    f32x4 xa[4], wa[4][NO], xb[4], wb[4][NO];
+    fetch(0, xa, wa);
+    int k = 0;
+    for (; k + 2 <= full; k += 2) {
+      fetch(16 * (k + 1), xb, wb);
+      sum(xa, wa, 16);
+      fetch(16 * min(k + 2, full), xa, wa);
+      sum(xb, wb, 16);
+    }
+    if (k < full) {
+      sum(xa, wa, 16);
+      k++;
+      fetch(16 * k, xa, wa);
+    }
+    if (16 * k < cnt) sum(xa, wa, cnt - 16 * k);
+    ring_barrier();
+  }
+  // Every buffer is free: the next layer's first chunks go out before this
+  // layer's outputs are written.
+  if (w_next) se_prefetch(w_next, n, n_next, ring, nb);
+#pragma unroll
+  for (int o = 0; o < NO; o++) {
+    if (has[o]) {
+      float v = acc[o];
+      if (bias) v = v + bias[t + 256 * o];
+      out[t + 256 * o] = act(v, code);
+    }
+  }
+}
+
+template <int NO>
+__device__ __forceinline__ void se_layer_f(const float *w, const float *bias, int m, int n, int code,
+                                           const float *in, float *out, float *ring, int nb,
+                                           const float *w_next, int n_next) {
+  if (n % 8 == 0) se_layer_n<NO, true>(w, bias, m, n, code, in, out, ring, nb, w_next, n_next);
+  else se_layer_n<NO, false>(w, bias, m, n, code, in, out, ring, nb, w_next, n_next);
+}
+
+// The layer whose first chunks se_prefetch has issued; w_next (n_next
+// outputs, over this layer's n) is the next layer's, prefetched at the end.
+__device__ __forceinline__ void se_layer(const float *w, const float *bias, int m, int n, int code,
+                                         const float *in, float *out, float *ring, int nb,
+                                         const float *w_next = nullptr, int n_next = 0) {
+  if (n <= 256) se_layer_f<1>(w, bias, m, n, code, in, out, ring, nb, w_next, n_next);
+  else if (n <= 512) se_layer_f<2>(w, bias, m, n, code, in, out, ring, nb, w_next, n_next);
+  else se_layer_f<4>(w, bias, m, n, code, in, out, ring, nb, w_next, n_next);
+}
+
+// Whether this workgroup is the last of `of` to count in on `*cnt` (then the
+// counter is zero again). What the workgroups exchange within a launch is
+// stored and loaded as device-scope atomics (coherent across the XCDs'
+// L2s without writing the L2s back), so waiting for this workgroup's stores
+// to complete before the count is enough for the last one to see them all.
+__device__ __forceinline__ bool count_in(int *cnt, int of, int *flag) {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const int last = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == of - 1;
+    if (last) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *flag = last;
+  }
+  __syncthreads();
+  return *flag != 0;
+}
+
+template <typename T>
+__device__ __forceinline__ void put_shared(T *p, T v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <typename T>
+__device__ __forceinline__ T get_shared(const T *p) {
+  return __hip_atomic_load(const_cast<T *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int V>
+__global__ __launch_bounds__(256) void mean_se(Group<MeanJob> grp) {
+  extern __shared__ __attribute__((aligned(16))) float dyn[];
+  __shared__ double red[256 * V];
+  __shared__ int flag;
   const int prob = group_problem(grp);
   const MeanJob &j = grp.a[prob];
-  const int pixels = j.pixels, c = j.c, chunk = grp.x[prob], chunks = j.chunks;
-  double *partial = j.partial;
+  const int cs = grp.x[prob] & 0xffff, nb = grp.x[prob] >> 16, S = grp.y[prob];
+  const int c = j.c, P = j.chunks, t = threadIdx.x;
+  const int K = j.x ? P : 1;
   const int blk = (int)blockIdx.x - grp.first[prob];
-  int ln = blk / chunks, run = blk - ln * chunks;
-  const float *xl = j.x + (long)ln * j.x_lane_stride;
-  int p0 = run * chunk, p1 = min(p0 + chunk, pixels);
-  double *out = partial + ((long)ln * chunks + run) * c;
-  for (int c0 = 0; c0 < c; c0 += 256) {
-    int cw = min(256, c - c0);
-    int rows = 256 / cw;
-    int t = threadIdx.x;
-    int ch = t % cw, r = t / cw;
-    double s = 0.0;
-    if (r < rows) {
-      // Eight loads in flight, then their sums in pixel order.
-      int p = p0 + r;
-      for (; p + 7 * rows < p1; p += 8 * rows) {
-        float v[8];
+  const int per_lane = S * K;
+  const int ln = blk / per_lane, r = blk - ln * per_lane;
+  const int k = r / S, s = r - k * S;
+  const int c0 = s * cs, cw = min(cs, c - c0);
+  const MeanShape sh = mean_shape(j.x != nullptr, j.pixels, c, j.lanes, j.x ? 0 : P, j.has_se != 0);
+  // With an SE, any workgroup may be the one that runs its layers: each
+  // starts the first layer's weights on their way into its LDS ring now,
+  // while it sums (those that are not last drop them).
+  float *ring = dyn + se_in_floats(c) + se_in_floats(j.se.mid);
+  if (j.has_se) se_prefetch(j.se.w1, c, j.se.mid, ring, nb);
+  double *pl = reinterpret_cast<double *>(j.work) + (long)ln * P * c;
+  int *cnt = j.count;  // [lanes] for the SE, then [lanes][S] for the slices
+  double tot = 0.0;  // threads below cw: the channel's sum
+  bool join = true;
+  if (j.x) {
+    const int chunk = (j.pixels + K - 1) / K;
+    const int p0 = k * chunk, p1 = min(p0 + chunk, j.pixels);
+    const float *xl = j.x + (long)ln * j.x_lane_stride;
+    if constexpr (V == 4) {
+      constexpr int NQ = kMeanSlice / 4, R = 256 / NQ;
+      const int q = t % NQ, rr = t / NQ, ch = c0 + 4 * q;
+      double a0 = 0.0, a1 = 0.0, a2 = 0.0, a3 = 0.0;
+      if (4 * q < cw) {
+        // kMeanStrides loads in flight; past the chunk they read zeros.
+        for (int p = p0 + rr; p < p1; p += kMeanStrides * R) {
+          f32x4 v[kMeanStrides];
 #pragma unroll
-        for (int k = 0; k < 8; k++) v[k] = xl[(long)(p + k * rows) * c + c0 + ch];
+          for (int u = 0; u < kMeanStrides; u++)
+            v[u] = p + u * R < p1 ? *reinterpret_cast<const f32x4 *>(xl + (long)(p + u * R) * c + ch)
+                                  : f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int k = 0; k < 8; k++) s += (double)v[k];
+          for (int u = 0; u < kMeanStrides; u++) a0 += (double)v[u].x, a1 += (double)v[u].y, a2 += (double)v[u].z, a3 += (double)v[u].w;
+        }
       }
-      for (; p < p1; p += rows) s += (double)xl[(long)p * c + c0 + ch];
-    }
-    sums[t] = s;
-    __syncthreads();
-    if (t < cw) {
-      double tot = 0.0;
-      for (int k = 0; k < rows; k++) tot += sums[k * cw + t];
-      out[c0 + t] = tot;
-    }
-    __syncthreads();
-  }
-}
-
-// One output of a 1x1 layer over one pixel, from its contiguous weight row
-// (inputs rounded up to 4, in LDS or global memory) and the inputs (LDS):
-// from zero, inputs in order, fused multiply-adds or separate products and
-// sums; eight float4 of weights and inputs read ahead of their sums.
-template <bool FUSED>
-__device__ __forceinline__ float se_row(const float *w, const float *in, int n) {
-  float acc = 0.0f;
-  const int n4 = (n + 3) / 4;
-  for (int i4 = 0; i4 < n4; i4 += 8) {
-    f32x4 wv[8], xv[8];
+      red[4 * t] = a0, red[4 * t + 1] = a1, red[4 * t + 2] = a2, red[4 * t + 3] = a3;
+      __syncthreads();
+      if (t < cw)
+        for (int x = 0; x < R; x++) tot += red[(x * NQ + t / 4) * 4 + (t & 3)];
+    } else {
+      constexpr int R = 256 / kMeanSlice;
+      const int cl = t % kMeanSlice, rr = t / kMeanSlice;
+      double a = 0.0;
+      if (cl < cw) {
+        for (int p = p0 + rr; p < p1; p += kMeanStrides * R) {
+          float v[kMeanStrides];
 #pragma unroll
-    for (int k = 0; k < 8; k++)
-      if (i4 + k < n4)
-        wv[k] = *reinterpret_cast<const f32x4 *>(w + 4 * (i4 + k)),
-        xv[k] = *reinterpret_cast<const f32x4 *>(in + 4 * (i4 + k));
+          for (int u = 0; u < kMeanStrides; u++) v[u] = p + u * R < p1 ? xl[(long)(p + u * R) * c + c0 + cl] : 0.0f;
 #pragma unroll
-    for (int k = 0; k < 8; k++) {
-#pragma unroll
-      for (int q = 0; q < 4; q++) {
-        const int i = 4 * (i4 + k) + q;
-        if (i < n) acc = FUSED ? fmaf(wv[k][q], xv[k][q], acc) : acc + xv[k][q] * wv[k][q];
+          for (int u = 0; u < kMeanStrides; u++) a += (double)v[u];
+        }
       }
+      red[t] = a;
+      __syncthreads();
+      if (t < cw)
+        for (int x = 0; x < R; x++) tot += red[x * kMeanSlice + t];
+    }
+    if (K == 1) {
+      join = false;
+    } else {
+      if (t < cw) put_shared(pl + (long)k * c + c0 + t, tot);
+      if (!count_in(cnt + j.lanes + ln * S + s, K, &flag)) return;
     }
   }
-  return acc;
-}
-
-// Pass 2: one block per lane joins the partials and divides; with an SE,
-// then the two 1x1 layers of one pixel, each output from zero with a fused
-// multiply-add per input in order (separate product and sum for the columns
-// past cols / 8 * 8, the engine's pointwise rule for one pixel), then its
-// bias, then its activation.
-//
-// The block is latency-bound, so every load it can issue early goes first:
-// each thread requests its share of the transposed weights (kSePer float4)
-// before the partial sums and moves them to LDS once the mean is known.
-// grp.x says how the weights travel: 1 both layers at once, 2 the first,
-// then the second while the first is summed, 0 neither (each output reads
-// its row from global memory, when a layer is larger than LDS). Each
-// channel's partials are split between J threads (a fixed split, sixteen
-// independent loads in flight per thread), joined in LDS in thread order.
-constexpr int kSePer = 9;
-constexpr int kSeThreads = 1024;
-constexpr int kSeStaged = kSePer * 4 * kSeThreads;  // floats one staging moves at most
-
-__global__ __launch_bounds__(1024) void mean_finish(Group<MeanJob> grp) {
-  extern __shared__ __attribute__((aligned(16))) float smem[];
-  __shared__ double red[kSeThreads];
-  const int prob = group_problem(grp);
-  const MeanJob &jb = grp.a[prob];
-  const double *partial = jb.partial;
-  const int pixels = jb.pixels, c = jb.c, chunks = jb.chunks, has_se = jb.has_se, stage = grp.x[prob];
-  const SeArgs &se = jb.se;
-  const int cp = se_row_stride(c), mp = se_row_stride(se.mid);
-  float *mean = smem;         // cp
-  float *hid = mean + cp;     // mp
-  float *W = hid + mp;        // staged weights
-  const int ln = (int)blockIdx.x - grp.first[prob], t = threadIdx.x;
-  const int n1 = has_se ? se.mid * cp : 0, n2 = has_se ? se.cout * mp : 0;
-  const int first = stage == 1 ? n1 + n2 : (stage == 2 ? n1 : 0);
-  f32x4 r[kSePer];
-#pragma unroll
-  for (int k = 0; k < kSePer; k++) {
-    const int e = 4 * (t + k * kSeThreads);
-    r[k] = e < first ? *reinterpret_cast<const f32x4 *>(e < n1 ? se.w1t + e : se.w2t + (e - n1))
-                     : f32x4{0.f, 0.f, 0.f, 0.f};
-  }
-  const double *pl = partial + (long)ln * chunks * c;
-  for (int c0 = 0; c0 < c; c0 += kSeThreads) {
-    const int cw = min(kSeThreads, c - c0);
-    const int J = kSeThreads / cw;
-    const int ch = t % cw, j = t / cw;
-    double s = 0.0;
-    if (j < J) {
-      const double *p = pl + c0 + ch;
-      for (int rr = j; rr < chunks; rr += 16 * J) {
+  if (join) {
+    // Rows another workgroup of this launch wrote are read as device-scope
+    // atomics; a depthwise convolution's rows come from the launch before.
+    const int J = 256 / cs, cl = t % cs, jj = t / cs;
+    double a = 0.0;
+    if (cl < cw) {
+      const double *p = pl + c0 + cl;
+      for (int rr = jj; rr < P; rr += 16 * J) {
         double v[16];
+        if (j.x) {
 #pragma unroll
-        for (int k = 0; k < 16; k++) v[k] = rr + k * J < chunks ? p[(long)(rr + k * J) * c] : 0.0;
+          for (int u = 0; u < 16; u++) v[u] = rr + u * J < P ? get_shared(p + (long)(rr + u * J) * c) : 0.0;
+        } else {
 #pragma unroll
-        for (int k = 0; k < 16; k++) s += v[k];
+          for (int u = 0; u < 16; u++) v[u] = rr + u * J < P ? p[(long)(rr + u * J) * c] : 0.0;
+        }
+#pragma unroll
+        for (int u = 0; u < 16; u++) a += v[u];
       }
     }
-    red[t] = s;
+    __syncthreads();  // the sum phase's join may still read red
+    red[t] = a;
     __syncthreads();
-    if (t < cw) {
-      double tot = 0.0;
-      for (int k = 0; k < J; k++) tot += red[k * cw + t];
-      mean[c0 + t] = (float)(tot / (double)pixels);
-    }
-    __syncthreads();
+    tot = 0.0;
+    if (t < cw)
+      for (int x = 0; x < J; x++) tot += red[x * cs + t];
   }
-  float *yl = jb.y + (long)ln * jb.y_lane_stride;
-  if (!has_se) {
-    for (int ch = t; ch < c; ch += kSeThreads) yl[ch] = mean[ch];
+  const float mean = (float)(tot / (double)j.pixels);
+  float *yl = j.y + (long)ln * j.y_lane_stride;
+  if (!j.has_se) {
+    if (t < cw) yl[c0 + t] = mean;
     return;
   }
-  if (t < cp - c) mean[c + t] = 0.0f;
-#pragma unroll
-  for (int k = 0; k < kSePer; k++) {
-    const int e = 4 * (t + k * kSeThreads);
-    if (e < first) *reinterpret_cast<f32x4 *>(W + e) = r[k];
-  }
-  if (stage == 2) {
-#pragma unroll
-    for (int k = 0; k < kSePer; k++) {
-      const int e = 4 * (t + k * kSeThreads);
-      r[k] = e < n2 ? *reinterpret_cast<const f32x4 *>(se.w2t + e) : f32x4{0.f, 0.f, 0.f, 0.f};
-    }
+  // The layers read their inputs sixteen at a time: room for 16 past each.
+  float *in = dyn;                                   // c floats
+  float *hid = dyn + se_in_floats(c);                // mid floats, then the ring
+  if (S > 1) {
+    float *means = j.work + sh.means_off + (long)ln * c;
+    if (t < cw) put_shared(means + c0 + t, mean);
+    if (!count_in(cnt + ln, S, &flag)) return;
+    for (int i = t; i < c; i += 256) in[i] = get_shared(means + i);
+  } else if (t < cw) {
+    in[t] = mean;
   }
   __syncthreads();
-  const float *w1 = stage ? W : se.w1t;
-  for (int j = t; j < se.mid; j += kSeThreads) {
-    float acc = j < se.mid / 8 * 8 ? se_row<true>(w1 + (long)j * cp, mean, c) : se_row<false>(w1 + (long)j * cp, mean, c);
-    if (se.b1) acc = acc + se.b1[j];
-    hid[j] = act(acc, se.act1);
-  }
-  if (t < mp - se.mid) hid[se.mid + t] = 0.0f;
+  const SeArgs &se = j.se;
+  se_layer(se.w1, se.b1, c, se.mid, se.act1, in, hid, ring, nb, se.w2, se.cout);
   __syncthreads();
-  if (stage == 2) {
-#pragma unroll
-    for (int k = 0; k < kSePer; k++) {
-      const int e = 4 * (t + k * kSeThreads);
-      if (e < n2) *reinterpret_cast<f32x4 *>(W + e) = r[k];
-    }
-    __syncthreads();
+  se_layer(se.w2, se.b2, se.mid, se.cout, se.act2, hid, yl, ring, nb);
+}
+
+__host__ __device__ MeanShape mean_shape(bool has_x, int pixels, int c, int lanes, int dw_rows, bool has_se) {
+  MeanShape m{};
+  if (has_x) {
+    m.cs = kMeanSlice;
+    int k = (pixels + 255) / 256;
+    m.k = k < 1 ? 1 : (k > kMeanMaxChunks ? kMeanMaxChunks : k);
+  } else {
+    // Join slices when the partial rows come from a depthwise convolution:
+    // the widest whose rows leave each thread at most sixteen loads.
+    int cs = 4;
+    for (int w = 32; w >= 8; w /= 2)
+      if ((dw_rows + 256 / w - 1) / (256 / w) <= 16) {
+        cs = w;
+        break;
+      }
+    m.cs = cs;
+    m.k = 1;
   }
-  const float *w2 = stage == 1 ? W + n1 : (stage == 2 ? W : se.w2t);
-  for (int j = t; j < se.cout; j += kSeThreads) {
-    float acc = j < se.cout / 8 * 8 ? se_row<true>(w2 + (long)j * mp, hid, se.mid)
-                                    : se_row<false>(w2 + (long)j * mp, hid, se.mid);
-    if (se.b2) acc = acc + se.b2[j];
-    yl[j] = act(acc, se.act2);
-  }
+  m.S = (c + m.cs - 1) / m.cs;
+  const size_t rows = has_x ? (m.k > 1 ? size_t(m.k) : 0) : size_t(dw_rows);
+  m.means_off = 2 * size_t(lanes) * rows * size_t(c);
+  m.floats = m.means_off + (has_se && m.S > 1 ? size_t(lanes) * c : 0);
+  // Counters: [lanes] for the SE, then [lanes][S] for the slices.
+  m.count_n = has_x && m.k > 1 ? size_t(lanes) * (1 + m.S) : (has_se ? size_t(lanes) : 0);
+  return m;
 }
 
-static int mean_chunk(int pixels) {
-  int chunk = (pixels + 255) / 256;
-  return chunk < 16 ? 16 : chunk;
+// The SE ring buffers one layer of `n` outputs over `m` inputs needs.
+static int se_chunks(int m, int n) {
+  const int rows = se_rows(n);
+  return rows > 0 ? (m + rows - 1) / rows : 0;
 }
 
-size_t mean_partial_doubles(int pixels, int c, int lanes) {
-  int chunk = mean_chunk(pixels);
-  int chunks = (pixels + chunk - 1) / chunk;
-  return (size_t)lanes * chunks * c;
+bool se_supported(int c, int mid, int cout) {
+  return c >= 1 && mid >= 1 && cout >= 1 && c <= 1024 && mid <= 1024 && cout <= 1024 && se_chunks(c, mid) > 0 &&
+         se_chunks(mid, cout) > 0;
 }
 
-// Jobs whose partial sums are not there yet get the first pass (one launch
-// for all of them), then every job the second (one launch).
 hipError_t launch_mean_group(const MeanJob *jobs, int n, hipStream_t s) {
   if (n < 1 || n > kGroupMax) return hipErrorInvalidValue;
-  Group<MeanJob> first{}, second{};
-  long b1 = 0, b2 = 0;
+  Group<MeanJob> g{};
+  long blocks = 0;
   size_t shm = 0;
+  bool vec = true;
   for (int p = 0; p < n; p++) {
-    MeanJob j = jobs[p];
-    if (j.lanes < 1 || j.c < 1) return hipErrorInvalidValue;
+    const MeanJob &j = jobs[p];
+    if (j.lanes < 1 || j.c < 1 || j.pixels < 1 || !j.work || !j.y) return hipErrorInvalidValue;
+    if (!j.x && j.chunks < 1) return hipErrorInvalidValue;
+    if ((reinterpret_cast<uintptr_t>(j.work) & 15) != 0) return hipErrorInvalidValue;
+    const MeanShape m = mean_shape(j.x != nullptr, j.pixels, j.c, j.lanes, j.x ? 0 : j.chunks, j.has_se != 0);
+    if (m.count_n && !j.count) return hipErrorInvalidValue;
+    MeanJob jj = j;
     if (j.x) {
-      const int chunk = mean_chunk(j.pixels);
-      j.chunks = (j.pixels + chunk - 1) / chunk;
-      first.first[first.n] = (int)b1;
-      first.x[first.n] = chunk;
-      first.a[first.n++] = j;
-      b1 += (long)j.chunks * j.lanes;
+      jj.chunks = m.k;
+      vec = vec && j.c % 4 == 0 && (reinterpret_cast<uintptr_t>(j.x) & 15) == 0 && j.x_lane_stride % 4 == 0;
     }
-    second.first[p] = (int)b2;
-    second.a[p] = j;
-    b2 += j.lanes;
-    // LDS: the mean and the hidden layer (rounded up to 4), then the staged
-    // weights: both layers, the larger one (one after the other), or none.
-    const size_t cp = size_t(se_row_stride(j.c)), mp = size_t(se_row_stride(j.se.mid));
-    const size_t base = cp + (j.has_se ? mp : 0);
-    const size_t dyn = (kMaxLds - kSeThreads * sizeof(double)) / sizeof(float);
-    if (base > dyn) return hipErrorInvalidValue;
-    int stage = 0;
-    size_t staged = 0;
+    int nb = 0;
     if (j.has_se) {
-      if (!j.se.w1t || !j.se.w2t) return hipErrorInvalidValue;
-      const size_t n1 = size_t(j.se.mid) * cp, n2 = size_t(j.se.cout) * mp;
-      const size_t room = std::min(dyn - base, size_t(kSeStaged));
-      if (n1 + n2 <= room)
-        stage = 1, staged = n1 + n2;
-      else if (std::max(n1, n2) <= room)
-        stage = 2, staged = std::max(n1, n2);
+      const SeArgs &se = j.se;
+      if (!se.w1 || !se.w2 || !se_supported(j.c, se.mid, se.cout)) return hipErrorInvalidValue;
+      if (((reinterpret_cast<uintptr_t>(se.w1) | reinterpret_cast<uintptr_t>(se.w2)) & 15) != 0)
+        return hipErrorInvalidValue;
+      nb = std::min(kSeRingMax, std::max(se_chunks(j.c, se.mid), se_chunks(se.mid, se.cout)));
+      nb = std::max(nb, 1);
+      const size_t in = size_t(se_in_floats(j.c)) + size_t(se_in_floats(se.mid));
+      shm = std::max(shm, (in + size_t(nb) * kSeBuf) * sizeof(float));
     }
-    second.x[p] = stage;
-    shm = std::max(shm, (base + staged) * sizeof(float));
+    g.first[p] = (int)blocks;
+    g.x[p] = m.cs | (nb << 16);
+    g.y[p] = m.S;
+    g.a[p] = jj;
+    blocks += long(j.lanes) * m.S * m.k;
+    if (blocks > 0x7fffffffL) return hipErrorInvalidValue;
   }
-  second.n = n;
-  first.first[first.n] = (int)b1;
-  second.first[n] = (int)b2;
-  if (first.n) {
-    hipLaunchKernelGGL(mean_partial, dim3((unsigned)b1), dim3(256), 0, s, first);
-    hipError_t e = hipGetLastError();
+  g.n = n;
+  g.first[n] = (int)blocks;
+  const void *fn = vec ? reinterpret_cast<const void *>(mean_se<4>) : reinterpret_cast<const void *>(mean_se<1>);
+  if (shm > 64 * 1024) {
+    hipError_t e = allow_lds(fn, (int)(kMaxLds - 256 * 4 * sizeof(double) - 64));
     if (e != hipSuccess) return e;
   }
-  if (shm > 64 * 1024 - kSeThreads * sizeof(double)) {
-    hipError_t e = allow_lds(reinterpret_cast<const void *>(mean_finish), (int)(kMaxLds - kSeThreads * sizeof(double)));
-    if (e != hipSuccess) return e;
-  }
-  hipLaunchKernelGGL(mean_finish, dim3((unsigned)b2), dim3(1024), shm, s, second);
+  if (vec)
+    hipLaunchKernelGGL(mean_se<4>, dim3((unsigned)blocks), dim3(256), shm, s, g);
+  else
+    hipLaunchKernelGGL(mean_se<1>, dim3((unsigned)blocks), dim3(256), shm, s, g);
   return hipGetLastError();
-}
-
-hipError_t launch_mean(const float *x, long x_lane_stride, int pixels, int c, int lanes,
-                       double *partial, const SeArgs *se, float *y, long y_lane_stride,
-                       hipStream_t s) {
-  MeanJob j{};
-  j.x = x, j.x_lane_stride = x_lane_stride, j.pixels = pixels, j.c = c, j.lanes = lanes;
-  j.partial = partial;
-  if (se) j.se = *se, j.has_se = 1;
-  j.y = y, j.y_lane_stride = y_lane_stride;
-  return launch_mean_group(&j, 1, s);
-}
-
-hipError_t launch_mean_finish(const double *partial, int pixels, int c, int chunks, int lanes,
-                              const SeArgs *se, float *y, long y_lane_stride, hipStream_t s) {
-  MeanJob j{};
-  j.pixels = pixels, j.c = c, j.lanes = lanes, j.chunks = chunks;
-  j.partial = const_cast<double *>(partial);  // read only: x is null
-  if (se) j.se = *se, j.has_se = 1;
-  j.y = y, j.y_lane_stride = y_lane_stride;
-  return launch_mean_group(&j, 1, s);
 }
 
 // ------------------------------------------------------------ layer norm

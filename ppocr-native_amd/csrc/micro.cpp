@@ -30,30 +30,49 @@ EltArgs flat(int mode, const float *a, const float *b, float *y, size_t n, int a
   return e;
 }
 
-// The channel mean's f64 partial sums: one buffer per device, grown on
-// demand and kept; calls that overlap on one device would share it.
+// The channel mean's workspace (f64 partial rows) and counters: one of each
+// per device, grown on demand and kept. The counters are zeroed when they
+// are allocated and every launch leaves them zero; calls that overlap on one
+// device would share both.
+struct MeanWork {
+  float *work = nullptr;
+  size_t floats = 0;
+  int *count = nullptr;
+  size_t counters = 0;
+};
 std::mutex g_mu;
-std::vector<std::pair<double *, size_t>> g_partial;
+std::vector<MeanWork> g_mean;
 
-double *partial_for(size_t doubles, hipError_t *err) {
+hipError_t mean_work_for(size_t floats, size_t counters, float **work, int **count) {
   int dev = 0;
-  *err = hipGetDevice(&dev);
-  if (*err != hipSuccess) return nullptr;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
   std::lock_guard<std::mutex> lock(g_mu);
-  if (g_partial.size() <= size_t(dev)) g_partial.resize(dev + 1, {nullptr, 0});
-  auto &slot = g_partial[dev];
-  if (slot.second < doubles) {
-    if (slot.first) {
-      hipDeviceSynchronize();
-      hipFree(slot.first);
-    }
-    slot = {nullptr, 0};
-    void *p = nullptr;
-    *err = hipMalloc(&p, doubles * sizeof(double));
-    if (*err != hipSuccess) return nullptr;
-    slot = {static_cast<double *>(p), doubles};
+  if (g_mean.size() <= size_t(dev)) g_mean.resize(dev + 1);
+  MeanWork &m = g_mean[dev];
+  if (m.floats < floats || m.counters < counters) {
+    e = hipDeviceSynchronize();
+    if (e != hipSuccess) return e;
   }
-  return slot.first;
+  if (m.floats < floats) {
+    if (m.work) hipFree(m.work);
+    m.work = nullptr, m.floats = 0;
+    e = hipMalloc(&m.work, std::max<size_t>(floats, 4) * sizeof(float));
+    if (e != hipSuccess) return e;
+    m.floats = floats;
+  }
+  if (m.counters < counters) {
+    if (m.count) hipFree(m.count);
+    m.count = nullptr, m.counters = 0;
+    e = hipMalloc(&m.count, counters * sizeof(int));
+    if (e != hipSuccess) return e;
+    e = hipMemset(m.count, 0, counters * sizeof(int));
+    if (e != hipSuccess) return e;
+    m.counters = counters;
+  }
+  *work = m.work;
+  *count = m.count;
+  return hipSuccess;
 }
 
 }  // namespace
@@ -127,10 +146,13 @@ int ppocr_hip_activation(const float *x, float *y, size_t n, int act, void *stre
 
 int ppocr_hip_channel_mean(const float *x, float *y, size_t pixels, size_t c, void *stream) {
   if (pixels == 0 || c == 0 || pixels > 0x7fffffff || c > 0x7fffffff) return int(hipErrorInvalidValue);
-  hipError_t e;
-  double *part = partial_for(mean_partial_doubles(int(pixels), int(c), 1), &e);
-  if (!part) return code(e);
-  return code(launch_mean(x, 0, int(pixels), int(c), 1, part, nullptr, y, 0, hipStream_t(stream)));
+  const MeanShape m = mean_shape(true, int(pixels), int(c), 1, 0, false);
+  MeanJob j{};
+  j.x = x, j.pixels = int(pixels), j.c = int(c), j.lanes = 1;
+  j.y = y;
+  hipError_t e = mean_work_for(m.floats, m.count_n, &j.work, &j.count);
+  if (e != hipSuccess) return code(e);
+  return code(launch_mean_group(&j, 1, hipStream_t(stream)));
 }
 
 int ppocr_hip_channel_mul(const float *x, const float *g, float *y, size_t pixels, size_t c,

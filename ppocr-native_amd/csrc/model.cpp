@@ -88,7 +88,7 @@ struct Step {
   GemmTile tile{};
   int gemm_n = 0, chunks = 0, ctot = 0, cpt = 0;
   size_t wt_off = 0, wt_k = 0;
-  size_t se_w1t = 0, se_w2t = 0;  // S_MEAN with an SE: the transposed 1x1 weights in the packed arena
+  size_t se_w1 = 0, se_w2 = 0;  // S_MEAN with an SE: the 1x1 weights, 16-byte aligned in the packed arena
 };
 
 enum GroupKind { GK_NONE = 0, GK_RING, GK_PATCH, GK_MEAN, GK_ELT };
@@ -287,6 +287,18 @@ static DwArgs dw_shape(const Op &op) {
   return a;
 }
 
+// How a channel-mean step's launch is cut, for L lanes of the batch's plan.
+static MeanShape mean_step_shape(const Step &s, const Plan &p, size_t L) {
+  const Op &op = p.ops[size_t(s.op)];
+  int rows = 0;
+  if (s.mean_of_dw >= 0) {
+    DwArgs d = dw_shape(p.ops[size_t(s.mean_of_dw)]);
+    d.lanes = int(L);
+    rows = dw_mean_blocks(d);
+  }
+  return mean_shape(s.mean_of_dw < 0, int(op.ih * op.iw), int(op.ic), int(L), rows, s.fc1 >= 0);
+}
+
 bool Model::build_steps(std::string &err) {
   const auto &ops = plan.ops;
   const size_t n = ops.size();
@@ -358,7 +370,8 @@ bool Model::build_steps(std::string &err) {
         if (i + 2 < n && readers[op.y] == 1) {
           const Op &f1 = ops[i + 1], &f2 = ops[i + 2];
           if (f1.kind == K_CONV && f1.is_pointwise() && f1.x == op.y && f2.kind == K_CONV &&
-              f2.is_pointwise() && f2.x == f1.y && readers[f1.y] == 1) {
+              f2.is_pointwise() && f2.x == f1.y && readers[f1.y] == 1 && f1.n2 == 0 && f2.n2 == 0 &&
+              se_supported(int(f1.ic), int(f1.oc), int(f2.oc))) {
             s.fc1 = int(i + 1), s.fc2 = int(i + 2);
             folded[i + 1] = folded[i + 2] = true;
           }
@@ -519,19 +532,15 @@ bool Model::pack(std::string &err) {
   const auto &ops = plan.ops;
   for (Step &s : steps) {
     if (s.kind == S_MEAN && s.fc1 >= 0) {
-      // The squeeze-and-excite's two 1x1 layers, each output's weights in a
-      // contiguous row of se_row_stride floats (zeros past the inputs).
+      // The squeeze-and-excite's two 1x1 layers in the kernel's groups of
+      // four inputs, each starting on a 256-byte boundary.
       const Op &f1 = ops[size_t(s.fc1)], &f2 = ops[size_t(s.fc2)];
-      const size_t c = f1.ic, mid = f1.oc, cout = f2.oc;
-      const size_t cp = size_t(se_row_stride(int(c))), mp = size_t(se_row_stride(int(mid)));
-      s.se_w1t = round_up(packed.size(), 64);
-      packed.resize(s.se_w1t + mid * cp, 0.0f);
-      for (size_t j = 0; j < mid; j++)
-        for (size_t i = 0; i < c; i++) packed[s.se_w1t + j * cp + i] = weights[f1.w0 + i * mid + j];
-      s.se_w2t = round_up(packed.size(), 64);
-      packed.resize(s.se_w2t + cout * mp, 0.0f);
-      for (size_t j = 0; j < cout; j++)
-        for (size_t i = 0; i < mid; i++) packed[s.se_w2t + j * mp + i] = weights[f2.w0 + i * cout + j];
+      s.se_w1 = round_up(packed.size(), 64);
+      packed.resize(s.se_w1 + se_pack_floats(int(f1.ic), int(f1.oc)), 0.0f);
+      se_pack(weights.data() + f1.w0, int(f1.ic), int(f1.oc), packed.data() + s.se_w1);
+      s.se_w2 = round_up(packed.size(), 64);
+      packed.resize(s.se_w2 + se_pack_floats(int(f2.ic), int(f2.oc)), 0.0f);
+      se_pack(weights.data() + f2.w0, int(f2.ic), int(f2.oc), packed.data() + s.se_w2);
       continue;
     }
     if (s.kind != S_GEMM && s.kind != S_CTC) continue;
@@ -761,10 +770,11 @@ bool Model::arrange(Batch &b, std::string &err) {
     const Step &s = steps[i];
     const Op &op = p.ops[s.op];
     size_t need = 0;
-    if (s.kind == S_MEAN && s.mean_of_dw >= 0)
-      need = 2 * L * size_t(dw_mean_blocks(dw_shape(p.ops[s.mean_of_dw]))) * op.ic;
-    else if (s.kind == S_MEAN)
-      need = 2 * mean_partial_doubles(int(op.ih * op.iw), int(op.ic), int(L));
+    if (s.kind == S_MEAN) {
+      // Partial rows and gathered means, then the counters.
+      const MeanShape m = mean_step_shape(s, p, L);
+      need = round_up(m.floats, 4) + m.count_n;
+    }
     if (s.kind == S_CTC) {
       size_t ntn = (s.gemm_n + s.tile.bn - 1) / s.tile.bn;
       need = L * op.iw * ntn * 4;
@@ -808,6 +818,14 @@ bool Model::arrange(Batch &b, std::string &err) {
     }
   }
   build_launches(b);
+  // The channel means' counters start at zero (each launch leaves them so).
+  for (const Launch &l : b.launches)
+    if (l.gk == GK_MEAN) {
+      const MeanJob &j = l.mean;
+      const MeanShape m = mean_shape(j.x != nullptr, j.pixels, j.c, j.lanes, j.x ? 0 : j.chunks, j.has_se != 0);
+      if (m.count_n)
+        HIPTRY(hipMemsetAsync(j.count, 0, m.count_n * sizeof(int), stream), "clearing the channel mean counters");
+    }
   account(b);
   group(b);
   return true;
@@ -985,38 +1003,30 @@ void Model::build_launches(Batch &b) {
         break;
       }
       case S_MEAN: {
-        const float *x = b.dev(op.x);
-        long xs = b.stride(op.x);
-        int pixels = int(op.ih * op.iw), c = int(op.ic);
-        double *part = reinterpret_cast<double *>(b.ws(si));
-        bool se = s.fc1 >= 0;
-        SeArgs sa{};
-        if (se) {
-          const Op &f1 = p.ops[s.fc1], &f2 = p.ops[s.fc2];
-          sa = SeArgs{W + f1.w0, f1.b1 ? W + f1.b0 : nullptr, int(f1.oc), f1.fused,
-                      W + f2.w0, f2.b1 ? W + f2.b0 : nullptr, int(f2.oc), f2.fused,
-                      dpacked + s.se_w1t, dpacked + s.se_w2t};
-        }
+        const bool se = s.fc1 >= 0;
+        MeanJob j{};
+        j.x = s.mean_of_dw >= 0 ? nullptr : b.dev(op.x);
+        j.x_lane_stride = b.stride(op.x);
+        j.pixels = int(op.ih * op.iw), j.c = int(op.ic), j.lanes = L;
         if (s.mean_of_dw >= 0) {
           DwArgs d = dw_shape(p.ops[s.mean_of_dw]);
           d.lanes = L;
-          const int chunks = dw_mean_blocks(d);
-          b.launches.push_back({se ? "se_squeeze" : "channel_mean", s.op, [=](hipStream_t st) {
-                                  return launch_mean_finish(part, pixels, c, chunks, L, se ? &sa : nullptr, Y, ys,
-                                                            st);
-                                }});
-          Launch &l = b.launches.back();
-          l.gk = GK_MEAN;
-          l.mean = MeanJob{nullptr, 0, pixels, c, int(L), chunks, part, sa, se ? 1 : 0, Y, ys};
-          break;
+          j.chunks = dw_mean_blocks(d);
         }
+        j.work = b.ws(si);
+        j.count = reinterpret_cast<int *>(b.ws(si) + round_up(mean_step_shape(s, p, L).floats, 4));
+        if (se) {
+          const Op &f1 = p.ops[s.fc1], &f2 = p.ops[s.fc2];
+          j.se = SeArgs{dpacked + s.se_w1, f1.b1 ? W + f1.b0 : nullptr, int(f1.oc), f1.fused,
+                        dpacked + s.se_w2, f2.b1 ? W + f2.b0 : nullptr, int(f2.oc), f2.fused};
+          j.has_se = 1;
+        }
+        j.y = Y, j.y_lane_stride = ys;
         b.launches.push_back({se ? "se_squeeze" : "channel_mean", s.op,
-                              [=](hipStream_t st) {
-                                return launch_mean(x, xs, pixels, c, L, part, se ? &sa : nullptr, Y, ys, st);
-                              }});
+                              [j](hipStream_t st) { return launch_mean_group(&j, 1, st); }});
         Launch &l = b.launches.back();
         l.gk = GK_MEAN;
-        l.mean = MeanJob{x, xs, pixels, c, int(L), 0, part, sa, se ? 1 : 0, Y, ys};
+        l.mean = j;
         break;
       }
       case S_LN: {

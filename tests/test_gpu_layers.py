@@ -283,6 +283,35 @@ def test_large_se_gate_exact(oracle, c):
     exact(got, want)
 
 
+@pytest.mark.parametrize("hw,c,lanes,dw", [((60, 61), 96, 3, False), ((33, 17), 30, 2, False),
+                                          ((160, 160), 96, 1, True), ((8, 9), 1024, 2, True),
+                                          ((30, 30), 384, 1, True), ((3, 80), 480, 16, True),
+                                          ((240, 240), 24, 1, False)])
+def test_mean_se_launch_shapes(oracle, hw, c, lanes, dw):
+    # The one-launch channel mean and squeeze-and-excite on the shapes that
+    # take each of its paths: an input summed in several pixel chunks and
+    # channel slices (the last chunk of a slice joins, the last slice of a
+    # lane runs the SE layers), channels not a multiple of four (scalar
+    # loads), a depthwise convolution's partial rows joined in slices of 4 to
+    # 32 channels, and SE layers streamed through the LDS ring in one to
+    # four buffers. The gate is the CPU's to the bit.
+    mid = max(1, c // 4)
+    w1 = RNG.normal(0, 1 / np.sqrt(c), (1, 1, c, mid)).astype(np.float32)
+    b1 = RNG.normal(0, 0.3, mid).astype(np.float32)
+    w2 = RNG.normal(0, 2 / np.sqrt(mid), (1, 1, mid, c)).astype(np.float32)
+    b2 = RNG.normal(0, 0.3, c).astype(np.float32)
+    wd = RNG.normal(0, 0.3, (3, 3, c)).astype(np.float32)
+
+    def build(b, t):
+        x = b.dwconv(t, wd, b2, k=(3, 3), fused="hardswish") if dw else t
+        m = b.mean(x)
+        g = b.conv(b.conv(m, w1, b1, fused="relu"), w2, b2, fused="hardsigmoid")
+        return [g, b.mean(x)]
+
+    got, want = both(build, (*hw, c), oracle, lanes=lanes)
+    exact(got, want)
+
+
 @pytest.mark.parametrize("mode", ["add", "resgate", "upsampleadd_resgate", "concat", "upsample"])
 def test_elementwise_exact(oracle, mode):
     c = 12
