@@ -164,6 +164,18 @@ int ppocr_hip_activation(const float *x, float *y, size_t n, int act, void *stre
  * x[p][c], summed in f64. */
 int ppocr_hip_channel_mean(const float *x, float *y, size_t pixels, size_t c, void *stream);
 
+/* `ppocr_hip_channel_mean` without any allocation: no counterpart in the
+ * reference; for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc). Its
+ * partial sums and counters live in a device array of the library that each
+ * GPU holds until the process ends (2 MiB and 4 KiB), so `c` is limited to
+ * 4096 channels; larger shapes return nonzero with the reason in `err`.
+ * Calls that overlap on one GPU share that array and race; calls in order
+ * (one stream, or synchronised) do not. Same kernel and same results, bit
+ * for bit, as ppocr_hip_channel_mean. */
+int ppocr_hip_channel_mean_noalloc(const float *x, float *y, size_t pixels, size_t c, void *stream, char *err,
+                                   size_t err_len);
+
 /* `Kind::Channelmul` (src/engine/kernels/elementwise.rs:178-200):
  * y[p][c] = x[p][c] * g[c]. */
 int ppocr_hip_channel_mul(const float *x, const float *g, float *y, size_t pixels, size_t c,

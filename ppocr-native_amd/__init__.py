@@ -76,6 +76,7 @@ def lib() -> C.CDLL:
         "ppocr_hip_mul": ([vp, vp, vp, sz, vp], C.c_int),
         "ppocr_hip_activation": ([vp, vp, sz, C.c_int, vp], C.c_int),
         "ppocr_hip_channel_mean": ([vp, vp, sz, sz, vp], C.c_int),
+        "ppocr_hip_channel_mean_noalloc": ([vp, vp, sz, sz, vp, C.c_char_p, sz], C.c_int),
         "ppocr_hip_channel_mul": ([vp, vp, vp, sz, sz, vp], C.c_int),
         "ppocr_hip_layer_norm": ([vp, vp, vp, sz, sz, vp], C.c_int),
         "ppocr_hip_row_argmax": ([vp, vp, sz, sz, vp], C.c_int),
@@ -269,6 +270,15 @@ def hip_activation(x: int, y: int, n: int, act: int, stream: int = 0) -> None:
 
 def hip_channel_mean(x: int, y: int, pixels: int, c: int, stream: int = 0) -> None:
     _check(lib().ppocr_hip_channel_mean(x, y, pixels, c, stream or None), "ppocr_hip_channel_mean")
+
+
+def hip_channel_mean_noalloc(x: int, y: int, pixels: int, c: int, stream: int = 0) -> None:
+    """ppocr_hip_channel_mean with its scratch in the library's device array
+    (no allocation; at most 4096 channels)."""
+    err = C.create_string_buffer(256)
+    rc = lib().ppocr_hip_channel_mean_noalloc(x, y, pixels, c, stream or None, err, 256)
+    if rc:
+        raise RuntimeError(f"ppocr_hip_channel_mean_noalloc: {err.value.decode()} ({rc})")
 
 
 def hip_channel_mul(x: int, g: int, y: int, pixels: int, c: int, stream: int = 0) -> None:

@@ -7,6 +7,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdio>
 #include <mutex>
 #include <vector>
 
@@ -72,6 +73,48 @@ hipError_t mean_work_for(size_t floats, size_t counters, float **work, int **cou
   }
   *work = m.work;
   *count = m.count;
+  return hipSuccess;
+}
+
+// The channel mean without allocation (ppocr_hip_channel_mean_noalloc): its
+// partial rows and counters live in `scratch`, a file-scope device array
+// each GPU holds until the process ends. On the host, `scratch` names a
+// host-side stand-in, never the device memory: each device's address comes
+// from hipGetSymbolAddress, once per device, with that device current, and
+// only that address is passed on.
+constexpr int kNoAllocMaxChannels = 4096;
+constexpr size_t kNoAllocPartials = size_t(64) * kNoAllocMaxChannels;  // doubles: 64 chunks x channels
+constexpr size_t kNoAllocCounters = 1024;                              // ints after the partial rows
+static __device__ __align__(256) double scratch[kNoAllocPartials + kNoAllocCounters / 2];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+double *g_scratch[kMaxDevices];
+
+__global__ void zero_ints(int *p, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0;
+}
+
+// This device's `scratch`, its counters zeroed (on `s`) the first time.
+hipError_t scratch_on_device(double **out, hipStream_t s) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch[dev]) {
+    void *p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    int *counters = reinterpret_cast<int *>(static_cast<double *>(p) + kNoAllocPartials);
+    hipLaunchKernelGGL(zero_ints, dim3((kNoAllocCounters + 255) / 256), dim3(256), 0, s, counters,
+                       int(kNoAllocCounters));
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    g_scratch[dev] = static_cast<double *>(p);
+  }
+  *out = g_scratch[dev];
   return hipSuccess;
 }
 
@@ -153,6 +196,36 @@ int ppocr_hip_channel_mean(const float *x, float *y, size_t pixels, size_t c, vo
   hipError_t e = mean_work_for(m.floats, m.count_n, &j.work, &j.count);
   if (e != hipSuccess) return code(e);
   return code(launch_mean_group(&j, 1, hipStream_t(stream)));
+}
+
+int ppocr_hip_channel_mean_noalloc(const float *x, float *y, size_t pixels, size_t c, void *stream, char *err,
+                                   size_t err_len) {
+  auto fail = [&](int code_, const char *msg) {
+    if (err && err_len) snprintf(err, err_len, "%s", msg);
+    return code_;
+  };
+  if (pixels == 0 || c == 0 || pixels > 0x7fffffff)
+    return fail(int(hipErrorInvalidValue), "channel mean: pixels and channels must be positive");
+  if (c > size_t(kNoAllocMaxChannels)) {
+    char m[160];
+    snprintf(m, sizeof m, "channel mean without allocation: %zu channels, over the %d its scratch holds", c,
+             kNoAllocMaxChannels);
+    return fail(int(hipErrorInvalidValue), m);
+  }
+  const MeanShape m = mean_shape(true, int(pixels), int(c), 1, 0, false);
+  if (m.floats > 2 * kNoAllocPartials || m.count_n > kNoAllocCounters)
+    return fail(int(hipErrorInvalidValue), "channel mean without allocation: shape exceeds its scratch");
+  double *sc = nullptr;
+  hipError_t e = scratch_on_device(&sc, hipStream_t(stream));
+  if (e != hipSuccess) return fail(int(e), hipGetErrorString(e));
+  MeanJob j{};
+  j.x = x, j.pixels = int(pixels), j.c = int(c), j.lanes = 1;
+  j.y = y;
+  j.work = reinterpret_cast<float *>(sc);
+  j.count = reinterpret_cast<int *>(sc + kNoAllocPartials);
+  e = launch_mean_group(&j, 1, hipStream_t(stream));
+  if (e != hipSuccess) return fail(int(e), hipGetErrorString(e));
+  return 0;
 }
 
 int ppocr_hip_channel_mul(const float *x, const float *g, float *y, size_t pixels, size_t c,
