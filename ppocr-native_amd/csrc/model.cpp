@@ -132,7 +132,6 @@ struct Batch {
   std::vector<size_t> home_floats, home_off;
   size_t ws_off = 0;          // workspace in the arena, floats
   std::vector<size_t> step_ws;  // each step's own workspace, floats past ws_off
-  std::vector<hipEvent_t> done; // per launch: recorded when another stream waits for it
   float *arena = nullptr;
   size_t arena_floats = 0;
   float *host_in = nullptr;   // pinned, lanes * in_len
@@ -154,21 +153,10 @@ struct Model {
   std::string name;
   int integrated = 0;
   hipStream_t stream = nullptr;
-  // Extra streams (default priority) for launches that do not depend on
-  // each other: the fork/join points are events, so a run is still one
-  // stream's work to the caller (and one graph when captured).
-  static constexpr int kSide = 3;
-  // Whether independent launches run on the side streams (and homes are
-  // reused only where that adds no ordering). Off: a run with them ended in
-  // a host crash on the 960 x 960 detector whose cause is not found yet;
-  // every launch then goes on `stream` in plan order.
-  static constexpr bool kConcurrent = false;
-  // Whether independent launches of one kind run as grouped launches (on
-  // `stream`, in a topological order of the groups); homes are then reused
-  // only where that adds no ordering, as for kConcurrent.
+  // Whether independent launches of one kind run as grouped launches (in a
+  // topological order of the groups); homes are then reused only where that
+  // adds no ordering the data lacks.
   static constexpr bool kGrouped = true;
-  hipStream_t side[kSide] = {};
-  hipEvent_t fork = nullptr, join[kSide] = {};
   Plan plan;
   std::vector<float> weights;     // host copy of the plan's weights
   float *dweights = nullptr;      // the plan's weights on the device
@@ -208,8 +196,6 @@ Model::~Model() {
   if (stream) hipStreamSynchronize(stream);
   drop_graph();
   for (auto &b : batches) {
-    for (hipEvent_t e : b->done)
-      if (e) hipEventDestroy(e);
     if (b->arena) hipFree(b->arena);
     if (b->host_in) hipHostFree(b->host_in);
     for (float *p : b->host_out)
@@ -217,11 +203,6 @@ Model::~Model() {
   }
   if (dweights) hipFree(dweights);
   if (dpacked) hipFree(dpacked);
-  for (int k = 0; k < kSide; k++) {
-    if (side[k]) hipStreamSynchronize(side[k]), hipStreamDestroy(side[k]);
-    if (join[k]) hipEventDestroy(join[k]);
-  }
-  if (fork) hipEventDestroy(fork);
   if (stream) hipStreamDestroy(stream);
 }
 
@@ -669,11 +650,6 @@ bool Model::load(const uint8_t *bytes, size_t len, std::string &err) {
   if (name.empty()) name = prop.gcnArchName;
   integrated = prop.integrated;
   HIPTRY(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking), "creating a stream");
-  for (int k = 0; k < kSide; k++) {
-    HIPTRY(hipStreamCreateWithFlags(&side[k], hipStreamNonBlocking), "creating a stream");
-    HIPTRY(hipEventCreateWithFlags(&join[k], hipEventDisableTiming), "creating an event");
-  }
-  HIPTRY(hipEventCreateWithFlags(&fork, hipEventDisableTiming), "creating an event");
   HIPTRY(hipMalloc(&dweights, std::max<size_t>(weights.size(), 1) * sizeof(float)),
          "allocating the weights");
   if (!weights.empty())
@@ -722,7 +698,7 @@ bool Model::arrange(Batch &b, std::string &err) {
   auto place = [&](size_t need, size_t i) {
     need = round_up(std::max<size_t>(need, 1), 64);
     auto allowed = [&](size_t h) {
-      if (!kConcurrent && !kGrouped) return true;
+      if (!kGrouped) return true;
       for (size_t r : held_by[h])
         if (i == SIZE_MAX || !anc[i][r]) return false;
       return true;
@@ -1097,15 +1073,12 @@ void Model::build_launches(Batch &b) {
 // reads and writes: its inputs' and output's homes (a home holds different
 // buffers over a run, so a later writer waits for the earlier readers) and
 // its own workspace region. A launch also follows the previous launch of its
-// step. Independent launches may then run on different streams.
+// step. Independent launches of one kind may then share one grid (group).
 void Model::link(Batch &b) const {
   const size_t H = b.home_floats.size();
   const size_t R = H + steps.size();
   std::vector<int> writer(R, -1);
   std::vector<std::vector<int>> readers(R);
-  for (hipEvent_t e : b.done)
-    if (e) hipEventDestroy(e);
-  b.done.assign(b.launches.size(), nullptr);
   for (size_t j = 0; j < b.launches.size(); j++) {
     Launch &l = b.launches[j];
     const Step &s = steps[size_t(l.step)];
@@ -1130,11 +1103,6 @@ void Model::link(Batch &b) const {
     for (size_t r : rd) readers[r].push_back(int(j));
     for (size_t w : wr) writer[w] = int(j), readers[w].clear();
   }
-  // An event for each launch some other launch waits for.
-  if (!kConcurrent) return;
-  for (const Launch &l : b.launches)
-    for (int d : l.deps)
-      if (!b.done[size_t(d)]) hipEventCreateWithFlags(&b.done[size_t(d)], hipEventDisableTiming);
 }
 
 // Independent launches of one kind as grouped launches. Kind by kind (the
@@ -1298,9 +1266,6 @@ void Model::group(Batch &b) const {
     deps.erase(std::unique(deps.begin(), deps.end()), deps.end());
     l.deps = deps;
   }
-  for (hipEvent_t e : b.done)
-    if (e) hipEventDestroy(e);
-  b.done.assign(out.size(), nullptr);
   b.launches = std::move(out);
 }
 
@@ -1482,64 +1447,13 @@ bool Model::enqueue(std::string &err) {
   return true;
 }
 
-// Every launch of the active batches: each on the stream of the dependency
-// it continues when it can, else on the stream idle longest; it waits for
-// its dependencies on other streams by their events. The side streams start
-// after the model stream's earlier work (the input copy) and the model
-// stream waits for all of them at the end, so a run is ordered like one
-// stream's work.
+// Every launch of the active batches, in order, on the model's stream.
 bool Model::launch_all(std::string &err) {
-  if (!kConcurrent) {
-    for (size_t g = 0; g < active_batches; g++)
-      for (const Launch &l : batches[g]->launches) {
-        hipError_t e = l.fn(stream);
-        if (e != hipSuccess)
-          return err = fmt("launching %s (operation %d): %s", l.name.c_str(), l.op, hipGetErrorString(e)), false;
-      }
-    return true;
-  }
-  hipStream_t S[1 + kSide] = {stream};
-  for (int k = 0; k < kSide; k++) S[1 + k] = side[k];
-  bool started[1 + kSide] = {true};
-  HIPTRY(hipEventRecord(fork, stream), "recording the run's start");
-  long last[1 + kSide];  // global index of the last launch on each stream
-  for (int k = 0; k <= kSide; k++) last[k] = -1 - k;
-  long global = 0;
-  for (size_t g = 0; g < active_batches; g++) {
-    Batch &b = *batches[g];
-    const long base = global;
-    std::vector<int> where(b.launches.size(), 0);
-    for (size_t j = 0; j < b.launches.size(); j++, global++) {
-      const Launch &l = b.launches[j];
-      int st = -1;
-      if (!l.deps.empty()) {
-        const int d = l.deps.back();
-        if (last[where[size_t(d)]] == base + d) st = where[size_t(d)];
-      }
-      if (st < 0) {
-        st = 0;
-        for (int k = 1; k <= kSide; k++)
-          if (last[k] < last[st]) st = k;
-      }
-      if (!started[st]) {
-        HIPTRY(hipStreamWaitEvent(S[st], fork, 0), "ordering a stream after the run's start");
-        started[st] = true;
-      }
-      for (int d : l.deps)
-        if (where[size_t(d)] != st)
-          HIPTRY(hipStreamWaitEvent(S[st], b.done[size_t(d)], 0), "waiting for a dependency");
-      hipError_t e = l.fn(S[st]);
+  for (size_t g = 0; g < active_batches; g++)
+    for (const Launch &l : batches[g]->launches) {
+      hipError_t e = l.fn(stream);
       if (e != hipSuccess)
         return err = fmt("launching %s (operation %d): %s", l.name.c_str(), l.op, hipGetErrorString(e)), false;
-      if (b.done[j]) HIPTRY(hipEventRecord(b.done[j], S[st]), "recording a launch");
-      where[j] = st;
-      last[st] = global;
-    }
-  }
-  for (int k = 0; k < kSide; k++)
-    if (started[1 + k]) {
-      HIPTRY(hipEventRecord(join[k], S[1 + k]), "recording a stream's end");
-      HIPTRY(hipStreamWaitEvent(stream, join[k], 0), "joining the streams");
     }
   return true;
 }
