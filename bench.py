@@ -49,10 +49,16 @@ def log(*a):
 
 
 def roofline(name: str, flops: float, nbytes: float, ms: float) -> dict:
+    """A launch's achieved rate against MI355X's peak for its class. A GEMM
+    is also scored against its attainable roof, min(FP32-MFMA peak,
+    arithmetic intensity x HBM peak): a thin 1x1 layer cannot reach the MFMA
+    peak whatever the kernel does."""
     if name in GEMM_LAUNCHES and flops > 0:
         ach = flops / (ms * 1e-3) / 1e12
+        roof = min(PEAK_FP32_MFMA_TFLOPS, flops / max(nbytes, 1.0) * PEAK_HBM_GBS / 1e3)
         return {"bound": "mfma", "achieved": round(ach, 3), "peak": PEAK_FP32_MFMA_TFLOPS,
-                "unit": "TFLOP/s", "frac": round(ach / PEAK_FP32_MFMA_TFLOPS, 4)}
+                "unit": "TFLOP/s", "frac": round(ach / PEAK_FP32_MFMA_TFLOPS, 4),
+                "attainable": round(roof, 3), "frac_attainable": round(ach / roof, 4)}
     ach = nbytes / (ms * 1e-3) / 1e9
     return {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
             "frac": round(ach / PEAK_HBM_GBS, 4)}
@@ -92,6 +98,8 @@ def by_kernel(rows: list[dict]) -> dict:
         rl = roofline(k, a["flops"], a["bytes"], a["ms"])
         out[k] = {"launches": a["launches"], "ms": round(a["ms"], 4), "achieved": rl["achieved"],
                   "unit": rl["unit"], "frac": rl["frac"]}
+        if "frac_attainable" in rl:
+            out[k]["frac_attainable"] = rl["frac_attainable"]
     return out
 
 
@@ -157,52 +165,77 @@ def bench_block(P, nets, steps, warmup):
 
 
 def bench_micro(P, repeats: int = 20) -> dict:
+    """The layer microkernels at the benchmark's sizes. `warm`: one set of
+    buffers, called back to back (small ones stay in the 256 MB last-level
+    cache). `cold`: the calls rotate over enough sets of buffers (over 256 MB
+    in all) that each call reads its inputs from HBM."""
     from ppocr_native_amd.devmem import DeviceArray, Timer
     rng = np.random.default_rng(0)
     out = {}
+    MALL = 256 << 20
 
-    def timeit(fn):
-        fn()
+    def timeit(fns):
+        for fn in fns[:2]:
+            fn()
         t = Timer()
         t.start()
-        for _ in range(repeats):
-            fn()
+        for k in range(repeats):
+            fns[k % len(fns)]()
         return t.stop() / repeats
 
+    def sets(nbytes):
+        return max(1, -(-(MALL + (64 << 20)) // nbytes))
+
+    def both(name, make, nbytes, per_set_bytes, frac=True):
+        warm = timeit([make(0)])
+        cold = timeit([make(k) for k in range(sets(per_set_bytes))])
+        r = {"ms": round(warm, 4), "gb_per_s": round(nbytes / warm / 1e6, 1),
+             "cold_ms": round(cold, 4), "cold_gb_per_s": round(nbytes / cold / 1e6, 1)}
+        if frac:
+            r["frac_hbm"] = round(nbytes / warm / 1e6 / PEAK_HBM_GBS, 3)
+            r["cold_frac_hbm"] = round(nbytes / cold / 1e6 / PEAK_HBM_GBS, 3)
+        out[name] = r
+
     n = 240 * 240 * 256
-    a = DeviceArray.of(rng.uniform(-1, 1, n).astype(np.float32))
-    b = DeviceArray.of(rng.uniform(-1, 1, n).astype(np.float32))
-    y = DeviceArray(4 * n)
-    for name, fn, nbytes in [
+    # Two sets of inputs and outputs: 354 MB, past the last-level cache.
+    A = [DeviceArray.of(rng.uniform(-1, 1, n).astype(np.float32)) for _ in range(2)]
+    B = [DeviceArray.of(rng.uniform(-1, 1, n).astype(np.float32)) for _ in range(2)]
+    Y = [DeviceArray(4 * n) for _ in range(2)]
+    for name, call, nbytes in [
         # A plain copy (activation code 0): the reference for HBM counters.
-        ("copy 1x256x240x240", lambda: P.hip_activation(a.addr, y.addr, n, 0), 8 * n),
-        ("add 1x256x240x240", lambda: P.hip_add(a.addr, b.addr, y.addr, n), 12 * n),
-        ("mul 1x256x240x240", lambda: P.hip_mul(a.addr, b.addr, y.addr, n), 12 * n),
-        ("hardswish 1x256x240x240", lambda: P.hip_activation(a.addr, y.addr, n, 7), 8 * n),
+        ("copy 1x256x240x240", lambda k: lambda: P.hip_activation(A[k % 2].addr, Y[k % 2].addr, n, 0), 8 * n),
+        ("add 1x256x240x240", lambda k: lambda: P.hip_add(A[k % 2].addr, B[k % 2].addr, Y[k % 2].addr, n), 12 * n),
+        ("mul 1x256x240x240", lambda k: lambda: P.hip_mul(A[k % 2].addr, B[k % 2].addr, Y[k % 2].addr, n), 12 * n),
+        ("hardswish 1x256x240x240", lambda k: lambda: P.hip_activation(A[k % 2].addr, Y[k % 2].addr, n, 7), 8 * n),
     ]:
-        ms = timeit(fn)
-        out[name] = {"ms": round(ms, 4), "gb_per_s": round(nbytes / ms / 1e6, 1),
-                     "frac_hbm": round(nbytes / ms / 1e6 / PEAK_HBM_GBS, 3)}
+        both(name, call, nbytes, nbytes)
+    del A, B, Y
     px, c = 3600, 480
-    x = DeviceArray.of(rng.uniform(-1, 1, px * c).astype(np.float32))
+    ns = sets(8 * px * c)
+    X = [DeviceArray.of(rng.uniform(-1, 1, px * c).astype(np.float32)) for _ in range(ns)]
+    YY = [DeviceArray(4 * px * c) for _ in range(ns)]
     g = DeviceArray.of(rng.uniform(-1, 1, c).astype(np.float32))
-    yy = DeviceArray(4 * px * c)
-    ms = timeit(lambda: P.hip_channel_mean(x.addr, yy.addr, px, c))
-    out["mean 1x480x60x60"] = {"ms": round(ms, 4), "gb_per_s": round(4 * px * c / ms / 1e6, 1)}
-    ms = timeit(lambda: P.hip_channel_mul(x.addr, g.addr, yy.addr, px, c))
-    out["channel_mul 1x480x60x60"] = {"ms": round(ms, 4), "gb_per_s": round(8 * px * c / ms / 1e6, 1)}
+    both("mean 1x480x60x60", lambda k: lambda: P.hip_channel_mean(X[k].addr, YY[k].addr, px, c),
+         4 * px * c + 4 * c, 8 * px * c)
+    both("channel_mul 1x480x60x60", lambda k: lambda: P.hip_channel_mul(X[k].addr, g.addr, YY[k].addr, px, c),
+         8 * px * c, 8 * px * c)
+    del X, YY
     rows, cc = 1280, 120
-    xl = DeviceArray.of(rng.uniform(-1, 1, rows * cc).astype(np.float32))
+    ns = sets(8 * rows * cc)
+    XL = [DeviceArray.of(rng.uniform(-1, 1, rows * cc).astype(np.float32)) for _ in range(ns)]
+    YL = [DeviceArray(4 * rows * cc) for _ in range(ns)]
     wl = DeviceArray.of(np.concatenate([np.ones(cc), np.zeros(cc), [1e-6]]).astype(np.float32))
-    ms = timeit(lambda: P.hip_layer_norm(xl.addr, wl.addr, yy.addr, rows, cc))
-    out["layernorm 1280x120"] = {"ms": round(ms, 4), "gb_per_s": round(8 * rows * cc / ms / 1e6, 1)}
+    both("layernorm 1280x120", lambda k: lambda: P.hip_layer_norm(XL[k].addr, wl.addr, YL[k].addr, rows, cc),
+         8 * rows * cc, 8 * rows * cc)
+    del XL, YL
     cols = 18385
-    xa = DeviceArray.of(rng.normal(0, 3, rows * cols).astype(np.float32))
-    ya = DeviceArray(8 * rows)
-    ms = timeit(lambda: P.hip_row_argmax(xa.addr, ya.addr, rows, cols))
     nb = 4 * rows * cols
-    out["row_argmax 1280x18385"] = {"ms": round(ms, 4), "gb_per_s": round(nb / ms / 1e6, 1),
-                                    "frac_hbm": round(nb / ms / 1e6 / PEAK_HBM_GBS, 3)}
+    ns = sets(nb)
+    XA = [DeviceArray.of(rng.normal(0, 3, rows * cols).astype(np.float32)) for _ in range(ns)]
+    ya = DeviceArray(8 * rows)
+    both("row_argmax 1280x18385", lambda k: lambda: P.hip_row_argmax(XA[k].addr, ya.addr, rows, cols),
+         nb + 8 * rows, nb)
+    del XA
     return out
 
 
@@ -376,31 +409,71 @@ def cpu_page(nets, threads: int) -> dict:
             "sample": f"one page of {len(quads)} lines through the C oracle's stages, {threads} threads"}
 
 
+def cpu_threads() -> tuple[int, int]:
+    """(threads for the all-cores run, nproc): the cores this process may
+    run on, at most OMP_NUM_THREADS (the CPU share a one-GPU box gives)."""
+    nproc = len(os.sched_getaffinity(0))
+    cap = int(os.environ.get("OMP_NUM_THREADS", nproc) or nproc)
+    return max(1, min(nproc, cap)), nproc
+
+
+def cpu_runs(fn, budget_s: float, want: int = 20, least: int = 3) -> tuple[float, float, int]:
+    """Median wall seconds and median process CPU seconds of calls of fn:
+    `want` calls, fewer (at least `least`) when they would overrun budget_s."""
+    fn()
+    walls, cpus = [], []
+    t_start = time.perf_counter()
+    while len(walls) < want and (len(walls) < least or time.perf_counter() - t_start < budget_s):
+        t0, c0 = time.perf_counter(), time.process_time()
+        fn()
+        walls.append(time.perf_counter() - t0)
+        cpus.append(time.process_time() - c0)
+    return float(np.median(walls)), float(np.median(cpus)), len(walls)
+
+
 def cpu_baseline(nets, det_plan, rec_plan, budget_s: float) -> tuple[dict, dict]:
+    """The C oracle (the engine's CPU path at the AVX2+FMA tier's summation
+    orders, vectorised across outputs) on this host: one thread pinned to
+    one core, and all the cores this process may use, as the reference's
+    benches time its CPU path (tools/bench_ocr_abba.py:32-43,
+    examples/plan.rs:57-90): medians of repeated runs, wall and process CPU
+    time."""
     sys.path.insert(0, str(ROOT))
     import oracle
-    threads = min(os.cpu_count() or 1, 16)
+    threads, nproc = cpu_threads()
     m = oracle.OracleModel(det_plan)
     img = nets.page_image(960, 960)
-    m.run(img, threads)
-    n, t0 = 0, time.perf_counter()
-    while n < 2 or (time.perf_counter() - t0 < budget_s and n < 20):
-        m.run(img, threads)
-        n += 1
-    det = n / (time.perf_counter() - t0)
     r = oracle.OracleModel(rec_plan)
     lines = nets.line_images(16)
-    r.run(lines[0], threads)
-    k, t0 = 0, time.perf_counter()
-    while k < 16 or (time.perf_counter() - t0 < budget_s / 2 and k < 64):
-        r.run(lines[k % 16], threads)
-        k += 1
-    rec = k / (time.perf_counter() - t0)
-    return ({"value": round(det, 3), "unit": "img/s", "cores": threads, "kind": "port",
-             "sample": f"{n} detector forwards at 1x3x960x960 on the C oracle (tier-3 FMA order), "
-                       f"{threads} OpenMP threads"},
-            {"value": round(rec, 2), "unit": "lines/s", "cores": threads, "kind": "port",
-             "sample": f"{k} recogniser lines of 3x48x320 one at a time, {threads} threads"})
+    k = [0]
+
+    def line(th):
+        r.run(lines[k[0] % 16], th)
+        k[0] += 1
+
+    res = {}
+    affinity = os.sched_getaffinity(0)
+    one = min(affinity)
+    os.sched_setaffinity(0, {one})
+    try:
+        res["det1"] = cpu_runs(lambda: m.run(img, 1), budget_s * 0.5)
+        res["rec1"] = cpu_runs(lambda: line(1), budget_s * 0.1)
+    finally:
+        os.sched_setaffinity(0, affinity)
+    res["detN"] = cpu_runs(lambda: m.run(img, threads), budget_s * 0.3)
+    res["recN"] = cpu_runs(lambda: line(threads), budget_s * 0.1)
+
+    def entry(key1, keyN, unit, per, what):
+        w1, c1, n1 = res[key1]
+        wN, cN, nN = res[keyN]
+        return {"value": round(per / wN, 3), "unit": unit, "cores": threads, "kind": "port",
+                "nproc": nproc, "one_thread_value": round(per / w1, 3),
+                "cpu_s_per_unit": round(cN / per, 4), "one_thread_cpu_s_per_unit": round(c1 / per, 4),
+                "sample": f"{what}: median of {nN} runs on {threads} OpenMP threads (nproc {nproc}) and of "
+                          f"{n1} runs on one thread pinned to core {one}; C oracle, tier-3 FMA order"}
+
+    return (entry("det1", "detN", "img/s", 1.0, "detector forwards at 1x3x960x960"),
+            entry("rec1", "recN", "lines/s", 1.0, "recogniser lines of 3x48x320, one line a run"))
 
 
 def main() -> int:
@@ -409,7 +482,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--cpu-seconds", type=float, default=30.0)
     ap.add_argument("--only", choices=["det", "rec", "all"], default="all")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -440,7 +513,8 @@ def main() -> int:
         "config": {"workload": "PP-OCR mobile-style DB detector forward, 1x3x960x960 synthetic "
                                "page, seeded N(0,0.05) weights (synthetic PPOCRPL1 plan)",
                    "batch": 1, "height": 960, "width": 960},
-        "roofline": {k: dom[k] for k in ("bound", "achieved", "peak", "unit", "frac")},
+        "roofline": {k: dom[k] for k in ("bound", "achieved", "peak", "unit", "frac") if k in dom}
+                    | {k: dom[k] for k in ("attainable", "frac_attainable") if k in dom},
         "wall_ms_per_step": round(det_wall, 4),
         "eager_ms_per_step": round(det_eager, 4),
         "with_host_copies_img_per_s": round(1e3 / pcie_ms, 2),
@@ -453,7 +527,8 @@ def main() -> int:
     result["roofline"]["kernel"] = launch_label(dom)
     result["roofline"]["launch_ms"] = round(dom["ms"], 5)
     result["det_kernels"] = by_kernel(det_rows)
-    result["det_launches"] = [[r["name"], r["ops"], round(r["ms"] * 1e3, 1), r["frac"]] for r in det_rows]
+    result["det_launches"] = [[r["name"], r["ops"], round(r["ms"] * 1e3, 1), r["frac"], r.get("frac_attainable")]
+                              for r in det_rows]
     if args.only in ("rec", "all"):
         log("bench: recogniser 16x3x48x320")
         rec_plan, rec_ms, rec_wall, rec_rows, rec_eager = bench_recognizer(P, nets, args.steps,
@@ -462,11 +537,12 @@ def main() -> int:
         result["rec"] = {"metric": "rec lines/s @16x3x48x320", "value": round(16e3 / rec_ms, 1),
                          "unit": "lines/s", "ms_per_batch": round(rec_ms, 4),
                          "eager_ms_per_batch": round(rec_eager, 4),
-                         "roofline": {k: rdom[k] for k in ("bound", "achieved", "peak", "unit", "frac")}
+                         "roofline": {k: rdom[k] for k in ("bound", "achieved", "peak", "unit", "frac",
+                                                           "attainable", "frac_attainable") if k in rdom}
                          | {"kernel": launch_label(rdom)},
                          "kernels": by_kernel(rec_rows),
-                         "launches": [[r["name"], r["ops"], round(r["ms"] * 1e3, 1), r["frac"]]
-                                      for r in rec_rows]}
+                         "launches": [[r["name"], r["ops"], round(r["ms"] * 1e3, 1), r["frac"],
+                                       r.get("frac_attainable")] for r in rec_rows]}
         log("bench: fused block, microkernels")
         result["block"] = bench_block(P, nets, args.steps, args.warmup)
         result["micro"] = bench_micro(P)

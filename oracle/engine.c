@@ -565,19 +565,32 @@ static void pointwise(const op_t *op, const float *x, float *y, const float *w, 
         size_t count = nr * op->ow;
         size_t bias_first = co % 16 == 0 ? count / 4 * 4 : 0;
         size_t fused = co / 8 * 8;
-        for (size_t p = 0; p < count; p++) {
-            const float *xp = x + (first * op->ow + p) * ci;
-            float *yp = y + (first * op->ow + p) * co;
-            for (size_t j = 0; j < co; j++) {
-                float acc = (b && p < bias_first) ? b[j] : 0.0f;
-                if (j < fused)
-                    for (size_t i = 0; i < ci; i++) acc = fmaf(w[i * co + j], xp[i], acc);
-                else
-                    for (size_t i = 0; i < ci; i++) acc = acc + xp[i] * w[i * co + j];
-                if (b && p >= bias_first) acc = acc + b[j];
-                yp[j] = oracle_act(acc, op->fused);
+        /* Four pixels at a time, every output's chain in input order; the
+         * innermost loops run across outputs (independent chains). */
+        float *acc = (float *)malloc(4 * co * sizeof(float));
+        for (size_t p0 = 0; p0 < count; p0 += 4) {
+            size_t np = count - p0 < 4 ? count - p0 : 4;
+            for (size_t q = 0; q < np; q++)
+                for (size_t j = 0; j < co; j++) acc[q * co + j] = (b && p0 + q < bias_first) ? b[j] : 0.0f;
+            for (size_t i = 0; i < ci; i++) {
+                const float *wi = w + i * co;
+                for (size_t q = 0; q < np; q++) {
+                    const float xi = x[(first * op->ow + p0 + q) * ci + i];
+                    float *a = acc + q * co;
+                    for (size_t j = 0; j < fused; j++) a[j] = fmaf(wi[j], xi, a[j]);
+                    for (size_t j = fused; j < co; j++) a[j] = a[j] + xi * wi[j];
+                }
+            }
+            for (size_t q = 0; q < np; q++) {
+                float *yp = y + (first * op->ow + p0 + q) * co;
+                for (size_t j = 0; j < co; j++) {
+                    float v = acc[q * co + j];
+                    if (b && p0 + q >= bias_first) v = v + b[j];
+                    yp[j] = oracle_act(v, op->fused);
+                }
             }
         }
+        free(acc);
     }
 }
 
@@ -585,9 +598,12 @@ static void pointwise(const op_t *op, const float *x, float *y, const float *w, 
  * `fused`, multiply then add for the rest. */
 static inline void tap_acc(float *acc, const float *tap, const float *px, size_t n, size_t co,
                            size_t fused) {
-    for (size_t i = 0; i < n; i++)
-        for (size_t j = 0; j < co; j++)
-            acc[j] = j < fused ? fmaf(tap[i * co + j], px[i], acc[j]) : acc[j] + px[i] * tap[i * co + j];
+    for (size_t i = 0; i < n; i++) {
+        const float *ti = tap + i * co;
+        const float xi = px[i];
+        for (size_t j = 0; j < fused; j++) acc[j] = fmaf(ti[j], xi, acc[j]);
+        for (size_t j = fused; j < co; j++) acc[j] = acc[j] + xi * ti[j];
+    }
 }
 
 /* Windowed dense convolution over one or two sources: kernels/dense.rs:38-147,
@@ -641,21 +657,22 @@ static void depthwise(const op_t *op, const float *x, float *y, const float *w, 
 #pragma omp parallel for schedule(static) num_threads(g_threads)
     for (oy = 0; oy < (long)op->oh; oy++) {
         for (size_t ox = 0; ox < op->ow; ox++) {
+            /* Each channel from its bias, taps row-major; the innermost
+             * loop runs across channels (independent chains). */
             float *yp = y + ((size_t)oy * op->ow + ox) * c;
-            for (size_t ch = 0; ch < c; ch++) {
-                float acc = b ? b[ch] : 0.0f;
-                for (size_t ky = 0; ky < op->kh; ky++) {
-                    long iy = (long)oy * (long)op->sh + (long)ky - op->pt;
-                    if (iy < 0 || iy >= (long)op->ih) continue;
-                    for (size_t kx = 0; kx < op->kw; kx++) {
-                        long ix = (long)ox * (long)op->sw + (long)kx - op->pl;
-                        if (ix < 0 || ix >= (long)op->iw) continue;
-                        acc = fmaf(w[(ky * op->kw + kx) * c + ch],
-                                   x[((size_t)iy * op->iw + (size_t)ix) * c + ch], acc);
-                    }
+            for (size_t ch = 0; ch < c; ch++) yp[ch] = b ? b[ch] : 0.0f;
+            for (size_t ky = 0; ky < op->kh; ky++) {
+                long iy = (long)oy * (long)op->sh + (long)ky - op->pt;
+                if (iy < 0 || iy >= (long)op->ih) continue;
+                for (size_t kx = 0; kx < op->kw; kx++) {
+                    long ix = (long)ox * (long)op->sw + (long)kx - op->pl;
+                    if (ix < 0 || ix >= (long)op->iw) continue;
+                    const float *wt = w + (ky * op->kw + kx) * c;
+                    const float *xt = x + ((size_t)iy * op->iw + (size_t)ix) * c;
+                    for (size_t ch = 0; ch < c; ch++) yp[ch] = fmaf(wt[ch], xt[ch], yp[ch]);
                 }
-                yp[ch] = oracle_act(acc, op->fused);
             }
+            for (size_t ch = 0; ch < c; ch++) yp[ch] = oracle_act(yp[ch], op->fused);
         }
     }
 }
@@ -841,11 +858,10 @@ static void ctc_head(const op_t *op, const float *x, float *y, const float *w, c
         for (size_t j = 0; j < panels; j++) {
             const float *panel = w + j * ci * PANEL;
             float logits[PANEL];
-            for (size_t col = 0; col < PANEL; col++) {
-                float acc = b[j * PANEL + col];
-                for (size_t i = 0; i < ci; i++) acc = fmaf(panel[i * PANEL + col], xp[i], acc);
-                logits[col] = acc;
-            }
+            for (size_t col = 0; col < PANEL; col++) logits[col] = b[j * PANEL + col];
+            for (size_t i = 0; i < ci; i++)
+                for (size_t col = 0; col < PANEL; col++)
+                    logits[col] = fmaf(panel[i * PANEL + col], xp[i], logits[col]);
             head_panel(&s, logits, j);
             if (probs) {
                 size_t n = vocab - j * PANEL < PANEL ? vocab - j * PANEL : PANEL;
