@@ -1,5 +1,5 @@
-// Host stages either side of the GPU model: CTC text decode and the DB
-// post-process (probability map -> text boxes). See post.cpp.
+// Host stages either side of the GPU model: CTC text decode (text.cpp) and
+// the DB post-process, probability map to text boxes (boxes.cpp).
 #pragma once
 #include <array>
 #include <cstddef>
