@@ -476,6 +476,42 @@ def cpu_baseline(nets, det_plan, rec_plan, budget_s: float) -> tuple[dict, dict]
             entry("rec1", "recN", "lines/s", 1.0, "recogniser lines of 3x48x320, one line a run"))
 
 
+def trace_runs(P, nets, which: str, runs: int) -> None:
+    """For rocprofv3 counter and kernel-trace runs: `runs` eager passes of
+    one workload, inputs resident, then its launch list (kernel, plan
+    operations, layer FLOPs and algorithmic bytes), one JSON line each, in
+    dispatch order. `copy` is the plain copy kernel (activation code 0) over
+    1x256x240x240 floats that HBM counters are scaled by."""
+    if which == "copy":
+        from ppocr_native_amd.devmem import DeviceArray, synchronize
+        n = 240 * 240 * 256
+        a = DeviceArray.of(np.random.default_rng(0).uniform(-1, 1, n).astype(np.float32))
+        y = DeviceArray(4 * n)
+        for _ in range(runs):
+            P.hip_activation(a.addr, y.addr, n, 0)
+        synchronize()
+        print(json.dumps({"name": "copy", "ops": [], "flops": 0, "bytes": 8 * n}), flush=True)
+        return
+    if which == "det":
+        g = P.GpuModel.load(nets.detector_plan(h=960, w=960, init="baseline"))
+        g.input_mut()[:] = nets.page_image(960, 960).reshape(-1)
+    elif which == "rec":
+        g = P.GpuModel.load(nets.recognizer_plan(init="baseline"))
+        lines = nets.line_images(16)
+        g.set_sizes([(48, 320)] * 16)
+        for i in range(16):
+            g.lane_input_mut(i)[:] = lines[i].reshape(-1)
+    else:
+        g = P.GpuModel.load(nets.fused_block_plan())
+        g.input_mut()[:] = np.random.default_rng(5).uniform(-1, 1, 160 * 160 * 96).astype(np.float32)
+    g.set_graphs(False)
+    g.upload()
+    g.run_resident(runs)
+    for (name, _), ops, (fl, by) in zip(g.launches(), g.launch_ops(), g.launch_work()):
+        print(json.dumps({"name": name, "ops": ops, "flops": fl, "bytes": by}), flush=True)
+    g.close()
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -484,6 +520,10 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--cpu-seconds", type=float, default=30.0)
     ap.add_argument("--only", choices=["det", "rec", "all"], default="all")
+    ap.add_argument("--trace", choices=["det", "rec", "block", "copy"],
+                    help="only run --trace-runs eager passes of one workload (for rocprofv3) "
+                         "and print its launch list")
+    ap.add_argument("--trace-runs", type=int, default=3)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the GPU path shards by page and by line batch with "
@@ -492,6 +532,9 @@ def main() -> int:
         return 2
     P = package()
     from ppocr_native_amd import nets
+    if args.trace:
+        trace_runs(P, nets, args.trace, args.trace_runs)
+        return 0
 
     log("bench: detector 1x3x960x960")
     det_plan, det_ms, det_wall, pcie_ms, det_rows, det_eager = bench_detector(P, nets, args.steps,
