@@ -319,6 +319,82 @@ hipError_t launch_attention(const float *x, long x_lane_stride, float scale, int
                             int heads, int lanes, float *y, long y_lane_stride, float *scratch,
                             hipStream_t s);
 
+// ------------------------------------------------------ transformer encoder
+
+// The encoder's GEMM weights (k inputs x n outputs, input-major as in the
+// plan) in MFMA operand order, inputs padded to kp (a multiple of 16): for
+// column block j and input group q of 16, 64 float4s, lane l's holding
+// W[16q + 4(l / 16) + e][16j + l % 16], e = 0..3, zero past k and n.
+int enc_kpad(int k);            // kp of the 1x1 layers over the encoder's width
+int enc_mlp_hpad(int hidden);   // kp of the MLP's fc2
+size_t enc_pack_floats(int kp, int n);
+void enc_pack(const float *w, int k, int n, int kp, float *out);
+
+// Rows of `rows` per lane, each lane `*_lane_stride` floats after the last.
+// y = act2(act(LN(x) W + bias) + res): LayerNorm when ln (gamma[k], beta[k],
+// eps) is set, the residual when res is.
+struct EncLinArgs {
+  int rows, lanes, k, n;
+  const float *x;
+  long x_lane_stride;
+  const float *ln;
+  const float *wt, *bias;  // wt: enc_pack, kp = enc_kpad(k)
+  int act, act2;
+  const float *res;
+  long res_lane_stride;
+  float *y;
+  long y_lane_stride;
+};
+bool enc_linear_supported(int k, int n);
+hipError_t launch_enc_linear(const EncLinArgs &a, hipStream_t s);
+
+// Attention of the lanes' t steps (rows of q | k | v, 3c floats), then
+// z = act2(act(attention Wp + bias) + res) with the c x c projection Wp;
+// when w1 is set, then y = act3m(z + act2m(act1m(LN(z) W1 + b1) W2 + b2))
+// and LN_out(y) in its place when ln_out is set; else y = z.
+struct EncAttnArgs {
+  int t, lanes, c, heads;
+  float scale;
+  const float *qkv;
+  long qkv_lane_stride;
+  const float *wt, *bias;  // wt: enc_pack, kp = enc_kpad(c)
+  int act, act2;
+  const float *res;
+  long res_lane_stride;
+  int hidden;
+  const float *ln;         // gamma[c], beta[c], eps
+  const float *w1, *b1;    // w1: enc_pack, kp = enc_kpad(c)
+  int act1m;
+  const float *w2, *b2;    // w2: enc_pack, kp = enc_mlp_hpad(hidden)
+  int act2m, act3m;
+  const float *ln_out;
+  float *y;
+  long y_lane_stride;
+};
+// hidden: the MLP's width, 0 without it.
+bool enc_attn_supported(int c, int heads, int hidden);
+bool enc_attn_fits(int t, int c, int heads, int hidden);  // the line's K and V fit LDS
+hipError_t launch_enc_attn(const EncAttnArgs &a, hipStream_t s);
+
+// z = act3(x + act2(act1(LN(x) W1 + b1) W2 + b2)) (the residual when
+// `residual`, else without x), then LN_out(z) in its place when ln_out is set.
+struct EncMlpArgs {
+  int rows, lanes, c, hidden;
+  const float *x;
+  long x_lane_stride;
+  const float *ln;
+  const float *w1, *b1;  // w1: enc_pack, kp = enc_kpad(c)
+  int act1;
+  const float *w2, *b2;  // w2: enc_pack, kp = enc_mlp_hpad(hidden)
+  int act2, act3;
+  int residual;
+  const float *ln_out;
+  float *y;
+  long y_lane_stride;
+};
+bool enc_mlp_supported(int c, int hidden);
+hipError_t launch_enc_mlp(const EncMlpArgs &a, hipStream_t s);
+
 hipError_t launch_row_argmax(const float *x, float *y, int rows, int cols, hipStream_t s);
 
 // Transposed convolution with few outputs per pixel (kh*kw*oc <= 16): one

@@ -63,7 +63,13 @@ void put_err(const std::string &m, char *err, size_t len) {
 
 size_t round_up(size_t v, size_t m) { return (v + m - 1) / m * m; }
 
-enum StepKind { S_GEMM, S_DW, S_ELT, S_POOL, S_MEAN, S_LN, S_ATTN, S_CTC, S_CONVT, S_DIRECT, S_HEAD };
+enum StepKind {
+  S_GEMM, S_DW, S_ELT, S_POOL, S_MEAN, S_LN, S_ATTN, S_CTC, S_CONVT, S_DIRECT, S_HEAD,
+  // The transformer encoder's fused steps: LayerNorm -> 1x1 (enc_linear),
+  // attention -> 1x1 -> Add (enc_attn_block), LayerNorm -> 1x1 -> 1x1 -> Add
+  // [-> LayerNorm] (enc_mlp), and the last two as one (enc_attn_block).
+  S_ENC_LIN, S_ENC_ATTN, S_ENC_MLP, S_ENC_BLOCK
+};
 
 struct Source {
   size_t slot;
@@ -76,7 +82,9 @@ struct Step {
   int gate = -1;     // Channelmul folded into a convolution's first input
   int add = -1;      // Add folded into a convolution's output / of a residual gate
   int resgate = -1;  // Channelmul of a residual gate, x + x * g
-  int fc1 = -1, fc2 = -1;  // squeeze-and-excite 1x1 layers after a Mean
+  int fc1 = -1, fc2 = -1;  // squeeze-and-excite 1x1 layers after a Mean; an encoder step's 1x1 layers
+  int ln_out = -1;         // S_ENC_MLP, S_ENC_BLOCK: the LayerNorm of its sum, written in its place
+  int m_ln = -1, m_fc1 = -1, m_fc2 = -1, m_add = -1;  // S_ENC_BLOCK: its MLP's operations
   int head2 = -1;          // the narrow transposed convolution folded into S_HEAD
   bool dw_sums = false;    // S_DW: also sum its output per channel for the next step's mean
   bool patch = false;      // S_GEMM: a windowed convolution on halo tiles (conv_patch)
@@ -89,6 +97,7 @@ struct Step {
   int gemm_n = 0, chunks = 0, ctot = 0, cpt = 0;
   size_t wt_off = 0, wt_k = 0;
   size_t se_w1 = 0, se_w2 = 0;  // S_MEAN with an SE: the 1x1 weights, 16-byte aligned in the packed arena
+  size_t enc_w1 = 0, enc_w2 = 0, enc_w3 = 0;  // encoder steps: their 1x1 weights in enc_pack order
 };
 
 enum GroupKind { GK_NONE = 0, GK_RING, GK_PATCH, GK_MEAN, GK_ELT };
@@ -189,6 +198,7 @@ struct Model {
   void group(Batch &b) const;
   bool run(bool copy_in, bool copy_out, std::string &err, bool sync = true);
   std::vector<size_t> step_reads(const Step &s) const;
+  int enc_hidden(const Step &s) const { return s.kind == S_ENC_BLOCK ? int(plan.ops[s.m_fc1].oc) : 0; }
   size_t step_writes(const Step &s) const;
 };
 
@@ -231,6 +241,19 @@ std::vector<size_t> Model::step_reads(const Step &s) const {
         if (op.has_second(&x2)) r.push_back(x2);
       }
       break;
+    case S_ENC_LIN:
+    case S_ENC_ATTN:
+    case S_ENC_MLP:
+    case S_ENC_BLOCK:
+      // Its first operation's input, and a residual other than that input.
+      r.push_back(op.x);
+      if (s.add >= 0) {
+        const Op &a = plan.ops[s.add];
+        const size_t last = plan.ops[s.kind == S_ENC_MLP ? s.fc2 : s.fc1].y;
+        const size_t res = a.x == last ? a.x2 : a.x;
+        if (res != op.x) r.push_back(res);
+      }
+      break;
     default:
       r.push_back(op.x);
   }
@@ -240,6 +263,9 @@ std::vector<size_t> Model::step_reads(const Step &s) const {
 size_t Model::step_writes(const Step &s) const {
   if (s.kind == S_HEAD) return plan.ops[s.head2].y;
   if (s.kind == S_MEAN && s.fc2 >= 0) return plan.ops[s.fc2].y;
+  if ((s.kind == S_ENC_MLP || s.kind == S_ENC_BLOCK) && s.ln_out >= 0) return plan.ops[s.ln_out].y;
+  if (s.kind == S_ENC_BLOCK) return plan.ops[s.m_add].y;
+  if ((s.kind == S_ENC_LIN || s.kind == S_ENC_ATTN) && s.add < 0) return plan.ops[s.fc1].y;
   if (s.kind == S_ELT && s.elt == ELT_UPSAMPLEADD_RESGATE) return plan.ops[s.op].y;
   if (s.add >= 0) return plan.ops[s.add].y;
   return plan.ops[s.op].y;
@@ -337,6 +363,21 @@ bool Model::build_steps(std::string &err) {
         }
       };
 
+  // Op k is a 1x1 convolution of one input, `from`, which nothing else reads.
+  auto plain_1x1 = [&](size_t k, size_t from) {
+    return k < n && ops[k].kind == K_CONV && ops[k].is_pointwise() && ops[k].x == from && ops[k].n2 == 0 &&
+           readers[from] == 1;
+  };
+  // Op k adds `from` (which nothing else reads) and `other`.
+  auto adds = [&](size_t k, size_t from, size_t other) {
+    return k < n && ops[k].kind == K_ADD && readers[from] == 1 &&
+           ((ops[k].x == from && ops[k].x2 == other) || (ops[k].x2 == from && ops[k].x == other));
+  };
+  // Op k adds `from` (which nothing else reads) to another buffer.
+  auto add_after = [&](size_t k, size_t from) {
+    return k < n && ops[k].kind == K_ADD && readers[from] == 1 && ((ops[k].x == from) != (ops[k].x2 == from));
+  };
+
   std::vector<bool> folded(n, false);
   std::vector<int> inside;
   steps.clear();
@@ -423,8 +464,47 @@ bool Model::build_steps(std::string &err) {
         }
         break;
       }
-      case K_LAYERNORM: s.kind = S_LN; break;
-      case K_ATTENTION: s.kind = S_ATTN; break;
+      case K_LAYERNORM: {
+        // The encoder's pre-norm layers: LayerNorm -> 1x1 -> 1x1 -> Add of
+        // the LayerNorm's input (the MLP and its residual), with the next
+        // LayerNorm folded in when only it reads the sum; else LayerNorm ->
+        // 1x1 (the q|k|v projection), with an Add after it folded in.
+        s.kind = S_LN;
+        const size_t c = op.oc;
+        if (plain_1x1(i + 1, op.y) && ops[i + 1].ic == c && plain_1x1(i + 2, ops[i + 1].y) &&
+            ops[i + 2].oc == c && adds(i + 3, ops[i + 2].y, op.x) &&
+            enc_mlp_supported(int(c), int(ops[i + 1].oc))) {
+          s.kind = S_ENC_MLP;
+          s.fc1 = int(i + 1), s.fc2 = int(i + 2), s.add = int(i + 3);
+          folded[i + 1] = folded[i + 2] = folded[i + 3] = true;
+          const size_t z = ops[i + 3].y;
+          if (i + 4 < n && ops[i + 4].kind == K_LAYERNORM && ops[i + 4].x == z && readers[z] == 1 &&
+              ops[i + 4].oc == c) {
+            s.ln_out = int(i + 4);
+            folded[i + 4] = true;
+          }
+        } else if (plain_1x1(i + 1, op.y) && ops[i + 1].ic == c &&
+                   enc_linear_supported(int(c), int(ops[i + 1].oc))) {
+          s.kind = S_ENC_LIN;
+          s.fc1 = int(i + 1);
+          folded[i + 1] = true;
+          if (add_after(i + 2, ops[i + 1].y)) s.add = int(i + 2), folded[i + 2] = true;
+        }
+        break;
+      }
+      case K_ATTENTION: {
+        // Attention -> its c -> c output projection, with an Add after it.
+        s.kind = S_ATTN;
+        const size_t c = op.oc;
+        if (plain_1x1(i + 1, op.y) && ops[i + 1].ic == c && ops[i + 1].oc == c &&
+            enc_attn_supported(int(c), int(op.n2), 0)) {
+          s.kind = S_ENC_ATTN;
+          s.fc1 = int(i + 1);
+          folded[i + 1] = true;
+          if (add_after(i + 2, ops[i + 1].y)) s.add = int(i + 2), folded[i + 2] = true;
+        }
+        break;
+      }
       case K_CTCARGMAX: s.kind = S_CTC; break;
       case K_CONVTRANSPOSE: {
         s.kind = op.kh * op.kw * op.oc <= 16 ? S_CONVT : S_GEMM;
@@ -454,6 +534,21 @@ bool Model::build_steps(std::string &err) {
                                return std::find(inside.begin(), inside.end(), s.op) != inside.end();
                              }),
               steps.end());
+  // Attention -> projection -> Add, then the MLP of that sum when nothing
+  // else reads the sum (its LayerNorm and its residual Add): one step, the
+  // sum never stored.
+  for (size_t k = 1; k < steps.size(); k++) {
+    Step &a = steps[k - 1], &m = steps[k];
+    if (a.kind != S_ENC_ATTN || a.add < 0 || m.kind != S_ENC_MLP) continue;
+    const size_t z = ops[a.add].y;
+    const Op &att = ops[a.op];
+    if (ops[m.op].x != z || readers[z] != 2 ||
+        !enc_attn_supported(int(att.oc), int(att.n2), int(ops[m.fc1].oc)))
+      continue;
+    a.kind = S_ENC_BLOCK;
+    a.m_ln = m.op, a.m_fc1 = m.fc1, a.m_fc2 = m.fc2, a.m_add = m.add, a.ln_out = m.ln_out;
+    steps.erase(steps.begin() + k);
+  }
   // A channel mean right after the depthwise convolution that produces its
   // input: the depthwise kernel sums its outputs per channel as it stores
   // them, and the mean step only joins those sums (no second read).
@@ -522,6 +617,29 @@ bool Model::pack(std::string &err) {
       s.se_w2 = round_up(packed.size(), 64);
       packed.resize(s.se_w2 + se_pack_floats(int(f2.ic), int(f2.oc)), 0.0f);
       se_pack(weights.data() + f2.w0, int(f2.ic), int(f2.oc), packed.data() + s.se_w2);
+      continue;
+    }
+    if (s.kind == S_ENC_LIN || s.kind == S_ENC_ATTN || s.kind == S_ENC_MLP || s.kind == S_ENC_BLOCK) {
+      // The encoder's 1x1 layers in MFMA operand order.
+      auto put = [&](const Op &f, int kp) {
+        const size_t at = round_up(packed.size(), 64);
+        packed.resize(at + enc_pack_floats(kp, int(f.oc)), 0.0f);
+        enc_pack(weights.data() + f.w0, int(f.ic), int(f.oc), kp, packed.data() + at);
+        return at;
+      };
+      const Op &f1 = ops[size_t(s.fc1)];
+      if (s.kind == S_ENC_BLOCK) {
+        const Op &g1 = ops[size_t(s.m_fc1)], &g2 = ops[size_t(s.m_fc2)];
+        s.enc_w1 = put(f1, enc_kpad(int(f1.ic)));
+        s.enc_w2 = put(g1, enc_kpad(int(g1.ic)));
+        s.enc_w3 = put(g2, enc_mlp_hpad(int(g2.ic)));
+      } else if (s.kind == S_ENC_MLP) {
+        const Op &f2 = ops[size_t(s.fc2)];
+        s.enc_w1 = put(f1, enc_kpad(int(f1.ic)));
+        s.enc_w2 = put(f2, enc_mlp_hpad(int(f2.ic)));
+      } else {
+        s.enc_w1 = put(f1, enc_kpad(int(f1.ic)));
+      }
       continue;
     }
     if (s.kind != S_GEMM && s.kind != S_CTC) continue;
@@ -756,6 +874,11 @@ bool Model::arrange(Batch &b, std::string &err) {
       need = L * op.iw * ntn * 4;
     }
     if (s.kind == S_ATTN) need = attention_scratch_floats(int(op.iw), int(op.oc), int(op.n2), int(L));
+    // Lines too long for the fused attention's LDS: attention rows, then the
+    // projection over them.
+    if ((s.kind == S_ENC_ATTN || s.kind == S_ENC_BLOCK) && !enc_attn_fits(int(op.iw), int(op.oc), int(op.n2), enc_hidden(s)))
+      need = round_up(L * op.iw * op.oc, 64) * (s.kind == S_ENC_BLOCK ? 2 : 1) +
+             attention_scratch_floats(int(op.iw), int(op.oc), int(op.n2), int(L));
     b.step_ws[i] = ws;
     ws += round_up(need, 64);
   }
@@ -1026,6 +1149,92 @@ void Model::build_launches(Batch &b) {
                               }});
         break;
       }
+      case S_ENC_LIN: {
+        const Op &f = p.ops[s.fc1];
+        EncLinArgs a{};
+        a.rows = int(op.oh * op.ow), a.lanes = L, a.k = int(f.ic), a.n = int(f.oc);
+        a.x = b.dev(op.x), a.x_lane_stride = b.stride(op.x);
+        a.ln = W + op.w0;
+        a.wt = dpacked + s.enc_w1, a.bias = f.b1 ? W + f.b0 : nullptr, a.act = f.fused;
+        if (s.add >= 0) {
+          const Op &ad = p.ops[s.add];
+          const size_t r = ad.x == f.y ? ad.x2 : ad.x;
+          a.res = b.dev(r), a.res_lane_stride = b.stride(r), a.act2 = ad.fused;
+        }
+        a.y = Y, a.y_lane_stride = ys;
+        b.launches.push_back({"ln_linear", s.op, [a](hipStream_t st) { return launch_enc_linear(a, st); }});
+        break;
+      }
+      case S_ENC_ATTN:
+      case S_ENC_BLOCK: {
+        const Op &f = p.ops[s.fc1];
+        EncAttnArgs a{};
+        a.t = int(op.iw), a.lanes = L, a.c = int(op.oc), a.heads = int(op.n2), a.scale = weights[op.w0];
+        a.qkv = b.dev(op.x), a.qkv_lane_stride = b.stride(op.x);
+        a.wt = dpacked + s.enc_w1, a.bias = f.b1 ? W + f.b0 : nullptr, a.act = f.fused;
+        if (s.add >= 0) {
+          const Op &ad = p.ops[s.add];
+          const size_t r = ad.x == f.y ? ad.x2 : ad.x;
+          a.res = b.dev(r), a.res_lane_stride = b.stride(r), a.act2 = ad.fused;
+        }
+        EncMlpArgs m{};  // the MLP part, for lines too long for one launch
+        if (s.kind == S_ENC_BLOCK) {
+          const Op &g1 = p.ops[s.m_fc1], &g2 = p.ops[s.m_fc2], &ln2 = p.ops[s.m_ln];
+          a.hidden = int(g1.oc), a.ln = W + ln2.w0;
+          a.w1 = dpacked + s.enc_w2, a.b1 = g1.b1 ? W + g1.b0 : nullptr, a.act1m = g1.fused;
+          a.w2 = dpacked + s.enc_w3, a.b2 = g2.b1 ? W + g2.b0 : nullptr, a.act2m = g2.fused;
+          a.act3m = p.ops[s.m_add].fused;
+          a.ln_out = s.ln_out >= 0 ? W + p.ops[s.ln_out].w0 : nullptr;
+          m.rows = a.t, m.lanes = L, m.c = a.c, m.hidden = a.hidden, m.ln = a.ln;
+          m.b1 = a.b1, m.act1 = a.act1m, m.b2 = a.b2, m.act2 = a.act2m, m.act3 = a.act3m;
+          m.residual = 1, m.ln_out = a.ln_out;
+        }
+        a.y = Y, a.y_lane_stride = ys;
+        if (enc_attn_fits(a.t, a.c, a.heads, a.w1 ? a.hidden : 0)) {
+          b.launches.push_back({s.kind == S_ENC_BLOCK ? "attention_block" : "attention_proj", s.op,
+                                [a](hipStream_t st) { return launch_enc_attn(a, st); }});
+          break;
+        }
+        // The attention rows into the workspace, then the projection (into
+        // the workspace too when the MLP follows), then the MLP.
+        float *rows = b.ws(si);
+        float *sum = rows + round_up(size_t(L) * a.t * a.c, 64);
+        float *scratch = s.kind == S_ENC_BLOCK ? sum + round_up(size_t(L) * a.t * a.c, 64) : sum;
+        const long rs = long(a.t) * a.c;
+        const float *x = a.qkv;
+        const long xs = a.qkv_lane_stride;
+        b.launches.push_back({"attention", s.op, [=](hipStream_t st) {
+                                return launch_attention(x, xs, a.scale, a.t, a.c, a.heads, L, rows, rs, scratch, st);
+                              }});
+        EncLinArgs g{};
+        g.rows = a.t, g.lanes = L, g.k = a.c, g.n = a.c;
+        g.x = rows, g.x_lane_stride = rs;
+        g.wt = a.wt, g.bias = a.bias, g.act = a.act, g.act2 = a.act2;
+        g.res = a.res, g.res_lane_stride = a.res_lane_stride;
+        g.y = s.kind == S_ENC_BLOCK ? sum : Y, g.y_lane_stride = s.kind == S_ENC_BLOCK ? rs : ys;
+        b.launches.push_back({"ln_linear", s.fc1, [g](hipStream_t st) { return launch_enc_linear(g, st); }});
+        if (s.kind == S_ENC_BLOCK) {
+          m.x = sum, m.x_lane_stride = rs;
+          m.w1 = a.w1, m.w2 = a.w2;
+          m.y = Y, m.y_lane_stride = ys;
+          b.launches.push_back({"ln_mlp", s.m_ln, [m](hipStream_t st) { return launch_enc_mlp(m, st); }});
+        }
+        break;
+      }
+      case S_ENC_MLP: {
+        const Op &f1 = p.ops[s.fc1], &f2 = p.ops[s.fc2], &ad = p.ops[s.add];
+        EncMlpArgs a{};
+        a.rows = int(op.oh * op.ow), a.lanes = L, a.c = int(op.oc), a.hidden = int(f1.oc);
+        a.x = b.dev(op.x), a.x_lane_stride = b.stride(op.x);
+        a.ln = W + op.w0;
+        a.w1 = dpacked + s.enc_w1, a.b1 = f1.b1 ? W + f1.b0 : nullptr, a.act1 = f1.fused;
+        a.w2 = dpacked + s.enc_w2, a.b2 = f2.b1 ? W + f2.b0 : nullptr, a.act2 = f2.fused;
+        a.act3 = ad.fused, a.residual = 1;
+        a.ln_out = s.ln_out >= 0 ? W + p.ops[s.ln_out].w0 : nullptr;
+        a.y = Y, a.y_lane_stride = ys;
+        b.launches.push_back({"ln_mlp", s.op, [a](hipStream_t st) { return launch_enc_mlp(a, st); }});
+        break;
+      }
       case S_CONVT: {
         ConvtArgs a{L, int(op.ih), int(op.iw), int(op.ic), int(op.oc), int(op.kh), int(op.kw),
                     b.dev(op.x), b.stride(op.x), W + op.w0, bias, op.fused, Y, ys};
@@ -1086,7 +1295,8 @@ void Model::link(Batch &b) const {
     for (size_t slot : step_reads(s)) rd.push_back(b.home[slot]);
     wr.push_back(b.home[step_writes(s)]);
     const size_t ws = H + size_t(l.step);
-    if (s.kind == S_MEAN || s.kind == S_CTC || s.kind == S_ATTN) rd.push_back(ws), wr.push_back(ws);
+    if (s.kind == S_MEAN || s.kind == S_CTC || s.kind == S_ATTN || s.kind == S_ENC_ATTN || s.kind == S_ENC_BLOCK)
+      rd.push_back(ws), wr.push_back(ws);
     if (s.kind == S_DW && s.dw_sums) wr.push_back(ws + 1);  // the next step's partial sums
     std::vector<int> deps;
     if (j > 0 && b.launches[j - 1].step == l.step) deps.push_back(int(j - 1));
@@ -1340,6 +1550,50 @@ void Model::account(Batch &b) const {
         double t = double(op.iw), hd = double(op.oc / op.n2);
         l.flops = L * op.n2 * t * t * hd * 4;
         l.bytes = F * L * t * (op.ic + op.oc);
+        break;
+      }
+      case S_ENC_LIN: {
+        const Op &f = p.ops[s.fc1];
+        const double M = L * out_px, K = double(f.ic), N = double(f.oc);
+        l.flops = 2.0 * M * N * K;
+        l.bytes = F * (M * K + 2.0 * K + 1 + K * N + (f.b1 ? N : 0) + M * N * (s.add >= 0 ? 2 : 1));
+        break;
+      }
+      case S_ENC_ATTN:
+      case S_ENC_BLOCK: {
+        const Op &f = p.ops[s.fc1];
+        const double t = double(op.iw), c = double(op.oc), hd = c / double(op.n2), M = L * t;
+        const double attn = L * op.n2 * t * t * hd * 4, proj = 2.0 * M * c * c;
+        const double w = F * (c * c + (f.b1 ? c : 0)), res = F * M * c * (s.add >= 0 ? 2 : 1);
+        double mlp_flops = 0, mlp_bytes = 0;  // the MLP after it, when merged
+        if (s.kind == S_ENC_BLOCK) {
+          const Op &g1 = p.ops[s.m_fc1], &g2 = p.ops[s.m_fc2];
+          const double h = double(g1.oc);
+          mlp_flops = 2.0 * M * c * h * 2;
+          mlp_bytes = F * (2 * c + 1 + 2 * c * h + (g1.b1 ? h : 0) + (g2.b1 ? c : 0) + (s.ln_out >= 0 ? 2 * c + 1 : 0));
+        }
+        if (b.launches.size() > li && b.launches[li].op == s.fc1) {
+          // Lines too long for one launch: attention rows to the workspace,
+          // the projection, then the MLP.
+          l.flops = attn, l.bytes = F * M * (op.ic + op.oc);
+          Launch &g = b.launches[li++];
+          g.flops = proj, g.bytes = F * M * c + w + res;
+          if (s.kind == S_ENC_BLOCK) {
+            Launch &m = b.launches[li++];
+            m.flops = mlp_flops, m.bytes = mlp_bytes + F * 2 * M * c;
+          }
+        } else {
+          l.flops = attn + proj + mlp_flops;
+          l.bytes = F * M * op.ic + w + res + mlp_bytes;
+        }
+        break;
+      }
+      case S_ENC_MLP: {
+        const Op &f1 = p.ops[s.fc1], &f2 = p.ops[s.fc2];
+        const double M = L * out_px, c = double(op.oc), h = double(f1.oc);
+        l.flops = 2.0 * M * c * h * 2;
+        l.bytes = F * (2 * M * c + 2 * c + 1 + 2 * c * h + (f1.b1 ? h : 0) + (f2.b1 ? c : 0) +
+                       (s.ln_out >= 0 ? 2 * c + 1 : 0));
         break;
       }
       case S_CONVT:
