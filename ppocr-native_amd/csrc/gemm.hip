@@ -26,6 +26,8 @@
 // activation (an Add folded in); a transposed convolution's spread store; or
 // the CTC head's per-row (max, sum of exp, first argmax) over the tile's
 // columns, merged across tiles by ctc_merge, so the logits never reach memory.
+#include <algorithm>
+
 #include "act.hpp"
 #include "kernels.hpp"
 
@@ -77,6 +79,88 @@ __device__ __forceinline__ ConvSrc pick_src(const ConvArgs &a, int c) {
 //  L_POINTWISE: 1x1 over one source (also the transposed conv's and the CTC
 //    head's input): base pointer plus a uniform channel offset.
 enum { L_FLAT = 0, L_SOURCES = 1, L_WINDOW = 2, L_POINTWISE = 3 };
+
+// The CTC head's epilogue for one wave's MT row blocks x NT column blocks
+// (rows from m_first, 16 a block; columns from n0): per row, the tile's
+// (max, sum of exp, first column of the max, second value). Each lane takes
+// the maximum of its NT columns (the first among equals: its columns rise
+// with j); the 16 lanes of the row then join the maximum, the sum of
+// exp(v - max) (hardware exp2, within 1 ulp: the sum is a probability's
+// denominator, held to a tolerance) and the lowest column holding the
+// maximum.
+template <int CTRL>
+__device__ __forceinline__ float dpp16(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+// Joins of the 16 lanes of a DPP row that leave the same bits in every lane:
+// pairs within quads, then mirrored quads (lane i <-> 7 - i), then mirrored
+// halves (lane i <-> 15 - i).
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp16<0xB1>(v));
+  v = fmaxf(v, dpp16<0x4E>(v));
+  v = fmaxf(v, dpp16<0x141>(v));
+  return fmaxf(v, dpp16<0x140>(v));
+}
+__device__ __forceinline__ float row16_min(float v) {
+  v = fminf(v, dpp16<0xB1>(v));
+  v = fminf(v, dpp16<0x4E>(v));
+  v = fminf(v, dpp16<0x141>(v));
+  return fminf(v, dpp16<0x140>(v));
+}
+__device__ __forceinline__ float row16_sum(float v) {
+  v = v + dpp16<0xB1>(v);
+  v = v + dpp16<0x4E>(v);
+  v = v + dpp16<0x141>(v);
+  return v + dpp16<0x140>(v);
+}
+
+template <int MT, int NT>
+__device__ __forceinline__ void ctc_rows(const f32x4 (&acc)[MT][NT], int m_first, int M, int n0, const float *bias,
+                                         int vocab, float *part, int ntn, int tn, int lane) {
+  const int li = lane & 15, lg = lane >> 4;
+  constexpr float L = 1.44269504088896341f;  // log2(e)
+  float bn[NT];  // this lane's columns' bias, once for the tile's rows
+#pragma unroll
+  for (int j = 0; j < NT; j++) {
+    const int n = n0 + j * 16 + li;
+    bn[j] = n < vocab ? bias[n] : 0.0f;
+  }
+#pragma unroll
+  for (int i = 0; i < MT; i++) {
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int m = m_first + i * 16 + lg * 4 + r;
+      float v[NT];
+      float lm = -__builtin_inff(), lb = __builtin_inff(), ls = -__builtin_inff();
+#pragma unroll
+      for (int j = 0; j < NT; j++) {
+        const int n = n0 + j * 16 + li;
+        v[j] = n < vocab ? acc[i][j][r] + bn[j] : -__builtin_inff();
+        if (v[j] > lm)
+          ls = lm, lm = v[j], lb = (float)n;
+        else if (v[j] > ls)
+          ls = v[j];
+      }
+      const float gm = row16_max(lm);
+      // The tile's second value (the maximum again when two columns hold
+      // it), for the near-tie check of ctc_merge.
+      float g2 = row16_max(lm == gm ? ls : lm);
+      const unsigned long long held = __ballot(lm == gm);
+      if (__popcll((held >> (lane & 48)) & 0xffffull) >= 2) g2 = gm;
+      const float c = gm * L;
+      float sum = 0.0f;
+#pragma unroll
+      for (int j = 0; j < NT; j++) sum += __builtin_amdgcn_exp2f(fmaf(v[j], L, -c));
+      sum = row16_sum(sum);
+      const float b = row16_min(lm == gm ? lb : __builtin_inff());
+      if (li == 0 && m < M) {
+        float4 *p = reinterpret_cast<float4 *>(part) + (long)m * ntn + tn;
+        *p = make_float4(gm, sum, b, g2);
+      }
+    }
+  }
+}
 
 template <int WM, int BN, int BK, int LAY, bool CTC>
 __global__ __launch_bounds__(256) void conv_mfma(ConvArgs a) {
@@ -286,55 +370,7 @@ __global__ __launch_bounds__(256) void conv_mfma(ConvArgs a) {
   }
 
   if constexpr (CTC) {
-    // Per row: the tile's (max, sum of exp, first column of the max). Each
-    // lane takes the maximum of its NT columns (the first among equals:
-    // its columns rise with j); the 16 lanes of the row then join the
-    // maximum, the sum of exp(v - max) (hardware exp2, within 1 ulp: the
-    // sum is a probability's denominator, held to a tolerance) and the
-    // lowest column holding the maximum.
-    constexpr float L = 1.44269504088896341f;  // log2(e)
-#pragma unroll
-    for (int i = 0; i < MT; i++) {
-#pragma unroll
-      for (int r = 0; r < 4; r++) {
-        const int m = m0 + wave * WM + i * 16 + lg * 4 + r;
-        float v[NT];
-        float lm = -__builtin_inff(), lb = __builtin_inff(), ls = -__builtin_inff();
-#pragma unroll
-        for (int j = 0; j < NT; j++) {
-          const int n = n0 + j * 16 + li;
-          v[j] = n < a.vocab ? acc[i][j][r] + a.bias[n] : -__builtin_inff();
-          if (v[j] > lm)
-            ls = lm, lm = v[j], lb = (float)n;
-          else if (v[j] > ls)
-            ls = v[j];
-        }
-        float gm = lm;
-#pragma unroll
-        for (int d = 1; d < 16; d <<= 1) gm = fmaxf(gm, __shfl_xor(gm, d, 64));
-        // The tile's second value (the maximum again when two columns hold
-        // it), for the near-tie check of ctc_merge.
-        float g2 = lm == gm ? ls : lm;
-#pragma unroll
-        for (int d = 1; d < 16; d <<= 1) g2 = fmaxf(g2, __shfl_xor(g2, d, 64));
-        const unsigned long long held = __ballot(lm == gm);
-        if (__popcll((held >> (lane & 48)) & 0xffffull) >= 2) g2 = gm;
-        const float c = gm * L;
-        float sum = 0.0f;
-#pragma unroll
-        for (int j = 0; j < NT; j++) sum += __builtin_amdgcn_exp2f(fmaf(v[j], L, -c));
-        float b = lm == gm ? lb : __builtin_inff();
-#pragma unroll
-        for (int d = 1; d < 16; d <<= 1) {
-          sum += __shfl_xor(sum, d, 64);
-          b = fminf(b, __shfl_xor(b, d, 64));
-        }
-        if (li == 0 && m < M) {
-          float4 *p = reinterpret_cast<float4 *>(a.part) + (long)m * ntn + tn;
-          *p = make_float4(gm, sum, b, g2);
-        }
-      }
-    }
+    ctc_rows<MT, NT>(acc, m0 + wave * WM, M, n0, a.bias, a.vocab, a.part, ntn, tn, lane);
     return;
   } else {
 #pragma unroll
@@ -686,6 +722,128 @@ __global__ __launch_bounds__(256) void ctc_merge(const float4 *part, int rows, i
     float *yp = y + (long)ln * y_lane_stride + 2L * tr;
     yp[0] = best;
     yp[1] = 1.0f / st.s;
+  }
+}
+
+// ------------------------------------------------------------ CTC, panels
+
+// The CTC head's GEMM when the head's input is at most 128 wide. A
+// workgroup keeps 128 rows (four waves of 32) in its operand registers for
+// the whole launch and walks a run of 64-column tiles: each tile's weights
+// (enc_pack order: four column blocks, 4 KB per group of 16 inputs) come
+// from global memory straight into one of two LDS stages (direct loads, the
+// next tile's in flight while the MFMAs run on this one), and every wave
+// reads its B fragments from there, one 16-byte read per lane per block and
+// group. Each tile's per-row partials go to ctc_merge as before. The
+// workgroups of one run of columns take one XCD's consecutive slots, so the
+// run's weights meet in that XCD's L2. Reduction order: groups of 16 inputs
+// in order, within a group four steps of one input per lane group.
+constexpr int kCtcRows = 128;
+
+template <int KQ>
+__global__ __launch_bounds__(256) void ctc_panel(CtcDirectArgs a, int row_tiles, int per_run) {
+  constexpr int MT = 2, NT = 4, STAGE = NT * KQ * 64 * 4;  // floats
+  extern __shared__ __attribute__((aligned(16))) float bs[];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int li = lane & 15, lg = lane >> 4;
+  const int M = a.rows_per_lane * a.lanes;
+  const int ntn = (a.vocab + 63) / 64, nb = (a.vocab + 15) / 16;
+  const int tile = xcd_tile(blockIdx.x, gridDim.x);
+  const int tm = tile % row_tiles, run = tile / row_tiles;
+  const int t0 = run * per_run, t1 = min(ntn, t0 + per_run);
+  const int m0 = tm * kCtcRows + wave * 32;
+  if (t0 >= t1) return;
+
+  // A tile's weights into stage `st`: 8 * KQ 16-byte groups a thread,
+  // blocks past the vocabulary read the last block (their columns are
+  // masked in the epilogue).
+  auto issue = [&](int t, int st) {
+    const f32x4 *src = reinterpret_cast<const f32x4 *>(a.wt);
+#pragma unroll
+    for (int i = 0; i < NT * KQ / 4; i++) {
+      const int e = i * 256 + tid;  // 16-byte group of the tile
+      const int blk = min(t * 4 + e / (KQ * 64), nb - 1);
+      const f32x4 *p = src + (long)blk * KQ * 64 + e % (KQ * 64);
+      __builtin_amdgcn_global_load_lds((const void *)p, (lds_void *)(bs + st * STAGE + (i * 256 + wave * 64) * 4), 16,
+                                       0, 0);
+    }
+  };
+  issue(t0, 0);
+
+  // This lane's rows (past the last row: the last row, never stored), zero
+  // past the input width.
+  f32x4 av[MT][KQ];
+#pragma unroll
+  for (int i = 0; i < MT; i++) {
+    const int m = min(m0 + 16 * i + li, M - 1);
+    const int ln = m / a.rows_per_lane;
+    const float *row = a.x + ln * a.x_lane_stride + (long)(m - ln * a.rows_per_lane) * a.ci;
+#pragma unroll
+    for (int q = 0; q < KQ; q++) {
+      const int k = 16 * q + 4 * lg;
+      av[i][q] = k < a.ci ? *reinterpret_cast<const f32x4 *>(row + k) : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  }
+
+  for (int t = t0; t < t1; t++) {
+    const int st = (t - t0) & 1;
+    // Every wave is done with the other stage (the tile before last).
+    ring_barrier();
+    if (t + 1 < t1) {
+      issue(t + 1, st ^ 1);
+      ring_wait<NT * KQ / 4>();
+    } else {
+      ring_wait<0>();
+    }
+    ring_barrier();  // this tile's weights have landed, from every wave
+    f32x4 acc[MT][NT];
+#pragma unroll
+    for (int i = 0; i < MT; i++)
+#pragma unroll
+      for (int j = 0; j < NT; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const f32x4 *bl = reinterpret_cast<const f32x4 *>(bs + st * STAGE) + lane;
+#pragma unroll
+    for (int q = 0; q < KQ; q++) {
+      f32x4 bv[NT];
+#pragma unroll
+      for (int j = 0; j < NT; j++) bv[j] = bl[(j * KQ + q) * 64];
+#pragma unroll
+      for (int e = 0; e < 4; e++)
+#pragma unroll
+        for (int i = 0; i < MT; i++)
+#pragma unroll
+          for (int j = 0; j < NT; j++)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[i][q][e], bv[j][e], acc[i][j], 0, 0, 0);
+    }
+    ctc_rows<MT, NT>(acc, m0, M, t * 64, a.bias, a.vocab, a.part, ntn, t, lane);
+  }
+}
+
+bool ctc_direct_supported(int ci) { return ci > 0 && ci <= 128 && ci % 4 == 0; }
+
+hipError_t launch_ctc_direct(const CtcDirectArgs &a, hipStream_t s) {
+  if (!ctc_direct_supported(a.ci) || a.x_lane_stride % 4 || a.vocab <= 0) return hipErrorInvalidValue;
+  const long M = (long)a.rows_per_lane * a.lanes;
+  if (M <= 0 || M >= (1L << 31)) return hipErrorInvalidValue;
+  const int row_tiles = (int)((M + kCtcRows - 1) / kCtcRows), ntn = (a.vocab + 63) / 64;
+  // About two workgroups a CU (each holds two 32 KB stages).
+  const int runs = std::max(1, std::min(ntn, (512 + row_tiles - 1) / row_tiles));
+  const int per_run = (ntn + runs - 1) / runs;
+  const unsigned blocks = (unsigned)(row_tiles * ((ntn + per_run - 1) / per_run));
+  const int kq = enc_kpad(a.ci) / 16;
+  const size_t shm = (size_t)2 * 4 * kq * 64 * 16;
+  auto go = [&](auto kernel) {
+    if (shm > 64 * 1024) {
+      hipError_t e = allow_lds(reinterpret_cast<const void *>(kernel), int(shm));
+      if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL(kernel, dim3(blocks), dim3(256), shm, s, a, row_tiles, per_run);
+    return hipGetLastError();
+  };
+  switch (kq) {
+    case 2: return go(ctc_panel<2>);
+    case 4: return go(ctc_panel<4>);
+    default: return go(ctc_panel<8>);
   }
 }
 

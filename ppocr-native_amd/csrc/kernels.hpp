@@ -196,6 +196,23 @@ struct CtcExact {
 hipError_t launch_ctc_merge(const float *part, int rows, int ntiles, float *y, long y_lane_stride,
                             int rows_per_lane, const CtcExact &ex, hipStream_t s);
 
+// The CTC head's GEMM over an input at most 128 wide (a multiple of 4), its
+// operands read straight into MFMA registers: the rows of x (ci floats,
+// rows_per_lane of them per lane) against the weights in enc_pack order
+// (kp = enc_kpad(ci), columns padded to 16), bias per column; per row and
+// 64-column tile a float4 partial (max, sum of exp, first column of the
+// max, second value) for launch_ctc_merge.
+struct CtcDirectArgs {
+  const float *x;
+  long x_lane_stride;
+  int rows_per_lane, lanes, ci;
+  const float *wt, *bias;
+  int vocab;
+  float *part;
+};
+bool ctc_direct_supported(int ci);
+hipError_t launch_ctc_direct(const CtcDirectArgs &a, hipStream_t s);
+
 // ---------------------------------------------------------------- depthwise
 
 struct DwArgs {

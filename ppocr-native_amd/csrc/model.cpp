@@ -750,6 +750,24 @@ bool Model::pack(std::string &err) {
         }
       }
     }
+    if (s.kind == S_CTC && ctc_direct_supported(int(op.ic))) {
+      // The same weights in MFMA operand order for ctc_direct (the rows above
+      // serve ctc_merge's exact recomputation of near ties): for column block
+      // j and input group q of 16, lane l's four inputs 16q + 4(l / 16) + e of
+      // column 16j + l % 16, from the plan's panels of 16 columns.
+      const int ci = int(op.ic), kp = enc_kpad(ci), kq = kp / 16, nb = (N + 15) / 16;
+      s.enc_w1 = round_up(packed.size(), 64);
+      packed.resize(s.enc_w1 + enc_pack_floats(kp, N), 0.0f);
+      float *o = packed.data() + s.enc_w1;
+      for (int j = 0; j < nb; j++)
+        for (int q = 0; q < kq; q++)
+          for (int l = 0; l < 64; l++)
+            for (int e = 0; e < 4; e++) {
+              const int kk = 16 * q + 4 * (l >> 4) + e, nn = 16 * j + (l & 15);
+              if (kk < ci && nn < N)
+                o[(((size_t)j * kq + q) * 64 + l) * 4 + e] = w[(size_t(nn) / 16) * ci * 16 + size_t(kk) * 16 + nn % 16];
+            }
+    }
   }
   if (packed.empty()) return true;
   HIPTRY(hipMalloc(&dpacked, packed.size() * sizeof(float)), "allocating packed weights");
@@ -1038,7 +1056,13 @@ void Model::build_launches(Batch &b) {
         GemmTile t = s.tile;
         int ntn = (a.n + t.bn - 1) / t.bn;
         int rows = L * int(op.iw), T = int(op.iw);
-        b.launches.push_back({"ctc_gemm", s.op, [a, t](hipStream_t st) { return launch_conv(a, t, st); }});
+        if (ctc_direct_supported(int(op.ic))) {
+          const CtcDirectArgs d{a.src[0].p, a.src[0].lane_stride, T, L, int(op.ic), dpacked + s.enc_w1, a.bias,
+                                a.vocab, part};
+          b.launches.push_back({"ctc_gemm", s.op, [d](hipStream_t st) { return launch_ctc_direct(d, st); }});
+        } else {
+          b.launches.push_back({"ctc_gemm", s.op, [a, t](hipStream_t st) { return launch_conv(a, t, st); }});
+        }
         const CtcExact ex{a.src[0].p, a.src[0].lane_stride, int(op.ic), a.wt, a.wt_k, a.bias, a.vocab, t.bn};
         b.launches.push_back({"ctc_merge", s.op, [part, rows, ntn, Y, ys, T, ex](hipStream_t st) {
                                 return launch_ctc_merge(part, rows, ntn, Y, ys, T, ex, st);
