@@ -738,11 +738,16 @@ __global__ __launch_bounds__(256) void ctc_merge(const float4 *part, int rows, i
 // workgroups of one run of columns take one XCD's consecutive slots, so the
 // run's weights meet in that XCD's L2. Reduction order: groups of 16 inputs
 // in order, within a group four steps of one input per lane group.
-constexpr int kCtcRows = 128;
+// Measured on 1280 x 18385 x 120: 32-row waves (64-row waves: 72 -> 86 us,
+// their 230 VGPRs leave one wave a SIMD) and about 512 workgroups (256:
+// 88 us, 1024: 74 us).
+constexpr int kCtcMt = 2;                 // row blocks of 16 a wave
+constexpr int kCtcRows = 64 * kCtcMt;     // rows a workgroup
+constexpr int kCtcTarget = 512;           // workgroups a launch aims at
 
 template <int KQ>
 __global__ __launch_bounds__(256) void ctc_panel(CtcDirectArgs a, int row_tiles, int per_run) {
-  constexpr int MT = 2, NT = 4, STAGE = NT * KQ * 64 * 4;  // floats
+  constexpr int MT = kCtcMt, NT = 4, STAGE = NT * KQ * 64 * 4;  // floats
   extern __shared__ __attribute__((aligned(16))) float bs[];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int li = lane & 15, lg = lane >> 4;
@@ -751,7 +756,7 @@ __global__ __launch_bounds__(256) void ctc_panel(CtcDirectArgs a, int row_tiles,
   const int tile = xcd_tile(blockIdx.x, gridDim.x);
   const int tm = tile % row_tiles, run = tile / row_tiles;
   const int t0 = run * per_run, t1 = min(ntn, t0 + per_run);
-  const int m0 = tm * kCtcRows + wave * 32;
+  const int m0 = tm * kCtcRows + wave * 16 * MT;
   if (t0 >= t1) return;
 
   // A tile's weights into stage `st`: 8 * KQ 16-byte groups a thread,
@@ -827,7 +832,7 @@ hipError_t launch_ctc_direct(const CtcDirectArgs &a, hipStream_t s) {
   if (M <= 0 || M >= (1L << 31)) return hipErrorInvalidValue;
   const int row_tiles = (int)((M + kCtcRows - 1) / kCtcRows), ntn = (a.vocab + 63) / 64;
   // About two workgroups a CU (each holds two 32 KB stages).
-  const int runs = std::max(1, std::min(ntn, (512 + row_tiles - 1) / row_tiles));
+  const int runs = std::max(1, std::min(ntn, (kCtcTarget + row_tiles - 1) / row_tiles));
   const int per_run = (ntn + runs - 1) / runs;
   const unsigned blocks = (unsigned)(row_tiles * ((ntn + per_run - 1) / per_run));
   const int kq = enc_kpad(a.ci) / 16;
