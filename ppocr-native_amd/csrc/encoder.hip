@@ -223,7 +223,8 @@ hipError_t launch_enc_linear(const EncLinArgs &a, hipStream_t s) {
 
 // --------------------------------------------------------- enc_attn_block
 
-// Workgroup b: lane b / runs, query rows tq * (b % runs) onward, every head:
+// Tile b (workgroups renumbered XCD by XCD): lane b / runs, query rows
+// tq * (b % runs) onward, every head:
 // heads * tq <= 64 score rows (head, query), eight threads a row, thread p
 // of a row taking keys j = p, p + 8, ... (the engine's softmax lanes).
 // LDS: K and V of the line per head (rows padded to 16 floats), the run's
@@ -266,7 +267,10 @@ __global__ __launch_bounds__(kEncThreads) void enc_attn_block(EncAttnArgs a, int
   constexpr int S = KP + 4, KQ = KP / 16;
   const int t = a.t, c = a.c, heads = a.heads, hd = c / heads, c4 = c / 4;
   const int runs = (t + tq - 1) / tq;
-  const int ln = blockIdx.x / runs, q0 = (blockIdx.x % runs) * tq, nq = min(tq, t - q0);
+  // The runs of one line on one XCD (each reads the line's K and V: they
+  // then meet in that XCD's L2).
+  const int tile = xcd_tile(blockIdx.x, gridDim.x);
+  const int ln = tile / runs, q0 = (tile % runs) * tq, nq = min(tq, t - q0);
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const AttnLds L = attn_lds(t, heads, tq, KP, HP);
   float *ks = sm + L.ks, *vs = sm + L.vs, *qs = sm + L.qs, *sc = sm + L.sc;
