@@ -424,7 +424,17 @@ __global__ __launch_bounds__(256) void conv_mfma(ConvArgs a) {
 constexpr int kPatchPer = 6;
 constexpr int kWeightPer = 9;
 
-template <int WR, int BN, int CB>
+// R8 (BN = 32, 17 to 24 output channels): the second column block holds at
+// most 8 real columns, which run on v_mfma_f32_4x4x1f32 instead of a 16 x 16
+// block three quarters padding. That instruction makes 16 independent 4 x 4
+// products: block b takes the A operand of lanes 4b..4b+3 and the B operand
+// of the same lanes, and lane 4b + j keeps column j of rows 0..3 in its four
+// accumulators. The A operand is the main block's own (lane l: pixel l % 16
+// at reduction index set l / 16), so block b covers pixels 4(b % 4)..+3 over
+// the reduction indices of lane group b / 4, against columns 16 + 4c..+3
+// (c = 0, 1: two instructions); the four lane groups' partial sums are added
+// at the end ((p0 + p1) + (p2 + p3), the same bits in every lane).
+template <int WR, int BN, int CB, bool R8>
 __global__ __launch_bounds__(256) void conv_patch(Group<ConvArgs> grp) {
   // Each XCD takes a contiguous run of tiles (xcd_tile): neighbouring tiles
   // share halo rows and columns, which then meet in one L2.
@@ -439,7 +449,8 @@ __global__ __launch_bounds__(256) void conv_patch(Group<ConvArgs> grp) {
   constexpr int KS = CB / 4;       // channels per lane group per tap
   constexpr int KW = KS >= 4 ? 4 : KS;
   constexpr int KR = KS / KW;
-  constexpr int NT = BN / 16;
+  static_assert(!R8 || BN == 32, "the 8-column remainder follows one 16-column block");
+  constexpr int NT = R8 ? 1 : BN / 16;  // 16 x 16 column blocks
   constexpr int TH = 4 * WR, TW = 16;
   constexpr int CQ = CB / 4;       // float4 groups per pixel
   extern __shared__ __attribute__((aligned(16))) float lds[];
@@ -478,6 +489,20 @@ __global__ __launch_bounds__(256) void conv_patch(Group<ConvArgs> grp) {
   for (int i = 0; i < WR; i++)
 #pragma unroll
     for (int j = 0; j < NT; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // R8: the remainder's columns 16 + 4c + lane % 4 and their accumulators.
+  constexpr int NR = R8 ? 2 : 0;
+  int rbase[R8 ? 2 : 1], rstep[R8 ? 2 : 1];
+  f32x4 accr[WR][R8 ? 2 : 1];
+  if constexpr (R8) {
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
+      const int n = 16 + 4 * c + (lane & 3);
+      rbase[c] = n < nr ? n * taps * S : nr * taps * S;
+      rstep[c] = n < nr ? S : 0;
+#pragma unroll
+      for (int i = 0; i < WR; i++) accr[i][c] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  }
 
   // Each thread stages one channel group q of every (256 / CQ)-th patch
   // pixel (at most kPatchPer of them), walking the pixels without divisions,
@@ -562,21 +587,34 @@ __global__ __launch_bounds__(256) void conv_patch(Group<ConvArgs> grp) {
 #pragma unroll
         for (int j = 0; j < NT; j++)
           bv[j] = *reinterpret_cast<const KT *>(Bs + bbase[j] + tp * bstep[j] + lg * KS + r * KW);
+        KT br[R8 ? 2 : 1];
+        if constexpr (R8) {
+#pragma unroll
+          for (int c = 0; c < NR; c++)
+            br[c] = *reinterpret_cast<const KT *>(Bs + rbase[c] + tp * rstep[c] + lg * KS + r * KW);
+        }
 #pragma unroll
         for (int k = 0; k < KW; k++) {
 #pragma unroll
           for (int i = 0; i < WR; i++) {
+            float x;
+            if constexpr (KW == 1) x = av[i];
+            else x = av[i][k];
 #pragma unroll
             for (int j = 0; j < NT; j++) {
-              float x, w;
-              if constexpr (KW == 1) {
-                x = av[i];
-                w = bv[j];
-              } else {
-                x = av[i][k];
-                w = bv[j][k];
-              }
+              float w;
+              if constexpr (KW == 1) w = bv[j];
+              else w = bv[j][k];
               acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(x, w, acc[i][j], 0, 0, 0);
+            }
+            if constexpr (R8) {
+#pragma unroll
+              for (int c = 0; c < NR; c++) {
+                float w;
+                if constexpr (KW == 1) w = br[c];
+                else w = br[c][k];
+                accr[i][c] = __builtin_amdgcn_mfma_f32_4x4x1f32(x, w, accr[i][c], 0, 0, 0);
+              }
             }
           }
         }
@@ -608,6 +646,31 @@ __global__ __launch_bounds__(256) void conv_patch(Group<ConvArgs> grp) {
         v = act(v, a.act);
         if (a.res) v = act(v + a.res[(long)ln * a.res_lane_stride + rem * a.n + n], a.act2);
         a.y[(long)ln * a.y_lane_stride + rem * a.n + n] = v;
+      }
+    }
+  }
+  if constexpr (R8) {
+    // The lane groups' partial sums, added the same way in every lane; then
+    // lane group g stores row g of each 4 x 4 block: pixel 4 * (li / 4) + g,
+    // column n0 + 16 + 4c + li % 4.
+#pragma unroll
+    for (int i = 0; i < WR; i++) {
+      const int oy = ty0 + wave * WR + i;
+#pragma unroll
+      for (int c = 0; c < NR; c++) {
+        f32x4 v = accr[i][c];
+#pragma unroll
+        for (int e = 0; e < 4; e++) v[e] = v[e] + __shfl_xor(v[e], 16);
+#pragma unroll
+        for (int e = 0; e < 4; e++) v[e] = v[e] + __shfl_xor(v[e], 32);
+        const int ox = tx0 + 4 * (li >> 2) + lg, n = n0 + 16 + 4 * c + (li & 3);
+        if (oy >= a.oh || ox >= a.ow || n >= a.n) continue;
+        const long rem = (long)oy * a.ow + ox;
+        float u = lg == 0 ? v[0] : (lg == 1 ? v[1] : (lg == 2 ? v[2] : v[3]));
+        if (a.bias) u = u + a.bias[n];
+        u = act(u, a.act);
+        if (a.res) u = act(u + a.res[(long)ln * a.res_lane_stride + rem * a.n + n], a.act2);
+        a.y[(long)ln * a.y_lane_stride + rem * a.n + n] = u;
       }
     }
   }
@@ -933,18 +996,36 @@ __global__ __launch_bounds__(256) void conv_ring(Group<ConvArgs> grp) {
   const int chunks = WIN ? a.chunks : (a.ctot + BK - 1) / BK;
   const int KP = chunks * BK;
 
-  // The gate rows, zero past ctot, before any direct load is issued.
+  // The residual rows of the outputs this thread stores go out first, into
+  // registers, so that their latency runs beside the operands'; then the
+  // gate rows (zero past ctot) by direct loads into LDS, ahead of the
+  // chunks, so that waiting for the first chunk also waits for them.
   const int lane0 = m0 / per_lane;
-  if constexpr (GATE) {
-    const int kv = KP / 4;
-    for (int e = tid; e < gate_lanes * kv; e += 256) {
-      const int l = e / kv, k = (e - l * kv) * 4;
-      f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
-      if (k < a.ctot && lane0 + l < a.lanes)
-        v = *reinterpret_cast<const f32x4 *>(a.gate + (long)(lane0 + l) * a.gate_lane_stride + k);
-      *reinterpret_cast<f32x4 *>(gs + l * KP + k) = v;
+  constexpr int RV = MT * NT;  // residual float4s per thread
+  const bool rows_store = a.mode == GEMM_STORE && ring_rows_store(a);
+  f32x4 rv[RV];
+  if (rows_store && a.res) {
+    constexpr int CV = BN / 4;
+#pragma unroll
+    for (int i = 0; i < RV; i++) {
+      const int e = tid + 256 * i, row = e / CV, c4 = e - row * CV;
+      const int m = m0 + row, n = n0 + c4 * 4;
+      rv[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (m < M && n < a.n) {
+        const int ln = m / per_lane, rem = m - ln * per_lane;
+        rv[i] = *reinterpret_cast<const f32x4 *>(a.res + (long)ln * a.res_lane_stride + (long)rem * a.n + n);
+      }
     }
-    __syncthreads();
+  }
+  if constexpr (GATE) {
+    const int kv = KP / 4, gslots = gate_lanes * kv;
+    for (int q = wave; q * 64 < gslots; q += 4) {
+      const int u = q * 64 + lane, l = u / kv, k = (u - l * kv) * 4;
+      const float *p = l < gate_lanes && k < a.ctot && lane0 + l < a.lanes
+                           ? a.gate + (long)(lane0 + l) * a.gate_lane_stride + k
+                           : kRingZeros;
+      __builtin_amdgcn_global_load_lds((const void *)p, (lds_void *)(gs + q * 256), 16, 0, 0);
+    }
   }
 
   // The global row and group each lane fetches for each of its direct loads.
@@ -1043,6 +1124,7 @@ __global__ __launch_bounds__(256) void conv_ring(Group<ConvArgs> grp) {
   for (int s = 0; s < ST - 1; s++)
     if (s < chunks) issue(s, s);
 
+
   for (int q = 0; q < chunks; q++) {
     // Chunk q is complete once no more than the later chunks' loads are
     // pending; the barrier then also frees the stage chunk q - 1 used.
@@ -1098,18 +1180,19 @@ __global__ __launch_bounds__(256) void conv_ring(Group<ConvArgs> grp) {
         }
     __syncthreads();
     constexpr int CV = BN / 4;
-    for (int e = tid; e < BM * CV; e += 256) {
-      const int row = e / CV, c4 = e - row * CV;
+    static_assert(BM * CV == 256 * RV, "one residual float4 per thread and store");
+#pragma unroll
+    for (int i = 0; i < RV; i++) {
+      const int e = tid + 256 * i, row = e / CV, c4 = e - row * CV;
       const int m = m0 + row, n = n0 + c4 * 4;
       if (m >= M || n >= a.n) continue;
       const int ln = m / per_lane, rem = m - ln * per_lane;
       f32x4 v = *reinterpret_cast<const f32x4 *>(ring + row * TS + c4 * 4);
       if (a.res) {
-        const f32x4 rv = *reinterpret_cast<const f32x4 *>(a.res + (long)ln * a.res_lane_stride + (long)rem * a.n + n);
-        v.x = act(v.x + rv.x, a.act2);
-        v.y = act(v.y + rv.y, a.act2);
-        v.z = act(v.z + rv.z, a.act2);
-        v.w = act(v.w + rv.w, a.act2);
+        v.x = act(v.x + rv[i].x, a.act2);
+        v.y = act(v.y + rv[i].y, a.act2);
+        v.z = act(v.z + rv[i].z, a.act2);
+        v.w = act(v.w + rv[i].w, a.act2);
       }
       *reinterpret_cast<f32x4 *>(a.y + (long)ln * a.y_lane_stride + (long)rem * a.n + n) = v;
     }
@@ -1167,7 +1250,8 @@ static size_t ring_lds(const ConvArgs &a, int mt, int nt, int st, int bk) {
   const int bm = 32 * mt, bn = 32 * nt, kp = ring_chunks(a, bk) * bk;
   size_t b = (size_t)ring_stages(a, st, bk) * (bm + bn) * bk * sizeof(float);
   if (a.mode == GEMM_STORE && ring_rows_store(a)) b = std::max(b, (size_t)bm * (bn + 4) * sizeof(float));
-  if (a.gate) b += (size_t)ring_gate_lanes(a, bm) * kp * sizeof(float);
+  // Gate rows by whole direct loads of 64 16-byte slots.
+  if (a.gate) b += ((size_t)ring_gate_lanes(a, bm) * (kp / 4) + 63) / 64 * 64 * 16;
   return b;
 }
 
@@ -1340,7 +1424,7 @@ size_t patch_lds_bytes(const ConvArgs &a, int wr, int bk, int bn) {
   return (pr * pc + nr * a.kh * a.kw + 1) * (bk + 4) * sizeof(float);
 }
 
-template <int WR, int BN, int CB>
+template <int WR, int BN, int CB, bool R8 = false>
 static hipError_t go_patch(const ConvArgs *as, int n, hipStream_t s) {
   constexpr int TH = 4 * WR;
   Group<ConvArgs> grp{};
@@ -1363,15 +1447,16 @@ static hipError_t go_patch(const ConvArgs *as, int n, hipStream_t s) {
   grp.first[n] = (int)blocks;
   if (shm > 160 * 1024) return hipErrorInvalidValue;
   if (shm > 64 * 1024) {
-    hipError_t e = allow_lds(reinterpret_cast<const void *>(conv_patch<WR, BN, CB>), 160 * 1024);
+    hipError_t e = allow_lds(reinterpret_cast<const void *>(conv_patch<WR, BN, CB, R8>), 160 * 1024);
     if (e != hipSuccess) return e;
   }
-  hipLaunchKernelGGL((conv_patch<WR, BN, CB>), dim3((unsigned)blocks), dim3(256), shm, s, grp);
+  hipLaunchKernelGGL((conv_patch<WR, BN, CB, R8>), dim3((unsigned)blocks), dim3(256), shm, s, grp);
   return hipGetLastError();
 }
 
 #define PPOCR_PATCH(WR, CB)                                        \
   if (bn == 16) return go_patch<WR, 16, CB>(as, n, s);           \
+  if (bn == 32 && r8 && WR == 2) return go_patch<2, 32, CB, true>(as, n, s); \
   if (bn == 32) return go_patch<WR, 32, CB>(as, n, s);           \
   if (bn == 64) return go_patch<WR, 64, CB>(as, n, s);
 
@@ -1381,8 +1466,16 @@ hipError_t launch_conv_patch(const ConvArgs &a, int wr, int bk, int bn, hipStrea
 
 hipError_t launch_conv_patch_group(const ConvArgs *as, int n, int wr, int bk, int bn, hipStream_t s) {
   if (n < 1 || n > kGroupMax) return hipErrorInvalidValue;
-  for (int p = 0; p < n; p++)
+  // 17 to 24 columns on 32-column tiles of two row blocks a wave: the
+  // 8-column remainder (R8); the detector head's 3 x 3 went from 40 to 35
+  // us. With one row block a wave its registers (168 -> 240, or 16 spilled
+  // when held to 168) cost the third wave per SIMD the LDS leaves room for,
+  // and the neck's group went from 51 to 54 us.
+  bool r8 = bn == 32 && wr == 2;
+  for (int p = 0; p < n; p++) {
     if (!patch_supported(as[p], wr, bk, bn)) return hipErrorInvalidValue;
+    r8 = r8 && as[p].n > 16 && as[p].n <= 24;
+  }
   if (wr == 2) {
     if (bk == 32) { PPOCR_PATCH(2, 32) }
     if (bk == 16) { PPOCR_PATCH(2, 16) }

@@ -137,7 +137,9 @@ def test_ring_upsampled_sources(oracle):
 
 @pytest.mark.parametrize("k,s,ci,co,hw,lanes", [
     (3, 1, 96, 24, (30, 40), 3),     # the neck's 3 x 3: 8-row tiles? no, 4-row
-    (3, 1, 96, 24, (256, 256), 1),   # 512 tiles of 8 rows
+    (3, 1, 96, 24, (256, 256), 1),   # 512 tiles of 8 rows: columns 16-23 on the 4 x 4 MFMA
+    (3, 1, 32, 20, (256, 256), 1),   # the same with 4 padded columns in the remainder
+    (3, 2, 24, 17, (512, 512), 1),   # stride 2, one real column in the remainder
     (3, 2, 48, 32, (33, 50), 2),     # stride 2, two sources below
     (2, 1, 24, 12, (37, 29), 2),     # the stem's 2 x 2
     (3, 1, 20, 96, (17, 35), 2),     # two column tiles of 64, channel block 16 + 4 padding
