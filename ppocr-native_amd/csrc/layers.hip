@@ -250,9 +250,190 @@ static int dw_fixed_kind(const DwArgs &a) {
   return 0;
 }
 
+// ------------------------------------------------------- depthwise on tiles
+
+// The depthwise convolution on output tiles of TR rows x TW columns x 4 * CG
+// channels of one lane (TR, TW chosen on the host so that a tile has at most
+// 256 / CG pixels): the tile's input window (the tile plus its halo, all its
+// rows and columns, zero outside the image) and the taps' weights go into LDS
+// by direct loads, all of them in flight at once, then each thread computes
+// one output pixel of four channels from LDS. The same arithmetic as
+// dwconv_fixed: from the bias, taps row by row, one fused multiply-add each,
+// taps outside the image skipped (not multiplied by zero, which could turn a
+// -0 sum into +0). Where dwconv_fixed makes each thread wait for K rows of
+// loads in turn and gives small maps few threads, a tile waits for one round
+// of loads and every output has its own thread.
+//
+// With MEAN the tile also sums its outputs per channel in f64 (pixels in
+// thread order) into the partial row of its spatial tile: row (lane, tile)
+// of dw_mean_blocks(a) rows per lane, the channels of the tile's group.
+constexpr int kDwTileThreads = 256;
+
+struct DwTile {
+  int cg, tr, tw, tiles_x, tiles_y;
+};
+
+__device__ __attribute__((aligned(16))) float kDwZeros[4];
+
+// Input rows and columns a tile's window covers.
+__host__ __device__ inline int dw_tile_rows(const DwArgs &a, int tr) { return (tr - 1) * a.sh + a.kh; }
+__host__ __device__ inline int dw_tile_cols(const DwArgs &a, int tw) { return (tw - 1) * a.sw + a.kw; }
+
+template <int K, int S, int CG, bool MEAN>
+__global__ __launch_bounds__(kDwTileThreads) void dwconv_tile(DwArgs a, DwTile tt) {
+  extern __shared__ __attribute__((aligned(16))) float lds[];
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int groups = a.c / (4 * CG);
+  const int per_lane = tt.tiles_y * tt.tiles_x;
+  // Blocks numbered XCD by XCD: neighbouring tiles of one channel group,
+  // which share halo rows, meet in one L2.
+  int b = xcd_tile((int)blockIdx.x, (int)gridDim.x);
+  const int tx = b % tt.tiles_x;
+  b /= tt.tiles_x;
+  const int ty = b % tt.tiles_y;
+  b /= tt.tiles_y;
+  const int gi = b % groups, ln = b / groups;
+  const int oy0 = ty * tt.tr, ox0 = tx * tt.tw, c0 = gi * 4 * CG;
+  const int IR = dw_tile_rows(a, tt.tr), IC = dw_tile_cols(a, tt.tw);
+  const int iy0 = oy0 * a.sh - a.pt, ix0 = ox0 * S - a.pl;
+  const int win = IR * IC * CG;  // float4s of the window
+  constexpr int WA = (K * K * CG + 63) / 64 * 64;  // float4s of the weights' area (whole loads)
+  float *W = lds;                          // K * K taps x CG float4
+  float *X = lds + WA * 4;                 // IR x IC pixels x CG float4 (rounded up to whole loads)
+  const float *xl = a.x + (long)ln * a.x_lane_stride + c0;
+  // Direct loads: float4 u of an area from src(u), 64 per instruction, the
+  // instructions dealt over the waves.
+  for (int q = wave; q * 64 < K * K * CG; q += 4) {
+    const int u = q * 64 + lane;
+    const int tap = u / CG, g = u - tap * CG;
+    const float *p = u < K * K * CG ? a.w + (long)tap * a.c + c0 + 4 * g : kDwZeros;
+    __builtin_amdgcn_global_load_lds((const void *)p, (lds_void *)(W + q * 256), 16, 0, 0);
+  }
+  for (int q = wave; q * 64 < win; q += 4) {
+    const int u = q * 64 + lane;
+    const int pix = u / CG, g = u - pix * CG;
+    const int r = pix / IC, col = pix - r * IC;
+    const int iy = iy0 + r, ix = ix0 + col;
+    const float *p = u < win && iy >= 0 && iy < a.ih && ix >= 0 && ix < a.iw
+                         ? xl + ((long)iy * a.iw + ix) * a.c + 4 * g
+                         : kDwZeros;
+    __builtin_amdgcn_global_load_lds((const void *)p, (lds_void *)(X + q * 256), 16, 0, 0);
+  }
+  const int g = tid % CG, px = tid / CG;
+  const int r = px / tt.tw, col = px - r * tt.tw;
+  const int oy = oy0 + r, ox = ox0 + col;
+  const bool live = r < tt.tr && oy < a.oh && ox < a.ow;
+  const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+  f32x4 acc = a.bias && live ? *reinterpret_cast<const f32x4 *>(a.bias + c0 + 4 * g) : zero;
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  double sum[4] = {0.0, 0.0, 0.0, 0.0};
+  if (live) {
+    const int ry = r * a.sh, cx = col * S;
+#pragma unroll
+    for (int ky = 0; ky < K; ky++) {
+      const int iy = iy0 + ry + ky;
+      if (iy < 0 || iy >= a.ih) continue;
+      const float *xr = X + ((ry + ky) * IC + cx) * CG * 4 + 4 * g;
+#pragma unroll
+      for (int kx = 0; kx < K; kx++) {
+        const int ix = ix0 + cx + kx;
+        if (ix < 0 || ix >= a.iw) continue;
+        const f32x4 wv = *reinterpret_cast<const f32x4 *>(W + (ky * K + kx) * CG * 4 + 4 * g);
+        const f32x4 xv = *reinterpret_cast<const f32x4 *>(xr + kx * CG * 4);
+        acc.x = fmaf(wv.x, xv.x, acc.x);
+        acc.y = fmaf(wv.y, xv.y, acc.y);
+        acc.z = fmaf(wv.z, xv.z, acc.z);
+        acc.w = fmaf(wv.w, xv.w, acc.w);
+      }
+    }
+    f32x4 v = acc;
+    v.x = act(v.x, a.act);
+    v.y = act(v.y, a.act);
+    v.z = act(v.z, a.act);
+    v.w = act(v.w, a.act);
+    *reinterpret_cast<f32x4 *>(a.y + (long)ln * a.y_lane_stride + ((long)oy * a.ow + ox) * a.c + c0 + 4 * g) = v;
+    if constexpr (MEAN) sum[0] = v.x, sum[1] = v.y, sum[2] = v.z, sum[3] = v.w;
+  }
+  if constexpr (MEAN) {
+    // The tile's f64 sums per channel, its pixels added in thread order.
+    __syncthreads();  // every wave is done with the window: reuse it
+    double *red = reinterpret_cast<double *>(X);
+#pragma unroll
+    for (int k = 0; k < 4; k++) red[tid * 4 + k] = sum[k];
+    __syncthreads();
+    if (tid < 4 * CG) {
+      const int gg = tid / 4, k = tid % 4;
+      double tot = 0.0;
+      for (int pp = 0; pp < kDwTileThreads / CG; pp++) tot += red[(pp * CG + gg) * 4 + k];
+      a.mean_part[((long)ln * per_lane + ty * tt.tiles_x + tx) * a.c + c0 + tid] = tot;
+    }
+  }
+}
+
+// The tiling of a layer, or cg = 0 when the tiled kernel does not take it.
+// It takes channels a multiple of 16, the compiled windows, within the LDS
+// bound, and of those the layers where it ran faster than dwconv_fixed in
+// the detector's and the recogniser's graphs: 7 x 7 windows (the detector's
+// 60 x 60 x 192 12.6 -> 9.4 us, 30 x 30 x 384 12.0 -> 8.3 us), 5 x 5 windows
+// of at most 180K output float4s (times the stride), where few long-latency
+// threads leave the GPU idle (60 x 60 x 192 8.0 -> 6.7 us, stride 2 to 30 x
+// 30 x 192 9.3 -> 6.6 us), and 3 x 3 windows of one image without channel
+// sums (the detector's three: its graph 508 -> 505 us). On the recogniser's
+// sixteen lines and on the fused block's 3 x 3 with sums, dwconv_fixed's
+// four outputs a thread reusing their loaded rows win (recogniser 413 ->
+// 419 us, fused block 42.4 -> 47.9 us when tiled).
+static DwTile dw_tile_of(const DwArgs &a, bool sums) {
+  DwTile t{};
+  const bool kind = a.kh == a.kw && (a.kh == 3 || a.kh == 5 || a.kh == 7) && (a.sw == 1 || (a.sw == 2 && a.kh != 7));
+  if (!kind || a.c % 16 != 0 || a.sh < 1 || a.sh > 2) return t;
+  const long work = (long)a.lanes * a.oh * a.ow * (a.c / 4) * a.sw;
+  const bool one_image_3x3 = a.kh == 3 && a.lanes == 1 && !sums;
+  if (!(a.kh == 7 || (a.kh == 5 && work <= 180L * 1024) || one_image_3x3)) return t;
+  const int cg = a.c % 32 == 0 ? 8 : 4;
+  const int pix = kDwTileThreads / cg;
+  const int nx = (a.ow + pix - 1) / pix;
+  const int tw = (a.ow + nx - 1) / nx;
+  const int tr = std::max(1, std::min(pix / tw, a.oh));
+  const size_t win = size_t(dw_tile_rows(a, tr)) * dw_tile_cols(a, tw) * cg;
+  const size_t floats = (size_t(a.kh) * a.kw * cg + 63) / 64 * 64 * 4 + (win + 63) / 64 * 64 * 4;
+  if (floats * sizeof(float) > 64 * 1024) return t;
+  t.cg = cg, t.tr = tr, t.tw = tw, t.tiles_x = nx, t.tiles_y = (a.oh + tr - 1) / tr;
+  return t;
+}
+
+static size_t dw_tile_lds(const DwArgs &a, const DwTile &t) {
+  const size_t win = size_t(dw_tile_rows(a, t.tr)) * dw_tile_cols(a, t.tw) * t.cg;
+  const size_t wa = (size_t(a.kh) * a.kw * t.cg + 63) / 64 * 64 * 4;
+  size_t floats = wa + (win + 63) / 64 * 64 * 4;
+  if (a.mean_part) floats = std::max(floats, wa + kDwTileThreads * 4 * 2);
+  return floats * sizeof(float);
+}
+
+template <int CG, bool MEAN>
+static hipError_t go_dw_tile(const DwArgs &a, const DwTile &t, hipStream_t s) {
+  const long blocks = (long)a.lanes * (a.c / (4 * CG)) * t.tiles_y * t.tiles_x;
+  if (blocks < 1 || blocks > 0x7fffffffL) return hipErrorInvalidValue;
+  const dim3 grid((unsigned)blocks), block(kDwTileThreads);
+  const size_t lds = dw_tile_lds(a, t);
+  const int kind = a.kh * 10 + a.sw;
+#define PPOCR_DW_TILE(KK, SS) \
+  if (kind == KK * 10 + SS) { hipLaunchKernelGGL((dwconv_tile<KK, SS, CG, MEAN>), grid, block, lds, s, a, t); return hipGetLastError(); }
+  PPOCR_DW_TILE(3, 1) PPOCR_DW_TILE(3, 2) PPOCR_DW_TILE(5, 1) PPOCR_DW_TILE(5, 2) PPOCR_DW_TILE(7, 1)
+#undef PPOCR_DW_TILE
+  return hipErrorInvalidValue;
+}
+
+static hipError_t launch_dw_tile(const DwArgs &a, const DwTile &t, hipStream_t s) {
+  if (a.mean_part) return t.cg == 8 ? go_dw_tile<8, true>(a, t, s) : go_dw_tile<4, true>(a, t, s);
+  return t.cg == 8 ? go_dw_tile<8, false>(a, t, s) : go_dw_tile<4, false>(a, t, s);
+}
+
 bool dw_mean_supported(const DwArgs &a) { return a.c % 4 == 0 && a.c <= 1024 && dw_fixed_kind(a) != 0; }
 
 int dw_mean_blocks(const DwArgs &a) {
+  const DwTile t = dw_tile_of(a, true);
+  if (t.cg) return t.tiles_y * t.tiles_x;  // one partial row per spatial tile
   const int cv = a.c / 4, R = kDwMeanThreads / cv;
   const int runs = (a.ow + kDwRun - 1) / kDwRun;  // the run with the sums (dw_run)
   return (a.oh * runs + R - 1) / R;
@@ -283,6 +464,8 @@ hipError_t launch_dwconv(const DwArgs &a, hipStream_t s) {
   auto aligned = [](const void *p) { return p == nullptr || (uintptr_t(p) & 15) == 0; };
   bool vec = a.c % 4 == 0 && aligned(a.x) && aligned(a.y) && aligned(a.w) && aligned(a.bias) &&
              a.x_lane_stride % 4 == 0 && a.y_lane_stride % 4 == 0;
+  const DwTile t = dw_tile_of(a, a.mean_part != nullptr);
+  if (vec && t.cg) return launch_dw_tile(a, t, s);
   const int kind = dw_fixed_kind(a);
   if (a.mean_part) {
     // With the channel sums: only the fixed variants, one grid row per lane.
