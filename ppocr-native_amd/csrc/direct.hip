@@ -201,15 +201,11 @@ __global__ __launch_bounds__(256) void conv_stem_kernel(DirectArgs a) {
 template <int KH, int KW, int IC, int OC>
 __global__ __launch_bounds__(256) void conv_direct_pix(DirectArgs a) {
   static_assert(IC % 4 == 0 && OC % 4 == 0, "four channels at a time");
-  constexpr int T = KH * KW, FUSED = OC / 8 * 8;
+  constexpr int T = KH * KW, K = T * IC, FUSED = OC / 8 * 8;
+  __shared__ __attribute__((aligned(16))) float ws[K * OC];
   __shared__ __attribute__((aligned(16))) float out[256 * OC];
-  // Every lane of a wave multiplies by the same weight: read through the
-  // constant address space, the weights come by scalar loads into SGPRs
-  // (the scalar cache holds the layer's K x OC floats) and each fused
-  // multiply-add takes one as its scalar operand, instead of a broadcast
-  // LDS read per four weights.
-  typedef const __attribute__((address_space(4))) float cfloat;
-  cfloat *ws = (cfloat *)(a.w);
+  for (int e = threadIdx.x; e < K * OC; e += 256) ws[e] = a.w[e];
+  __syncthreads();
   const int per = a.oh * a.ow, total = a.lanes * per;
   // Blocks numbered XCD by XCD (xcd_tile): neighbouring output rows, which
   // read the same input rows, meet in one L2.
@@ -242,9 +238,14 @@ __global__ __launch_bounds__(256) void conv_direct_pix(DirectArgs a) {
 #pragma unroll
       for (int i = 0; i < IC; i++) {
         const float v = cur[i / 4][i % 4];
-        cfloat *wr = ws + (t * IC + i) * OC;
+        const float *wr = ws + (t * IC + i) * OC;
 #pragma unroll
-        for (int j = 0; j < OC; j++) acc[j] = j < FUSED ? fmaf(wr[j], v, acc[j]) : acc[j] + wr[j] * v;
+        for (int j = 0; j < OC; j += 4) {
+          const f32x4 w = *reinterpret_cast<const f32x4 *>(wr + j);
+#pragma unroll
+          for (int q = 0; q < 4; q++)
+            acc[j + q] = j + q < FUSED ? fmaf(w[q], v, acc[j + q]) : acc[j + q] + w[q] * v;
+        }
       }
 #pragma unroll
       for (int q = 0; q < IC / 4; q++) cur[q] = nxt[q];
