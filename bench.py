@@ -26,6 +26,11 @@ ROOT = Path(__file__).resolve().parent
 PEAK_HBM_GBS = 8000.0
 PEAK_FP32_MFMA_TFLOPS = 157.3
 GEMM_LAUNCHES = {"pointwise_gemm", "conv_gemm", "conv_patch", "convt_gemm", "ctc_gemm"}
+# Launches whose products run as FP32 fused multiply-adds on the vector ALUs
+# (in the CPU engine's order), scored against the unpacked FP32 vector rate:
+# 256 CUs x 4 SIMDs x 16 lanes x 2 flops x 2.4 GHz (packed FP32 is not used).
+PEAK_FP32_VALU_TFLOPS = 78.6
+VALU_LAUNCHES = {"stem_block"}
 # HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE,
 # scaled by a plain copy kernel's counters (x2.0 / x1.0), for the launches
 # the bench reports a roofline of: (kernel, plan operations) -> (read, write)
@@ -59,6 +64,10 @@ def roofline(name: str, flops: float, nbytes: float, ms: float) -> dict:
         return {"bound": "mfma", "achieved": round(ach, 3), "peak": PEAK_FP32_MFMA_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(ach / PEAK_FP32_MFMA_TFLOPS, 4),
                 "attainable": round(roof, 3), "frac_attainable": round(ach / roof, 4)}
+    if name in VALU_LAUNCHES and flops > 0:
+        ach = flops / (ms * 1e-3) / 1e12
+        return {"bound": "valu", "achieved": round(ach, 3), "peak": PEAK_FP32_VALU_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(ach / PEAK_FP32_VALU_TFLOPS, 4)}
     ach = nbytes / (ms * 1e-3) / 1e9
     return {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
             "frac": round(ach / PEAK_HBM_GBS, 4)}

@@ -322,6 +322,221 @@ hipError_t launch_conv_direct(const DirectArgs &a, hipStream_t s) {
   return hipGetLastError();
 }
 
+// ---------------------------------------------------------------- stem block
+
+// One workgroup per T x T tile of one lane's oh x ow maps. It computes s1
+// over the tile plus two rows and columns (what the pool and the 2x2 layers
+// read), the first 2x2 over the tile plus one row and column, then the max
+// pool and the second 2x2 over the tile; s1 and the first 2x2's output never
+// leave LDS. Each layer in the CPU engine's order: s1 from its bias, taps
+// [ky][kx] skipping those outside the input, channels in order, every column
+// a fused multiply-add (the stem rule, src/engine/conv.rs:146-236); a 2x2
+// from its bias for pixels left of first_end, else adding it last, taps
+// outside the map skipped, columns below C / 8 * 8 fused and the rest a
+// separate multiply and add (kernels/dense.rs:38-147); the pool seeded with
+// its first tap, a later tap inside the map kept only when greater
+// (conv.rs:404-440). The weights are wave-uniform reads, served by the
+// scalar cache into scalar operands, so LDS holds only the two maps.
+constexpr int kStemT = 14;
+// The bias of a layer that has none: its sums start from, or add, nothing.
+__device__ __attribute__((aligned(16))) float kStemNoBias[32];
+
+// ACT: the activation of all three layers, fixed at compile time (a
+// runtime choice per output would inline every activation's code).
+template <int C1, int C2, int C3, int ACT>
+__global__ __launch_bounds__(256) void stem_block(StemArgs a) {
+  constexpr int T = kStemT, R1 = T + 2, R2 = T + 1;
+  // Pixels an odd number of float4s apart: a wave's float4 reads of
+  // consecutive pixels fall in distinct banks.
+  constexpr int P1 = (C1 / 4) % 2 ? C1 : C1 + 4, P2 = (C2 / 4) % 2 ? C2 : C2 + 4;
+  constexpr int F2 = C2 / 8 * 8, F3 = C3 / 8 * 8;
+  static_assert(R1 * R1 == 256, "one s1 pixel per thread");
+  static_assert(C1 % 8 == 0 && C2 % 4 == 0 && C3 % 4 == 0, "float4 channels, every stem column fused");
+  __shared__ __attribute__((aligned(16))) float m1[R1 * R1 * P1];
+  __shared__ __attribute__((aligned(16))) float m2[R2 * R2 * P2];
+  const int tiles_x = (a.ow + T - 1) / T, tiles_y = (a.oh + T - 1) / T;
+  // Tiles numbered XCD by XCD (xcd_tile): neighbours, which share input
+  // rows, meet in one L2.
+  int t = xcd_tile((int)blockIdx.x, (int)gridDim.x);
+  const int tx = t % tiles_x;
+  t /= tiles_x;
+  const int ty = t % tiles_y;
+  const int ln = t / tiles_y;
+  const int y0 = ty * T, x0 = tx * T, tid = threadIdx.x;
+  // Read through the constant address space: wave-uniform scalar loads.
+  typedef const __attribute__((address_space(4))) float cfloat;
+  cfloat *w1 = (cfloat *)a.w1, *w2 = (cfloat *)a.w2, *w3 = (cfloat *)a.w3;
+
+  // s1: thread tid is pixel (y0 + tid / R1, x0 + tid % R1). The kernel
+  // rows of the window rolled (the next row's nine values requested before
+  // this row's sums), each row's products unrolled.
+  {
+    const int Y = y0 + tid / R1, X = x0 + tid % R1;
+    if (Y < a.oh && X < a.ow) {
+      const float *x = a.x + (long)ln * a.x_lane_stride;
+      auto load = [&](int ky, float *v, bool *in) {
+        const int iy = 2 * Y + ky - 1;
+#pragma unroll
+        for (int kx = 0; kx < 3; kx++) {
+          const int ix = 2 * X + kx - 1;
+          in[kx] = iy >= 0 && iy < a.ih && ix >= 0 && ix < a.iw;
+          const float *px = x + ((long)(in[kx] ? iy : 0) * a.iw + (in[kx] ? ix : 0)) * 3;
+#pragma unroll
+          for (int i = 0; i < 3; i++) v[kx * 3 + i] = px[i];
+        }
+      };
+      // A missing bias reads zeros: every sum starts from +0 either way.
+      cfloat *b = (cfloat *)(a.b1 ? a.b1 : kStemNoBias);
+      float acc[C1];
+#pragma unroll
+      for (int j = 0; j < C1; j++) acc[j] = b[j];
+      float cur[9], nxt[9];
+      bool cin[3], nin[3];
+      load(0, cur, cin);
+#pragma unroll 1
+      for (int ky = 0; ky < 3; ky++) {
+        load(ky < 2 ? ky + 1 : ky, nxt, nin);
+#pragma unroll
+        for (int kx = 0; kx < 3; kx++) {
+          if (!cin[kx]) continue;
+#pragma unroll
+          for (int i = 0; i < 3; i++) {
+            cfloat *w = w1 + ((ky * 3 + kx) * 3 + i) * C1;
+#pragma unroll
+            for (int j = 0; j < C1; j++) acc[j] = fmaf(w[j], cur[kx * 3 + i], acc[j]);
+          }
+        }
+#pragma unroll
+        for (int e = 0; e < 9; e++) cur[e] = nxt[e];
+#pragma unroll
+        for (int e = 0; e < 3; e++) cin[e] = nin[e];
+      }
+      f32x4 *o = reinterpret_cast<f32x4 *>(m1 + tid * P1);
+#pragma unroll
+      for (int j = 0; j < C1; j += 4)
+        o[j / 4] = f32x4{act(acc[j], ACT), act(acc[j + 1], ACT), act(acc[j + 2], ACT),
+                         act(acc[j + 3], ACT)};
+    }
+  }
+  __syncthreads();
+
+  // The first 2x2 over (T + 1) x (T + 1) pixels, one a thread.
+  if (tid < R2 * R2) {
+    const int sy = tid / R2, sx = tid % R2, Y = y0 + sy, X = x0 + sx;
+    if (Y < a.oh && X < a.ow) {
+      cfloat *b = (cfloat *)(a.b2 ? a.b2 : kStemNoBias);
+      float bias[C2];
+#pragma unroll
+      for (int j = 0; j < C2; j++) bias[j] = b[j];
+      const bool first = a.b2 && X < a.first_end2, last = a.b2 && !first;
+      float acc[C2];
+#pragma unroll
+      for (int j = 0; j < C2; j++) acc[j] = first ? bias[j] : 0.0f;
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        const int ky = k >> 1, kx = k & 1;
+        if (Y + ky >= a.oh || X + kx >= a.ow) continue;
+        const f32x4 *src = reinterpret_cast<const f32x4 *>(m1 + ((sy + ky) * R1 + sx + kx) * P1);
+#pragma unroll
+        for (int q = 0; q < C1 / 4; q++) {
+          const f32x4 v4 = src[q];
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            cfloat *w = w2 + (k * C1 + q * 4 + e) * C2;
+#pragma unroll
+            for (int j = 0; j < C2; j++) acc[j] = j < F2 ? fmaf(w[j], v4[e], acc[j]) : acc[j] + v4[e] * w[j];
+          }
+        }
+      }
+      float *o = m2 + tid * P2;
+#pragma unroll
+      for (int j = 0; j < C2; j++) o[j] = act(last ? acc[j] + bias[j] : acc[j], ACT);
+    }
+  }
+  // The pool over the tile, one pixel a thread.
+  if (tid < T * T) {
+    const int oy = tid / T, ox = tid % T, Y = y0 + oy, X = x0 + ox;
+    if (Y < a.oh && X < a.ow) {
+      f32x4 *dst = reinterpret_cast<f32x4 *>(a.pool + (long)ln * a.pool_lane_stride + ((long)Y * a.ow + X) * C1);
+#pragma unroll
+      for (int q = 0; q < C1 / 4; q++) {
+        f32x4 m = reinterpret_cast<const f32x4 *>(m1 + (oy * R1 + ox) * P1)[q];
+#pragma unroll
+        for (int k = 1; k < 4; k++) {
+          const int ky = k / 2, kx = k % 2;
+          if (Y + ky >= a.oh || X + kx >= a.ow) continue;
+          const f32x4 v = reinterpret_cast<const f32x4 *>(m1 + ((oy + ky) * R1 + ox + kx) * P1)[q];
+#pragma unroll
+          for (int e = 0; e < 4; e++) m[e] = v[e] > m[e] ? v[e] : m[e];
+        }
+        dst[q] = m;
+      }
+    }
+  }
+  __syncthreads();
+
+  // The second 2x2 over the tile, one pixel a thread.
+  if (tid < T * T) {
+    const int oy = tid / T, ox = tid % T, Y = y0 + oy, X = x0 + ox;
+    if (Y < a.oh && X < a.ow) {
+      cfloat *b = (cfloat *)(a.b3 ? a.b3 : kStemNoBias);
+      float bias[C3];
+#pragma unroll
+      for (int j = 0; j < C3; j++) bias[j] = b[j];
+      const bool first = a.b3 && X < a.first_end3, last = a.b3 && !first;
+      float acc[C3];
+#pragma unroll
+      for (int j = 0; j < C3; j++) acc[j] = first ? bias[j] : 0.0f;
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        const int ky = k >> 1, kx = k & 1;
+        if (Y + ky >= a.oh || X + kx >= a.ow) continue;
+        const f32x4 *src = reinterpret_cast<const f32x4 *>(m2 + ((oy + ky) * R2 + ox + kx) * P2);
+#pragma unroll
+        for (int q = 0; q < C2 / 4; q++) {
+          const f32x4 v4 = src[q];
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            cfloat *w = w3 + (k * C2 + q * 4 + e) * C3;
+#pragma unroll
+            for (int j = 0; j < C3; j++) acc[j] = j < F3 ? fmaf(w[j], v4[e], acc[j]) : acc[j] + v4[e] * w[j];
+          }
+        }
+      }
+      f32x4 *dst = reinterpret_cast<f32x4 *>(a.y + (long)ln * a.y_lane_stride + ((long)Y * a.ow + X) * C3);
+#pragma unroll
+      for (int j = 0; j < C3; j += 4) {
+        float r[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) r[e] = act(last ? acc[j + e] + bias[j + e] : acc[j + e], ACT);
+        dst[j / 4] = f32x4{r[0], r[1], r[2], r[3]};
+      }
+    }
+  }
+}
+
+bool stem_block_supported(int c1, int c2, int c3, int act1, int act2, int act3) {
+  return c1 == 24 && c2 == 12 && c3 == 24 && act1 == act2 && act2 == act3 && (act1 == ACT_HARDSWISH || act1 == ACT_RELU);
+}
+
+hipError_t launch_stem_block(const StemArgs &a, hipStream_t s) {
+  if (!stem_block_supported(a.c1, a.c2, a.c3, a.act1, a.act2, a.act3) || a.ih < 1 || a.iw < 1 || a.lanes < 0)
+    return hipErrorInvalidValue;
+  // s1 is the 3x3 stride-2 pad-1 map of the input; float4 stores.
+  if (a.oh != (a.ih - 1) / 2 + 1 || a.ow != (a.iw - 1) / 2 + 1) return hipErrorInvalidValue;
+  if ((reinterpret_cast<uintptr_t>(a.pool) & 15) || (reinterpret_cast<uintptr_t>(a.y) & 15) ||
+      a.pool_lane_stride % 4 || a.y_lane_stride % 4)
+    return hipErrorInvalidValue;
+  const long tiles = (long)a.lanes * ((a.oh + kStemT - 1) / kStemT) * ((a.ow + kStemT - 1) / kStemT);
+  if (tiles == 0) return hipSuccess;
+  if (tiles > 0x7fffffffL) return hipErrorInvalidValue;
+  if (a.act1 == ACT_RELU)
+    hipLaunchKernelGGL((stem_block<24, 12, 24, ACT_RELU>), dim3((unsigned)tiles), dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL((stem_block<24, 12, 24, ACT_HARDSWISH>), dim3((unsigned)tiles), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
 // Thread = one input pixel (iy, ix) of the first transposed convolution and
 // one of its two output rows ky (blockIdx.y, so the weights a wave reads are
 // uniform). It forms the 2 x OC1 values of intermediate pixels

@@ -415,14 +415,34 @@ __global__ __launch_bounds__(256) void conv_mfma(ConvArgs a) {
 // tap, then runs all taps from there: each input element is fetched, and its
 // source and position decoded, once per block instead of once per tap.
 // Channel blocks are the packed weights' chunks (BK = CB), so the reduction
-// order is channel block, tap, channel; bias, activation, residual and the
-// second activation as in conv_mfma's epilogue. Wave w owns output rows
+// order is channel block, tap, then the block's channels in MFMA steps (r, k)
+// of four, lane group g supplying channel 16r + 4g + k (CB >= 16); bias,
+// activation, residual and the second activation as in conv_mfma's epilogue. Wave w owns output rows
 // w * WR .. w * WR + WR - 1 of the tile, one 16 x 16 MFMA row block each.
 // Registers a thread of conv_patch holds for the next channel block: patch
 // float4s (its channel group of every 256 / (CB / 4)-th pixel) and weight
 // float4s (taps x its column pairs).
 constexpr int kPatchPer = 6;
 constexpr int kWeightPer = 9;
+
+// LDS layout of conv_patch. A ds_read_b128 on gfx950 (measured) serves lanes
+// 32h..32h+31 in two cycles of 16 lanes split by the parity of lane bits
+// 2..4, over 64 banks of 4 bytes; lanes of one cycle that read different
+// addresses in one bank conflict. A fragment read's lane (li, lg) reads pixel
+// (or column) li at channel quad lg + 4r, so one cycle holds each li once,
+// from two lane groups whose quads differ by one. Rows of patch_row floats
+// (a stride of 2 mod 4 quads on stride-1 tiles, odd quads on stride-2 tiles,
+// whose pixels are two rows apart) and columns patch_col_stride floats apart
+// (2 mod 4 quads) put every such read in distinct banks; a store of eight
+// consecutive lanes (one pixel's or one (column, tap)'s eight quads) meets
+// none either.
+__host__ __device__ inline int patch_row(int cb, int stride) {
+  return cb + (cb >= 16 && stride == 1 ? 8 : 4);
+}
+__host__ __device__ inline int patch_col_stride(int taps, int row, int cb) {
+  const int ns = taps * row;
+  return cb >= 16 ? ns + 4 * ((2 - ns / 4) & 3) : ns;
+}
 
 // R8 (BN = 32, 17 to 24 output channels): the second column block holds at
 // most 8 real columns, which run on v_mfma_f32_4x4x1f32 instead of a 16 x 16
@@ -445,7 +465,7 @@ __global__ __launch_bounds__(256) void conv_patch(Group<ConvArgs> grp) {
     if (k < grp.n && bid >= grp.first[k]) prob = k;
   const ConvArgs &a = grp.a[prob];
   const int tiles_x = grp.x[prob], tiles_y = grp.y[prob];
-  constexpr int S = CB + 4;        // LDS row of one pixel / one (n, tap)
+  const int S = patch_row(CB, a.sw);  // LDS row of one pixel / one (n, tap)
   constexpr int KS = CB / 4;       // channels per lane group per tap
   constexpr int KW = KS >= 4 ? 4 : KS;
   constexpr int KR = KS / KW;
@@ -457,7 +477,8 @@ __global__ __launch_bounds__(256) void conv_patch(Group<ConvArgs> grp) {
   const int taps = a.kh * a.kw;
   const int PR = (TH - 1) * a.sh + a.kh, PC = (TW - 1) * a.sw + a.kw;
   float *P = lds;                      // PR * PC pixels x S
-  float *Bs = lds + PR * PC * S;       // nr x taps x S, then one zero row of S
+  float *Bs = lds + PR * PC * S;       // nr columns NS apart (taps x S), then one zero row of S
+  const int NS = patch_col_stride(taps, S, CB);
 
   const int ntn = (a.n + BN - 1) / BN;
   int t = bid - grp.first[prob];
@@ -471,18 +492,23 @@ __global__ __launch_bounds__(256) void conv_patch(Group<ConvArgs> grp) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int li = lane & 15, lg = lane >> 4;
   const int iy0 = ty0 * a.sh - a.pt, ix0 = tx0 * a.sw - a.pl;
-  // Columns of this tile that exist: only their weights are staged; the MFMA
-  // lanes of the others read the zero row.
+  // Columns of this tile that exist: only their weights are staged. The MFMA
+  // lanes of the others only feed output columns that are never stored: past
+  // the first block they read the staged column li (the same banks as the
+  // real lanes of the first block, none of this block's), else the zero row.
   const int nr = min(BN, a.n - n0);
-  float *Z = Bs + nr * taps * S;
+  float *Z = Bs + nr * NS;
   if (tid < S) Z[tid] = 0.0f;
   int bbase[NT], bstep[NT];
 #pragma unroll
   for (int j = 0; j < NT; j++) {
     const int n = j * 16 + li;
-    bbase[j] = n < nr ? n * taps * S : nr * taps * S;
-    bstep[j] = n < nr ? S : 0;
+    const int nn = n < nr ? n : (j > 0 && li < nr ? li : -1);
+    bbase[j] = nn >= 0 ? nn * NS : nr * NS;
+    bstep[j] = nn >= 0 ? S : 0;
   }
+  // The channel offset of lane group g's quad of read r within a pixel row.
+  auto quad = [&](int g, int r) { return KW == 4 ? r * 16 + g * 4 : g * KS + r * KW; };
 
   f32x4 acc[WR][NT];
 #pragma unroll
@@ -497,8 +523,9 @@ __global__ __launch_bounds__(256) void conv_patch(Group<ConvArgs> grp) {
 #pragma unroll
     for (int c = 0; c < 2; c++) {
       const int n = 16 + 4 * c + (lane & 3);
-      rbase[c] = n < nr ? n * taps * S : nr * taps * S;
-      rstep[c] = n < nr ? S : 0;
+      const int nn = n < nr ? n : (n - 16 < nr ? n - 16 : -1);
+      rbase[c] = nn >= 0 ? nn * NS : nr * NS;
+      rstep[c] = nn >= 0 ? S : 0;
 #pragma unroll
       for (int i = 0; i < WR; i++) accr[i][c] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
@@ -562,7 +589,7 @@ __global__ __launch_bounds__(256) void conv_patch(Group<ConvArgs> grp) {
 #pragma unroll
       for (int tp = 0; tp < kWeightPer / PPAIRS; tp++)
         if (pr < PAIRS && n < nr && tp < taps)
-          *reinterpret_cast<f32x4 *>(Bs + (n * taps + tp) * S + qq * 4) = rw[u * (kWeightPer / PPAIRS) + tp];
+          *reinterpret_cast<f32x4 *>(Bs + n * NS + tp * S + qq * 4) = rw[u * (kWeightPer / PPAIRS) + tp];
     }
   };
   fetch(0);
@@ -582,16 +609,16 @@ __global__ __launch_bounds__(256) void conv_patch(Group<ConvArgs> grp) {
         for (int i = 0; i < WR; i++) {
           const int ty = wave * WR + i;
           const int pix = (ty * a.sh + ky) * PC + li * a.sw + kx;
-          av[i] = *reinterpret_cast<const KT *>(P + pix * S + lg * KS + r * KW);
+          av[i] = *reinterpret_cast<const KT *>(P + pix * S + quad(lg, r));
         }
 #pragma unroll
         for (int j = 0; j < NT; j++)
-          bv[j] = *reinterpret_cast<const KT *>(Bs + bbase[j] + tp * bstep[j] + lg * KS + r * KW);
+          bv[j] = *reinterpret_cast<const KT *>(Bs + bbase[j] + tp * bstep[j] + quad(lg, r));
         KT br[R8 ? 2 : 1];
         if constexpr (R8) {
 #pragma unroll
           for (int c = 0; c < NR; c++)
-            br[c] = *reinterpret_cast<const KT *>(Bs + rbase[c] + tp * rstep[c] + lg * KS + r * KW);
+            br[c] = *reinterpret_cast<const KT *>(Bs + rbase[c] + tp * rstep[c] + quad(lg, r));
         }
 #pragma unroll
         for (int k = 0; k < KW; k++) {
@@ -928,8 +955,13 @@ hipError_t launch_ctc_direct(const CtcDirectArgs &a, hipStream_t s) {
 // Tile: BM = 32 * MT rows (pixels) x BN = 32 * NT columns, four waves as a
 // 2 x 2 grid, each 16 * MT x 16 * NT. A stage holds the tile's A rows then
 // its B rows (the packed weights' rows), BK floats each, row-major, with the
-// 16-byte group g of row r stored at slot g ^ ring_swz(r) so that the
-// sixteen rows an MFMA fragment read touches land in distinct banks. A direct
+// 16-byte group g of row r stored at slot g ^ ring_swz(r) so that an MFMA
+// fragment read (ds_read_b128) meets no bank conflict. Measured on gfx950:
+// such a read serves lanes 32h..32h+31 in two cycles of 16 lanes, split by
+// the parity of lane bits 2..4, over 64 banks of 4 bytes; conflicts are
+// counted within a cycle. A fragment read's lane (li, lg) wants row li at
+// group 4r + lg, and one cycle holds each li once, with lg = 2h or 2h + 1
+// as the parity of li's bits 2..3 says. A direct
 // load writes 64 lanes x 16 bytes contiguously from a wave-uniform LDS
 // address, so each lane loads whichever global group belongs at its slot.
 // Rows past the matrix and channels past ctot read kRingZeros. A GEMM of
@@ -949,7 +981,10 @@ constexpr int kRingBK = 32;
 
 template <int BK>
 __device__ __forceinline__ int ring_swz(int row) {
-  if constexpr (BK == 32) return (row & 7) ^ ((row >> 3) & 1);
+  // Two rows of 32 floats span the 64 banks (row & 1 picks the half), so the
+  // slot must differ over the eight rows of one parity in a cycle: row / 2,
+  // flipped in bit 0 where the cycle's lane group does (bits 2 and 3 of row).
+  if constexpr (BK == 32) return ((row >> 1) & 7) ^ (((row >> 2) ^ (row >> 3)) & 1);
   else return row & 15;
 }
 
@@ -1408,7 +1443,8 @@ bool patch_fits(int kh, int kw, int stride, int wr, int bk, int bn) {
   const int pr = (4 * wr - 1) * stride + kh, pc = 15 * stride + kw;
   if ((pr * pc + pstep - 1) / pstep > kPatchPer) return false;
   if (kWeightPer % pairs || kh * kw > kWeightPer / pairs) return false;
-  return size_t(pr * pc + bn * kh * kw + 1) * (bk + 4) * sizeof(float) <= 160 * 1024;
+  const int row = patch_row(bk, stride);
+  return (size_t(pr * pc + 1) * row + size_t(bn) * patch_col_stride(kh * kw, row, bk)) * sizeof(float) <= 160 * 1024;
 }
 
 bool patch_supported(const ConvArgs &a, int wr, int bk, int bn) {
@@ -1421,7 +1457,8 @@ bool patch_supported(const ConvArgs &a, int wr, int bk, int bn) {
 size_t patch_lds_bytes(const ConvArgs &a, int wr, int bk, int bn) {
   const size_t pr = size_t(4 * wr - 1) * a.sh + a.kh, pc = size_t(15) * a.sw + a.kw;
   const size_t nr = size_t(std::min(bn, a.n));  // staged columns; the zero row besides
-  return (pr * pc + nr * a.kh * a.kw + 1) * (bk + 4) * sizeof(float);
+  const int row = patch_row(bk, a.sw);
+  return ((pr * pc + 1) * row + nr * patch_col_stride(a.kh * a.kw, row, bk)) * sizeof(float);
 }
 
 template <int WR, int BN, int CB, bool R8 = false>

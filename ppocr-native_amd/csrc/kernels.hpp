@@ -445,6 +445,27 @@ bool direct_supported(int kh, int kw, int ic);
 bool direct_pix_supported(int kh, int kw, int ic, int oc);
 hipError_t launch_conv_direct(const DirectArgs &a, hipStream_t s);
 
+// The detector's stem block in one pass: s1 = 3x3 stride-2 convolution of
+// the RGB input (pad 1, 3 -> C1, the stem rule), then from s1 both a 2x2
+// stride-1 max pool cut at the bottom and right edges (`pool`) and two 2x2
+// stride-1 convolutions padded right and bottom, C1 -> C2 -> C3 (`y`). The
+// s1 map and the first 2x2's map stay in LDS. The input is ih x iw; s1 is
+// oh x ow, as are both outputs; first_end2/3: pixels left of it take the
+// bias first.
+struct StemArgs {
+  int lanes, ih, iw, oh, ow, c1, c2, c3;
+  const float *x; long x_lane_stride;
+  const float *w1, *b1; int act1;
+  const float *w2, *b2; int act2, first_end2;
+  const float *w3, *b3; int act3, first_end3;
+  float *pool; long pool_lane_stride;
+  float *y; long y_lane_stride;
+};
+// The stem block's kernels: C1 24, C2 12, C3 24, one activation, ReLU or
+// hard swish, for all three layers.
+bool stem_block_supported(int c1, int c2, int c3, int act1, int act2, int act3);
+hipError_t launch_stem_block(const StemArgs &a, hipStream_t s);
+
 // Two 2x2 stride-2 transposed convolutions in a row: ic -> oc1 (act1), then
 // oc1 -> 1 (act2); y is the final map, (4 ih) x (4 iw).
 struct HeadArgs {

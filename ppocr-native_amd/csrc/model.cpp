@@ -65,6 +65,8 @@ size_t round_up(size_t v, size_t m) { return (v + m - 1) / m * m; }
 
 enum StepKind {
   S_GEMM, S_DW, S_ELT, S_POOL, S_MEAN, S_LN, S_ATTN, S_CTC, S_CONVT, S_DIRECT, S_HEAD,
+  // The detector's stem block: RGB stem, its 2x2 max pool and two 2x2 layers.
+  S_STEM,
   // The transformer encoder's fused steps: LayerNorm -> 1x1 (enc_linear),
   // attention -> 1x1 -> Add (enc_attn_block), LayerNorm -> 1x1 -> 1x1 -> Add
   // [-> LayerNorm] (enc_mlp), and the last two as one (enc_attn_block).
@@ -86,6 +88,7 @@ struct Step {
   int ln_out = -1;         // S_ENC_MLP, S_ENC_BLOCK: the LayerNorm of its sum, written in its place
   int m_ln = -1, m_fc1 = -1, m_fc2 = -1, m_add = -1;  // S_ENC_BLOCK: its MLP's operations
   int head2 = -1;          // the narrow transposed convolution folded into S_HEAD
+  int st2 = -1, st3 = -1, st_pool = -1;  // S_STEM: the two 2x2 layers and the pool
   bool dw_sums = false;    // S_DW: also sum its output per channel for the next step's mean
   bool patch = false;      // S_GEMM: a windowed convolution on halo tiles (conv_patch)
   bool ring = false;       // S_GEMM: a windowed convolution on the LDS ring (conv_ring)
@@ -200,6 +203,8 @@ struct Model {
   std::vector<size_t> step_reads(const Step &s) const;
   int enc_hidden(const Step &s) const { return s.kind == S_ENC_BLOCK ? int(plan.ops[s.m_fc1].oc) : 0; }
   size_t step_writes(const Step &s) const;
+  // A second output of the step (S_STEM's pool), else SIZE_MAX.
+  size_t step_writes2(const Step &s) const { return s.kind == S_STEM ? plan.ops[s.st_pool].y : SIZE_MAX; }
 };
 
 Model::~Model() {
@@ -262,6 +267,7 @@ std::vector<size_t> Model::step_reads(const Step &s) const {
 
 size_t Model::step_writes(const Step &s) const {
   if (s.kind == S_HEAD) return plan.ops[s.head2].y;
+  if (s.kind == S_STEM) return plan.ops[s.st3].y;
   if (s.kind == S_MEAN && s.fc2 >= 0) return plan.ops[s.fc2].y;
   if ((s.kind == S_ENC_MLP || s.kind == S_ENC_BLOCK) && s.ln_out >= 0) return plan.ops[s.ln_out].y;
   if (s.kind == S_ENC_BLOCK) return plan.ops[s.m_add].y;
@@ -378,6 +384,37 @@ bool Model::build_steps(std::string &err) {
     return k < n && ops[k].kind == K_ADD && readers[from] == 1 && ((ops[k].x == from) != (ops[k].x2 == from));
   };
 
+  // Operation i as the stem block's RGB stem: q = its two 2x2 layers (a
+  // 2x2 stride-1 convolution padded right and bottom by one) and its pool.
+  auto stem_block_at = [&](size_t i, int q[3]) {
+    const Op &s1 = ops[i];
+    if (!(s1.kh == 3 && s1.kw == 3 && s1.sh == 2 && s1.sw == 2 && s1.pt == 1 && s1.pl == 1 && s1.ic == 3 &&
+          s1.n2 == 0 && readers[s1.y] == 2))
+      return false;
+    auto pad2x2 = [&](const Op &o, size_t from) {
+      return o.kind == K_CONV && o.x == from && o.n2 == 0 && o.kh == 2 && o.kw == 2 && o.sh == 1 && o.sw == 1 &&
+             o.pt == 0 && o.pl == 0 && o.oh == o.ih && o.ow == o.iw;
+    };
+    int c2 = -1, c3 = -1, pool = -1;
+    for (size_t j = i + 1; j < n; j++) {
+      const Op &o = ops[j];
+      if (o.x == s1.y && pad2x2(o, s1.y)) c2 = int(j);
+      if (o.x == s1.y && o.kind == K_MAXPOOL && o.kh == 2 && o.kw == 2 && o.sh == 1 && o.sw == 1 &&
+          o.oh == o.ih && o.ow == o.iw)
+        pool = int(j);
+      if (c2 >= 0 && c3 < 0 && pad2x2(o, ops[size_t(c2)].y)) c3 = int(j);
+    }
+    if (c2 < 0 || c3 < 0 || pool < 0 || readers[ops[size_t(c2)].y] != 1) return false;
+    const Op &o2 = ops[size_t(c2)], &o3 = ops[size_t(c3)];
+    // An Add after the second 2x2 that only it feeds would fold into it.
+    if (readers[o3.y] == 1 && size_t(c3) + 1 < n && ops[size_t(c3) + 1].kind == K_ADD &&
+        (ops[size_t(c3) + 1].x == o3.y || ops[size_t(c3) + 1].x2 == o3.y))
+      return false;
+    if (!stem_block_supported(int(s1.oc), int(o2.oc), int(o3.oc), s1.fused, o2.fused, o3.fused)) return false;
+    q[0] = c2, q[1] = c3, q[2] = pool;
+    return true;
+  };
+
   std::vector<bool> folded(n, false);
   std::vector<int> inside;
   steps.clear();
@@ -447,6 +484,17 @@ bool Model::build_steps(std::string &err) {
             ((op.ic % 4 != 0 && direct_supported(int(op.kh), int(op.kw), int(op.ic))) ||
              direct_pix_supported(int(op.kh), int(op.kw), int(op.ic), int(op.oc))))
           s.kind = S_DIRECT;
+        // The stem block: a 3x3 stride-2 RGB stem whose map only a 2x2 max
+        // pool and a 2x2 layer read, that layer's map only a second 2x2
+        // layer: one step, neither map stored.
+        if (s.kind == S_DIRECT) {
+          int q[3];
+          if (stem_block_at(i, q)) {
+            s.kind = S_STEM;
+            s.st2 = q[0], s.st3 = q[1], s.st_pool = q[2];
+            for (int k : q) folded[size_t(k)] = true;
+          }
+        }
         break;
       }
       case K_DWCONV: s.kind = S_DW; break;
@@ -816,6 +864,7 @@ bool Model::arrange(Batch &b, std::string &err) {
   std::vector<std::vector<size_t>> slot_readers(p.pool.size());
   for (size_t i = 0; i < n; i++) {
     producer[step_writes(steps[i])] = i;
+    if (step_writes2(steps[i]) != SIZE_MAX) producer[step_writes2(steps[i])] = i;
     for (size_t sl : step_reads(steps[i])) slot_readers[sl].push_back(i);
   }
   std::vector<std::vector<bool>> anc(n, std::vector<bool>(n, false));
@@ -860,6 +909,8 @@ bool Model::arrange(Batch &b, std::string &err) {
   for (size_t i = 0; i < n; i++) {
     size_t y = step_writes(steps[i]);
     b.home[y] = place(p.pool[y], i);
+    const size_t y2 = step_writes2(steps[i]);
+    if (y2 != SIZE_MAX) b.home[y2] = place(p.pool[y2], i);
     for (size_t sl : step_reads(steps[i]))
       if (last[sl] == i && std::find(freel.begin(), freel.end(), b.home[sl]) == freel.end()) {
         freel.push_back(b.home[sl]);
@@ -1284,6 +1335,25 @@ void Model::build_launches(Batch &b) {
         b.launches.push_back({"conv_direct", s.op, [a](hipStream_t st) { return launch_conv_direct(a, st); }});
         break;
       }
+      case S_STEM: {
+        const Op &o2 = p.ops[s.st2], &o3 = p.ops[s.st3], &pl = p.ops[s.st_pool];
+        StemArgs a{};
+        a.lanes = L;
+        a.ih = int(op.ih), a.iw = int(op.iw), a.oh = int(op.oh), a.ow = int(op.ow);
+        a.c1 = int(op.oc), a.c2 = int(o2.oc), a.c3 = int(o3.oc);
+        a.x = b.dev(op.x), a.x_lane_stride = b.stride(op.x);
+        a.w1 = W + op.w0, a.b1 = bias, a.act1 = op.fused;
+        // kernels/dense.rs:38-147: a multiple-of-16 width starts from the
+        // bias except for the row's last ow % 4 pixels, else adds it last.
+        a.w2 = W + o2.w0, a.b2 = o2.b1 ? W + o2.b0 : nullptr, a.act2 = o2.fused;
+        a.first_end2 = o2.oc % 16 == 0 ? a.ow - a.ow % 4 : 0;
+        a.w3 = W + o3.w0, a.b3 = o3.b1 ? W + o3.b0 : nullptr, a.act3 = o3.fused;
+        a.first_end3 = o3.oc % 16 == 0 ? a.ow - a.ow % 4 : 0;
+        a.pool = b.dev(pl.y), a.pool_lane_stride = b.stride(pl.y);
+        a.y = Y, a.y_lane_stride = ys;
+        b.launches.push_back({"stem_block", s.op, [a](hipStream_t st) { return launch_stem_block(a, st); }});
+        break;
+      }
       case S_HEAD: {
         const Op &o2 = p.ops[s.head2];
         HeadArgs a{};
@@ -1318,6 +1388,7 @@ void Model::link(Batch &b) const {
     std::vector<size_t> rd, wr;
     for (size_t slot : step_reads(s)) rd.push_back(b.home[slot]);
     wr.push_back(b.home[step_writes(s)]);
+    if (step_writes2(s) != SIZE_MAX) wr.push_back(b.home[step_writes2(s)]);
     const size_t ws = H + size_t(l.step);
     if (s.kind == S_MEAN || s.kind == S_CTC || s.kind == S_ATTN || s.kind == S_ENC_ATTN || s.kind == S_ENC_BLOCK)
       rd.push_back(ws), wr.push_back(ws);
@@ -1628,6 +1699,14 @@ void Model::account(Batch &b) const {
         l.flops = 2.0 * L * out_px * op.oc * op.kh * op.kw * op.ic;
         l.bytes = F * (L * in_px * op.ic + L * out_px * op.oc + op.w1 + op.b1);
         break;
+      case S_STEM: {
+        // Each layer's products; the input read and both outputs written once.
+        const Op &o2 = p.ops[s.st2], &o3 = p.ops[s.st3];
+        l.flops = 2.0 * L * out_px * (op.oc * 27.0 + 4.0 * o2.ic * o2.oc + 4.0 * o3.ic * o3.oc);
+        l.bytes = F * (L * in_px * op.ic + L * out_px * (op.oc + o3.oc) + op.w1 + op.b1 + o2.w1 + o2.b1 +
+                       o3.w1 + o3.b1);
+        break;
+      }
       case S_HEAD: {
         const Op &o2 = p.ops[s.head2];
         const double mid_px = out_px, fin_px = double(o2.oh) * o2.ow;

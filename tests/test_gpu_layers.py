@@ -377,6 +377,36 @@ def test_direct_conv_exact(oracle, ci, co, k, s, pad, hw):
     exact(got, want)
 
 
+@pytest.mark.parametrize("hw,biased,lanes", [
+    ((19, 30), True, 3),     # one 14 x 14 tile of the 10 x 15 maps, cut at both edges
+    ((64, 70), True, 3),     # 32 x 35: whole and partial tiles
+    ((61, 97), False, 2),    # odd input sides; no biases (every sum from zero)
+    ((480, 452), True, 1),   # 240 x 226: many tiles, the last row and column partial
+])
+def test_stem_block_exact(oracle, hw, biased, lanes):
+    # The RGB stem, its 2x2 max pool and two 2x2 layers padded right and
+    # bottom: one fused step whose s1 and first 2x2 maps stay on chip.
+    rng = np.random.default_rng(7)
+    w1 = rng.normal(0, 0.3, (3, 3, 3, 24)).astype(np.float32)
+    w2 = rng.normal(0, 0.3, (2, 2, 24, 12)).astype(np.float32)
+    w3 = rng.normal(0, 0.3, (2, 2, 12, 24)).astype(np.float32)
+    bs = [rng.normal(0, 0.3, c).astype(np.float32) if biased else None for c in (24, 12, 24)]
+
+    def build(b, t):
+        s1 = b.conv(t, w1, bs[0], k=(3, 3), s=(2, 2), pad=(1, 1, 1, 1), fused="hardswish")
+        s2 = b.conv(s1, w2, bs[1], k=(2, 2), pad=(0, 1, 0, 1), fused="hardswish")
+        s3 = b.conv(s2, w3, bs[2], k=(2, 2), pad=(0, 1, 0, 1), fused="hardswish")
+        return [b.maxpool(s1), s3]
+
+    h, w = hw
+    b = PlanBuilder(h, w, 3)
+    g = GpuModel.load(b.to_bytes(build(b, b.input)))
+    assert "stem_block" in [name for name, _ in g.launches()]
+    g.close()
+    got, want = both(build, (h, w, 3), oracle, lanes=lanes)
+    exact(got, want)
+
+
 @pytest.mark.parametrize("oc1,hw", [(24, (9, 13)), (16, (6, 8))])
 def test_db_head_exact(oracle, oc1, hw):
     # A wide 2x2 transposed conv read only by a narrow one: one fused step.
