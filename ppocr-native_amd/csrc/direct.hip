@@ -328,15 +328,14 @@ hipError_t launch_conv_direct(const DirectArgs &a, hipStream_t s) {
 // over the tile plus two rows and columns (what the pool and the 2x2 layers
 // read), the first 2x2 over the tile plus one row and column, then the max
 // pool and the second 2x2 over the tile; s1 and the first 2x2's output never
-// leave LDS. Each layer in the CPU engine's order: s1 from its bias, taps
-// [ky][kx] skipping those outside the input, channels in order, every column
-// a fused multiply-add (the stem rule, src/engine/conv.rs:146-236); a 2x2
-// from its bias for pixels left of first_end, else adding it last, taps
-// outside the map skipped, columns below C / 8 * 8 fused and the rest a
-// separate multiply and add (kernels/dense.rs:38-147); the pool seeded with
-// its first tap, a later tap inside the map kept only when greater
-// (conv.rs:404-440). The weights are wave-uniform reads, served by the
-// scalar cache into scalar operands, so LDS holds only the two maps.
+// leave LDS. s1 and the pool in the CPU engine's order, bit for bit: s1 from
+// its bias, taps [ky][kx] skipping those outside the input, channels in
+// order, every column a fused multiply-add (the stem rule,
+// src/engine/conv.rs:146-236), its weights wave-uniform scalar operands
+// (the scalar cache); the pool seeded with its first tap, a later tap inside
+// the map kept only when greater (conv.rs:404-440). The two 2x2 layers run
+// on FP32 MFMA (sums in another order, within the MFMA tolerance), bias and
+// activation after the products.
 constexpr int kStemT = 14;
 // The bias of a layer that has none: its sums start from, or add, nothing.
 __device__ __attribute__((aligned(16))) float kStemNoBias[32];
@@ -349,7 +348,6 @@ __global__ __launch_bounds__(256) void stem_block(StemArgs a) {
   // Pixels an odd number of float4s apart: a wave's float4 reads of
   // consecutive pixels fall in distinct banks.
   constexpr int P1 = (C1 / 4) % 2 ? C1 : C1 + 4, P2 = (C2 / 4) % 2 ? C2 : C2 + 4;
-  constexpr int F2 = C2 / 8 * 8, F3 = C3 / 8 * 8;
   static_assert(R1 * R1 == 256, "one s1 pixel per thread");
   static_assert(C1 % 8 == 0 && C2 % 4 == 0 && C3 % 4 == 0, "float4 channels, every stem column fused");
   __shared__ __attribute__((aligned(16))) float m1[R1 * R1 * P1];
@@ -365,7 +363,33 @@ __global__ __launch_bounds__(256) void stem_block(StemArgs a) {
   const int y0 = ty * T, x0 = tx * T, tid = threadIdx.x;
   // Read through the constant address space: wave-uniform scalar loads.
   typedef const __attribute__((address_space(4))) float cfloat;
-  cfloat *w1 = (cfloat *)a.w1, *w2 = (cfloat *)a.w2, *w3 = (cfloat *)a.w3;
+  cfloat *w1 = (cfloat *)a.w1;
+  // The 2x2 layers on FP32 MFMA (v_mfma_f32_16x16x4f32): rows are the
+  // map's pixels in row-major order of the region, 16 a row block, the
+  // reduction index k = tap * C + channel, taps [ky][kx]. Lane (li, lg)
+  // holds a row block's A at row li, k = 16s + 4lg + e (e = 0..3 in the four
+  // MFMAs of step s: one float4 read from LDS), and B at column li for the
+  // same k. Both layers' B (and biases) are requested first, so that their
+  // loads run beside s1. A tap outside the map reads zeros.
+  const int lane = tid & 63, wave = tid >> 6, li = lane & 15, lg = lane >> 4;
+  constexpr int S2 = 4 * C1 / 16, S3 = 4 * C2 / 16, NB3 = (C3 + 15) / 16;
+  static_assert(C2 <= 16 && 4 * C1 % 16 == 0 && 4 * C2 % 16 == 0, "one column block; whole steps");
+  f32x4 bw2[S2], bw3[NB3][S3];
+#pragma unroll
+  for (int q = 0; q < S2; q++)
+#pragma unroll
+    for (int e = 0; e < 4; e++) bw2[q][e] = li < C2 ? a.w2[(16 * q + 4 * lg + e) * C2 + li] : 0.0f;
+  const float bias2 = a.b2 && li < C2 ? a.b2[li] : 0.0f;
+  float bias3[NB3];
+#pragma unroll
+  for (int c = 0; c < NB3; c++) {
+    const int n = 16 * c + li;
+#pragma unroll
+    for (int q = 0; q < S3; q++)
+#pragma unroll
+      for (int e = 0; e < 4; e++) bw3[c][q][e] = n < C3 ? a.w3[(16 * q + 4 * lg + e) * C3 + n] : 0.0f;
+    bias3[c] = a.b3 && n < C3 ? a.b3[n] : 0.0f;
+  }
 
   // s1: thread tid is pixel (y0 + tid / R1, x0 + tid % R1). The kernel
   // rows of the window rolled (the next row's nine values requested before
@@ -420,37 +444,28 @@ __global__ __launch_bounds__(256) void stem_block(StemArgs a) {
   }
   __syncthreads();
 
-  // The first 2x2 over (T + 1) x (T + 1) pixels, one a thread.
-  if (tid < R2 * R2) {
-    const int sy = tid / R2, sx = tid % R2, Y = y0 + sy, X = x0 + sx;
-    if (Y < a.oh && X < a.ow) {
-      cfloat *b = (cfloat *)(a.b2 ? a.b2 : kStemNoBias);
-      float bias[C2];
+  // The first 2x2 over (T + 1) x (T + 1) pixels.
+  {
+    constexpr int M = R2 * R2, MB = (M + 15) / 16, S = S2;
+    for (int b = wave; b < MB; b += 4) {
+      const int m = b * 16 + li, sy = m / R2, sx = m - sy * R2;
+      const bool live = m < M && y0 + sy < a.oh && x0 + sx < a.ow;
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int j = 0; j < C2; j++) bias[j] = b[j];
-      const bool first = a.b2 && X < a.first_end2, last = a.b2 && !first;
-      float acc[C2];
+      for (int q = 0; q < S; q++) {
+        const int k = 16 * q + 4 * lg, tap = k / C1, ch = k - tap * C1, ky = tap >> 1, kx = tap & 1;
+        f32x4 v = {0.f, 0.f, 0.f, 0.f};
+        if (live && y0 + sy + ky < a.oh && x0 + sx + kx < a.ow)
+          v = *reinterpret_cast<const f32x4 *>(m1 + ((sy + ky) * R1 + sx + kx) * P1 + ch);
 #pragma unroll
-      for (int j = 0; j < C2; j++) acc[j] = first ? bias[j] : 0.0f;
-#pragma unroll
-      for (int k = 0; k < 4; k++) {
-        const int ky = k >> 1, kx = k & 1;
-        if (Y + ky >= a.oh || X + kx >= a.ow) continue;
-        const f32x4 *src = reinterpret_cast<const f32x4 *>(m1 + ((sy + ky) * R1 + sx + kx) * P1);
-#pragma unroll
-        for (int q = 0; q < C1 / 4; q++) {
-          const f32x4 v4 = src[q];
-#pragma unroll
-          for (int e = 0; e < 4; e++) {
-            cfloat *w = w2 + (k * C1 + q * 4 + e) * C2;
-#pragma unroll
-            for (int j = 0; j < C2; j++) acc[j] = j < F2 ? fmaf(w[j], v4[e], acc[j]) : acc[j] + v4[e] * w[j];
-          }
-        }
+        for (int e = 0; e < 4; e++) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(v[e], bw2[q][e], acc, 0, 0, 0);
       }
-      float *o = m2 + tid * P2;
+      // acc[r]: row 4 lg + r of the block, column li.
 #pragma unroll
-      for (int j = 0; j < C2; j++) o[j] = act(last ? acc[j] + bias[j] : acc[j], ACT);
+      for (int r = 0; r < 4; r++) {
+        const int mo = b * 16 + 4 * lg + r;
+        if (mo < M && li < C2) m2[mo * P2 + li] = act(acc[r] + bias2, ACT);
+      }
     }
   }
   // The pool over the tile, one pixel a thread.
@@ -475,43 +490,45 @@ __global__ __launch_bounds__(256) void stem_block(StemArgs a) {
   }
   __syncthreads();
 
-  // The second 2x2 over the tile, one pixel a thread.
-  if (tid < T * T) {
-    const int oy = tid / T, ox = tid % T, Y = y0 + oy, X = x0 + ox;
-    if (Y < a.oh && X < a.ow) {
-      cfloat *b = (cfloat *)(a.b3 ? a.b3 : kStemNoBias);
-      float bias[C3];
+  // The second 2x2 over the tile, its outputs staged in LDS over s1 (no
+  // longer read), then stored as whole pixel rows.
+  float *st = m1;
+  {
+    constexpr int M = T * T, MB = (M + 15) / 16, S = S3, NB = NB3;
+    static_assert(M * C3 <= R1 * R1 * P1, "staging fits");
+    for (int b = wave; b < MB; b += 4) {
+      const int m = b * 16 + li, oy = m / T, ox = m - oy * T;
+      const bool live = m < M && y0 + oy < a.oh && x0 + ox < a.ow;
+      f32x4 acc[NB];
 #pragma unroll
-      for (int j = 0; j < C3; j++) bias[j] = b[j];
-      const bool first = a.b3 && X < a.first_end3, last = a.b3 && !first;
-      float acc[C3];
+      for (int c = 0; c < NB; c++) acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int j = 0; j < C3; j++) acc[j] = first ? bias[j] : 0.0f;
+      for (int q = 0; q < S; q++) {
+        const int k = 16 * q + 4 * lg, tap = k / C2, ch = k - tap * C2, ky = tap >> 1, kx = tap & 1;
+        f32x4 v = {0.f, 0.f, 0.f, 0.f};
+        if (live && y0 + oy + ky < a.oh && x0 + ox + kx < a.ow)
+          v = *reinterpret_cast<const f32x4 *>(m2 + ((oy + ky) * R2 + ox + kx) * P2 + ch);
 #pragma unroll
-      for (int k = 0; k < 4; k++) {
-        const int ky = k >> 1, kx = k & 1;
-        if (Y + ky >= a.oh || X + kx >= a.ow) continue;
-        const f32x4 *src = reinterpret_cast<const f32x4 *>(m2 + ((oy + ky) * R2 + ox + kx) * P2);
+        for (int e = 0; e < 4; e++)
 #pragma unroll
-        for (int q = 0; q < C2 / 4; q++) {
-          const f32x4 v4 = src[q];
+          for (int c = 0; c < NB; c++) acc[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(v[e], bw3[c][q][e], acc[c], 0, 0, 0);
+      }
 #pragma unroll
-          for (int e = 0; e < 4; e++) {
-            cfloat *w = w3 + (k * C2 + q * 4 + e) * C3;
+      for (int c = 0; c < NB; c++)
 #pragma unroll
-            for (int j = 0; j < C3; j++) acc[j] = j < F3 ? fmaf(w[j], v4[e], acc[j]) : acc[j] + v4[e] * w[j];
-          }
+        for (int r = 0; r < 4; r++) {
+          const int mo = b * 16 + 4 * lg + r, n = 16 * c + li;
+          if (mo < M && n < C3) st[mo * C3 + n] = act(acc[c][r] + bias3[c], ACT);
         }
-      }
-      f32x4 *dst = reinterpret_cast<f32x4 *>(a.y + (long)ln * a.y_lane_stride + ((long)Y * a.ow + X) * C3);
-#pragma unroll
-      for (int j = 0; j < C3; j += 4) {
-        float r[4];
-#pragma unroll
-        for (int e = 0; e < 4; e++) r[e] = act(last ? acc[j + e] + bias[j + e] : acc[j + e], ACT);
-        dst[j / 4] = f32x4{r[0], r[1], r[2], r[3]};
-      }
     }
+  }
+  __syncthreads();
+  // Copy-out: each valid pixel's C3 outputs as C3 / 4 float4 stores.
+  for (int e = tid; e < T * T * (C3 / 4); e += 256) {
+    const int m = e / (C3 / 4), q = e - m * (C3 / 4), oy = m / T, ox = m - oy * T, Y = y0 + oy, X = x0 + ox;
+    if (Y < a.oh && X < a.ow)
+      reinterpret_cast<f32x4 *>(a.y + (long)ln * a.y_lane_stride + ((long)Y * a.ow + X) * C3)[q] =
+          reinterpret_cast<const f32x4 *>(st + m * C3)[q];
   }
 }
 

@@ -383,9 +383,11 @@ def test_direct_conv_exact(oracle, ci, co, k, s, pad, hw):
     ((61, 97), False, 2),    # odd input sides; no biases (every sum from zero)
     ((480, 452), True, 1),   # 240 x 226: many tiles, the last row and column partial
 ])
-def test_stem_block_exact(oracle, hw, biased, lanes):
+def test_stem_block(oracle, hw, biased, lanes):
     # The RGB stem, its 2x2 max pool and two 2x2 layers padded right and
-    # bottom: one fused step whose s1 and first 2x2 maps stay on chip.
+    # bottom: one fused step whose s1 and first 2x2 maps stay on chip. The
+    # pool (of s1, which keeps the engine's order) bit-exact; the 2x2 layers
+    # run on MFMA: within the MFMA tolerance.
     rng = np.random.default_rng(7)
     w1 = rng.normal(0, 0.3, (3, 3, 3, 24)).astype(np.float32)
     w2 = rng.normal(0, 0.3, (2, 2, 24, 12)).astype(np.float32)
@@ -404,7 +406,8 @@ def test_stem_block_exact(oracle, hw, biased, lanes):
     assert "stem_block" in [name for name, _ in g.launches()]
     g.close()
     got, want = both(build, (h, w, 3), oracle, lanes=lanes)
-    exact(got, want)
+    exact([[g[0]] for g in got], [[w_[0]] for w_ in want])
+    near([[g[1]] for g in got], [[w_[1]] for w_ in want])
 
 
 @pytest.mark.parametrize("oc1,hw", [(24, (9, 13)), (16, (6, 8))])
