@@ -369,8 +369,9 @@ __global__ __launch_bounds__(256) void stem_block(StemArgs a) {
   // reduction index k = tap * C + channel, taps [ky][kx]. Lane (li, lg)
   // holds a row block's A at row li, k = 16s + 4lg + e (e = 0..3 in the four
   // MFMAs of step s: one float4 read from LDS), and B at column li for the
-  // same k. Both layers' B (and biases) are requested first, so that their
-  // loads run beside s1. A tap outside the map reads zeros.
+  // same k. The first layer's B (and bias) is requested before s1, the
+  // second's after it, each well before its use. A tap outside the map
+  // reads zeros.
   const int lane = tid & 63, wave = tid >> 6, li = lane & 15, lg = lane >> 4;
   constexpr int S2 = 4 * C1 / 16, S3 = 4 * C2 / 16, NB3 = (C3 + 15) / 16;
   static_assert(C2 <= 16 && 4 * C1 % 16 == 0 && 4 * C2 % 16 == 0, "one column block; whole steps");
@@ -381,6 +382,46 @@ __global__ __launch_bounds__(256) void stem_block(StemArgs a) {
     for (int e = 0; e < 4; e++) bw2[q][e] = li < C2 ? a.w2[(16 * q + 4 * lg + e) * C2 + li] : 0.0f;
   const float bias2 = a.b2 && li < C2 ? a.b2[li] : 0.0f;
   float bias3[NB3];
+
+  // s1: thread tid is pixel (y0 + tid / R1, x0 + tid % R1). All 27 input
+  // values are requested before the first product (their latency, from
+  // memory not yet cached, is the phase's longest wait).
+  {
+    const int Y = y0 + tid / R1, X = x0 + tid % R1;
+    if (Y < a.oh && X < a.ow) {
+      const float *x = a.x + (long)ln * a.x_lane_stride;
+      float v[27];
+      bool in[9];
+#pragma unroll
+      for (int k = 0; k < 9; k++) {
+        const int iy = 2 * Y + k / 3 - 1, ix = 2 * X + k % 3 - 1;
+        in[k] = iy >= 0 && iy < a.ih && ix >= 0 && ix < a.iw;
+        const float *px = x + ((long)(in[k] ? iy : 0) * a.iw + (in[k] ? ix : 0)) * 3;
+#pragma unroll
+        for (int i = 0; i < 3; i++) v[k * 3 + i] = px[i];
+      }
+      // A missing bias reads zeros: every sum starts from +0 either way.
+      cfloat *b = (cfloat *)(a.b1 ? a.b1 : kStemNoBias);
+      float acc[C1];
+#pragma unroll
+      for (int j = 0; j < C1; j++) acc[j] = b[j];
+#pragma unroll
+      for (int k = 0; k < 9; k++) {
+        if (!in[k]) continue;
+#pragma unroll
+        for (int i = 0; i < 3; i++) {
+          cfloat *w = w1 + (k * 3 + i) * C1;
+#pragma unroll
+          for (int j = 0; j < C1; j++) acc[j] = fmaf(w[j], v[k * 3 + i], acc[j]);
+        }
+      }
+      f32x4 *o = reinterpret_cast<f32x4 *>(m1 + tid * P1);
+#pragma unroll
+      for (int j = 0; j < C1; j += 4)
+        o[j / 4] = f32x4{act(acc[j], ACT), act(acc[j + 1], ACT), act(acc[j + 2], ACT),
+                         act(acc[j + 3], ACT)};
+    }
+  }
 #pragma unroll
   for (int c = 0; c < NB3; c++) {
     const int n = 16 * c + li;
@@ -390,82 +431,45 @@ __global__ __launch_bounds__(256) void stem_block(StemArgs a) {
       for (int e = 0; e < 4; e++) bw3[c][q][e] = n < C3 ? a.w3[(16 * q + 4 * lg + e) * C3 + n] : 0.0f;
     bias3[c] = a.b3 && n < C3 ? a.b3[n] : 0.0f;
   }
-
-  // s1: thread tid is pixel (y0 + tid / R1, x0 + tid % R1). The kernel
-  // rows of the window rolled (the next row's nine values requested before
-  // this row's sums), each row's products unrolled.
-  {
-    const int Y = y0 + tid / R1, X = x0 + tid % R1;
-    if (Y < a.oh && X < a.ow) {
-      const float *x = a.x + (long)ln * a.x_lane_stride;
-      auto load = [&](int ky, float *v, bool *in) {
-        const int iy = 2 * Y + ky - 1;
-#pragma unroll
-        for (int kx = 0; kx < 3; kx++) {
-          const int ix = 2 * X + kx - 1;
-          in[kx] = iy >= 0 && iy < a.ih && ix >= 0 && ix < a.iw;
-          const float *px = x + ((long)(in[kx] ? iy : 0) * a.iw + (in[kx] ? ix : 0)) * 3;
-#pragma unroll
-          for (int i = 0; i < 3; i++) v[kx * 3 + i] = px[i];
-        }
-      };
-      // A missing bias reads zeros: every sum starts from +0 either way.
-      cfloat *b = (cfloat *)(a.b1 ? a.b1 : kStemNoBias);
-      float acc[C1];
-#pragma unroll
-      for (int j = 0; j < C1; j++) acc[j] = b[j];
-      float cur[9], nxt[9];
-      bool cin[3], nin[3];
-      load(0, cur, cin);
-#pragma unroll 1
-      for (int ky = 0; ky < 3; ky++) {
-        load(ky < 2 ? ky + 1 : ky, nxt, nin);
-#pragma unroll
-        for (int kx = 0; kx < 3; kx++) {
-          if (!cin[kx]) continue;
-#pragma unroll
-          for (int i = 0; i < 3; i++) {
-            cfloat *w = w1 + ((ky * 3 + kx) * 3 + i) * C1;
-#pragma unroll
-            for (int j = 0; j < C1; j++) acc[j] = fmaf(w[j], cur[kx * 3 + i], acc[j]);
-          }
-        }
-#pragma unroll
-        for (int e = 0; e < 9; e++) cur[e] = nxt[e];
-#pragma unroll
-        for (int e = 0; e < 3; e++) cin[e] = nin[e];
-      }
-      f32x4 *o = reinterpret_cast<f32x4 *>(m1 + tid * P1);
-#pragma unroll
-      for (int j = 0; j < C1; j += 4)
-        o[j / 4] = f32x4{act(acc[j], ACT), act(acc[j + 1], ACT), act(acc[j + 2], ACT),
-                         act(acc[j + 3], ACT)};
-    }
-  }
   __syncthreads();
 
-  // The first 2x2 over (T + 1) x (T + 1) pixels.
+  // The first 2x2 over (T + 1) x (T + 1) pixels: a wave takes row blocks
+  // two at a time (b and b + 4), two independent MFMA chains.
   {
     constexpr int M = R2 * R2, MB = (M + 15) / 16, S = S2;
-    for (int b = wave; b < MB; b += 4) {
-      const int m = b * 16 + li, sy = m / R2, sx = m - sy * R2;
-      const bool live = m < M && y0 + sy < a.oh && x0 + sx < a.ow;
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int b0 = wave; b0 < MB; b0 += 8) {
+      int sy[2], sx[2];
+      bool live[2];
+#pragma unroll
+      for (int u = 0; u < 2; u++) {
+        const int m = (b0 + 4 * u) * 16 + li;
+        sy[u] = m / R2, sx[u] = m - sy[u] * R2;
+        live[u] = m < M && y0 + sy[u] < a.oh && x0 + sx[u] < a.ow;
+      }
+      f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
       for (int q = 0; q < S; q++) {
         const int k = 16 * q + 4 * lg, tap = k / C1, ch = k - tap * C1, ky = tap >> 1, kx = tap & 1;
-        f32x4 v = {0.f, 0.f, 0.f, 0.f};
-        if (live && y0 + sy + ky < a.oh && x0 + sx + kx < a.ow)
-          v = *reinterpret_cast<const f32x4 *>(m1 + ((sy + ky) * R1 + sx + kx) * P1 + ch);
+        f32x4 v[2];
 #pragma unroll
-        for (int e = 0; e < 4; e++) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(v[e], bw2[q][e], acc, 0, 0, 0);
-      }
-      // acc[r]: row 4 lg + r of the block, column li.
+        for (int u = 0; u < 2; u++) {
+          v[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+          if (live[u] && y0 + sy[u] + ky < a.oh && x0 + sx[u] + kx < a.ow)
+            v[u] = *reinterpret_cast<const f32x4 *>(m1 + ((sy[u] + ky) * R1 + sx[u] + kx) * P1 + ch);
+        }
 #pragma unroll
-      for (int r = 0; r < 4; r++) {
-        const int mo = b * 16 + 4 * lg + r;
-        if (mo < M && li < C2) m2[mo * P2 + li] = act(acc[r] + bias2, ACT);
+        for (int e = 0; e < 4; e++)
+#pragma unroll
+          for (int u = 0; u < 2; u++) acc[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(v[u][e], bw2[q][e], acc[u], 0, 0, 0);
       }
+      // acc[u][r]: row 4 lg + r of block b0 + 4u, column li.
+#pragma unroll
+      for (int u = 0; u < 2; u++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          const int mo = (b0 + 4 * u) * 16 + 4 * lg + r;
+          if (mo < M && li < C2) m2[mo * P2 + li] = act(acc[u][r] + bias2, ACT);
+        }
     }
   }
   // The pool over the tile, one pixel a thread.
