@@ -343,15 +343,20 @@ __device__ __attribute__((aligned(16))) float kStemNoBias[32];
 // ACT: the activation of all three layers, fixed at compile time (a
 // runtime choice per output would inline every activation's code).
 template <int C1, int C2, int C3, int ACT>
-__global__ __launch_bounds__(256) void stem_block(StemArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5))) void stem_block(StemArgs a) {
   constexpr int T = kStemT, R1 = T + 2, R2 = T + 1;
   // Pixels an odd number of float4s apart: a wave's float4 reads of
   // consecutive pixels fall in distinct banks.
   constexpr int P1 = (C1 / 4) % 2 ? C1 : C1 + 4, P2 = (C2 / 4) % 2 ? C2 : C2 + 4;
   static_assert(R1 * R1 == 256, "one s1 pixel per thread");
   static_assert(C1 % 8 == 0 && C2 % 4 == 0 && C3 % 4 == 0, "float4 channels, every stem column fused");
-  __shared__ __attribute__((aligned(16))) float m1[R1 * R1 * P1];
-  __shared__ __attribute__((aligned(16))) float m2[R2 * R2 * P2];
+  // One LDS area: s1 until the first 2x2 has read it; then the first 2x2's
+  // map (held in registers across the barrier) and the staged outputs. At
+  // 29.6 KB, five workgroups share a CU.
+  constexpr int F2 = R2 * R2 * P2, LDS_F = R1 * R1 * P1 > F2 + T * T * C3 ? R1 * R1 * P1 : F2 + T * T * C3;
+  static_assert(F2 % 4 == 0, "staging on a float4 boundary");
+  __shared__ __attribute__((aligned(16))) float lds[LDS_F];
+  float *const m1 = lds, *const m2 = lds, *const st = lds + F2;
   const int tiles_x = (a.ow + T - 1) / T, tiles_y = (a.oh + T - 1) / T;
   // Tiles numbered XCD by XCD (xcd_tile): neighbours, which share input
   // rows, meet in one L2.
@@ -434,10 +439,16 @@ __global__ __launch_bounds__(256) void stem_block(StemArgs a) {
   __syncthreads();
 
   // The first 2x2 over (T + 1) x (T + 1) pixels: a wave takes row blocks
-  // two at a time (b and b + 4), two independent MFMA chains.
+  // two at a time (b and b + 4), two independent MFMA chains; its outputs
+  // stay in registers until s1 is no longer read.
+  constexpr int M2 = R2 * R2, MB2 = (M2 + 15) / 16;
+  static_assert(MB2 <= 16, "two rounds of two row blocks a wave");
+  f32x4 res[2][2];
   {
-    constexpr int M = R2 * R2, MB = (M + 15) / 16, S = S2;
-    for (int b0 = wave; b0 < MB; b0 += 8) {
+    constexpr int M = M2, S = S2;
+#pragma unroll
+    for (int it = 0; it < 2; it++) {
+      const int b0 = wave + 8 * it;
       int sy[2], sx[2];
       bool live[2];
 #pragma unroll
@@ -466,10 +477,7 @@ __global__ __launch_bounds__(256) void stem_block(StemArgs a) {
 #pragma unroll
       for (int u = 0; u < 2; u++)
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-          const int mo = (b0 + 4 * u) * 16 + 4 * lg + r;
-          if (mo < M && li < C2) m2[mo * P2 + li] = act(acc[u][r] + bias2, ACT);
-        }
+        for (int r = 0; r < 4; r++) res[it][u][r] = act(acc[u][r] + bias2, ACT);
     }
   }
   // The pool over the tile, one pixel a thread.
@@ -493,13 +501,21 @@ __global__ __launch_bounds__(256) void stem_block(StemArgs a) {
     }
   }
   __syncthreads();
+#pragma unroll
+  for (int it = 0; it < 2; it++)
+#pragma unroll
+    for (int u = 0; u < 2; u++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const int mo = (wave + 8 * it + 4 * u) * 16 + 4 * lg + r;
+        if (mo < M2 && li < C2) m2[mo * P2 + li] = res[it][u][r];
+      }
+  __syncthreads();
 
-  // The second 2x2 over the tile, its outputs staged in LDS over s1 (no
-  // longer read), then stored as whole pixel rows.
-  float *st = m1;
+  // The second 2x2 over the tile, its outputs staged in LDS past the first's
+  // map, then stored as whole pixel rows.
   {
     constexpr int M = T * T, MB = (M + 15) / 16, S = S3, NB = NB3;
-    static_assert(M * C3 <= R1 * R1 * P1, "staging fits");
     for (int b = wave; b < MB; b += 4) {
       const int m = b * 16 + li, oy = m / T, ox = m - oy * T;
       const bool live = m < M && y0 + oy < a.oh && x0 + ox < a.ow;
