@@ -575,31 +575,35 @@ hipError_t launch_stem_block(const StemArgs &a, hipStream_t s) {
 }
 
 // Thread = one input pixel (iy, ix) of the first transposed convolution and
-// one of its two output rows ky (blockIdx.y, so the weights a wave reads are
-// uniform). It forms the 2 x OC1 values of intermediate pixels
-// (2iy+ky, 2ix+kx), kx = 0, 1, as the engine's pointwise call over one input
-// row does (src/engine/layers.rs:600-680): the bias first for a
-// multiple-of-16 column count except the row's last iw % 4 pixels, else
-// last; fused multiply-adds below cols / 8 * 8. After the first activation,
-// each intermediate pixel gives its 2 x 2 outputs of the second convolution
-// (four columns: bias last, separate multiply and add), then the second
-// activation; the thread writes 2 rows x 4 columns of the final map.
+// one of its four taps (ky, kx) (blockIdx.y = 2 ky + kx, so the weights a
+// wave reads are uniform: scalar operands from the scalar cache). It forms
+// the OC1 values of intermediate pixel (2iy+ky, 2ix+kx) as the engine's
+// pointwise call over one input row does (src/engine/layers.rs:600-680):
+// the bias first for a multiple-of-16 column count except the row's last
+// iw % 4 pixels, else last; fused multiply-adds below cols / 8 * 8. After
+// the first activation the intermediate pixel gives its 2 x 2 outputs of
+// the second convolution (four columns: bias last, separate multiply and
+// add), then the second activation; the thread writes 2 rows x 2 columns of
+// the final map. A1, A2: the activations when fixed at compile time (the
+// DB head's ReLU and sigmoid), else -1 and read from the arguments.
 constexpr int kHeadMaxIc = 128;
 
-template <int OC1>
+template <int A>
+__device__ __forceinline__ float head_act(float v, int code) {
+  if constexpr (A >= 0) return act(v, A);
+  else return act(v, code);
+}
+
+template <int OC1, int A1, int A2>
 __global__ __launch_bounds__(256) void db_head_kernel(HeadArgs a) {
   constexpr int COLS1 = 4 * OC1;
   // 4 * OC1 columns, a multiple of 8 for every supported OC1: all of them
   // fuse their multiply-adds (columns below cols / 8 * 8 do).
   static_assert(COLS1 % 8 == 0, "every first-layer column fuses");
-  constexpr int T = 2 * OC1;  // the thread's first-layer columns
-  __shared__ __attribute__((aligned(16))) float w1s[kHeadMaxIc * T];
-  __shared__ __attribute__((aligned(16))) float w2s[OC1 * 4];
-  const int ky = blockIdx.y;
-  const int n0 = ky * T;  // columns of taps (ky, 0) and (ky, 1)
-  for (int e = threadIdx.x; e < a.ic * T; e += 256) w1s[e] = a.w1[(long)(e / T) * COLS1 + n0 + e % T];
-  for (int e = threadIdx.x; e < OC1 * 4; e += 256) w2s[e] = a.w2[e];
-  __syncthreads();
+  typedef const __attribute__((address_space(4))) float cfloat;
+  const int ky = blockIdx.y >> 1, kx = blockIdx.y & 1;
+  const int n0 = (ky * 2 + kx) * OC1;  // the columns of tap (ky, kx)
+  cfloat *w1 = (cfloat *)a.w1 + n0, *w2 = (cfloat *)a.w2;
   const int per = a.ih * a.iw;
   const int g = blockIdx.x * 256 + threadIdx.x;
   if (g >= a.lanes * per) return;
@@ -608,9 +612,11 @@ __global__ __launch_bounds__(256) void db_head_kernel(HeadArgs a) {
   const int iy = pix / a.iw, ix = pix - iy * a.iw;
   const bool first = COLS1 % 16 == 0 && ix < a.iw / 4 * 4;
   const float *xp = a.x + (long)ln * a.x_lane_stride + (long)pix * a.ic;
-  float t[T];
+  float b1[OC1], t[OC1];
 #pragma unroll
-  for (int n = 0; n < T; n++) t[n] = (a.b1 && first) ? a.b1[n0 + n] : 0.0f;
+  for (int n = 0; n < OC1; n++) b1[n] = a.b1 ? ((cfloat *)a.b1)[n0 + n] : 0.0f;
+#pragma unroll
+  for (int n = 0; n < OC1; n++) t[n] = first ? b1[n] : 0.0f;
   // Channels in runs of eight: the next run's loads are issued before this
   // run's sums, so a thread waits for memory once per run, not per channel.
   float4 cur0 = *reinterpret_cast<const float4 *>(xp), cur1 = *reinterpret_cast<const float4 *>(xp + 4);
@@ -623,44 +629,28 @@ __global__ __launch_bounds__(256) void db_head_kernel(HeadArgs a) {
     const float xv[8] = {cur0.x, cur0.y, cur0.z, cur0.w, cur1.x, cur1.y, cur1.z, cur1.w};
 #pragma unroll
     for (int ii = 0; ii < 8; ii++) {
-      const float v = xv[ii];
-      const float *wr = w1s + (i0 + ii) * T;
+      cfloat *wr = w1 + (long)(i0 + ii) * COLS1;
 #pragma unroll
-      for (int n = 0; n < T; n += 4) {
-        const float4 w = *reinterpret_cast<const float4 *>(wr + n);
-        const float wv[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-        for (int k = 0; k < 4; k++) t[n + k] = fmaf(wv[k], v, t[n + k]);
-      }
+      for (int n = 0; n < OC1; n++) t[n] = fmaf(wr[n], xv[ii], t[n]);
     }
     cur0 = nx0, cur1 = nx1;
   }
 #pragma unroll
-  for (int n = 0; n < T; n++) {
-    float v = t[n];
-    if (a.b1 && !first) v = v + a.b1[n0 + n];
-    t[n] = act(v, a.act1);
-  }
-  // Second convolution, oc 1: four columns per intermediate pixel, tap
-  // (ky2, kx2) = column ky2 * 2 + kx2.
-  float out[2][4];
+  for (int n = 0; n < OC1; n++) t[n] = head_act<A1>(a.b1 && !first ? t[n] + b1[n] : t[n], a.act1);
+  // Second convolution, oc 1: four columns, tap (ky2, kx2) = column ky2 * 2 + kx2.
+  float out[4];
 #pragma unroll
-  for (int kx = 0; kx < 2; kx++) {
+  for (int c = 0; c < 4; c++) {
+    float acc = 0.0f;
 #pragma unroll
-    for (int c = 0; c < 4; c++) {
-      float acc = 0.0f;
-#pragma unroll
-      for (int o = 0; o < OC1; o++) acc = acc + t[kx * OC1 + o] * w2s[o * 4 + c];
-      if (a.b2) acc = acc + a.b2[c];
-      out[c >> 1][kx * 2 + (c & 1)] = act(acc, a.act2);
-    }
+    for (int o = 0; o < OC1; o++) acc = acc + t[o] * w2[o * 4 + c];
+    if (a.b2) acc = acc + ((cfloat *)a.b2)[c];
+    out[c] = head_act<A2>(acc, a.act2);
   }
   const long ow = 4L * a.iw;
-  const long row = 4L * iy + 2L * ky;
-  float *y = a.y + (long)ln * a.y_lane_stride + row * ow + 4L * ix;
-#pragma unroll
-  for (int r = 0; r < 2; r++)
-    *reinterpret_cast<float4 *>(y + r * ow) = make_float4(out[r][0], out[r][1], out[r][2], out[r][3]);
+  float *y = a.y + (long)ln * a.y_lane_stride + (4L * iy + 2L * ky) * ow + 4L * ix + 2L * kx;
+  *reinterpret_cast<float2 *>(y) = make_float2(out[0], out[1]);
+  *reinterpret_cast<float2 *>(y + ow) = make_float2(out[2], out[3]);
 }
 
 bool head_supported(int ic, int oc1) {
@@ -670,16 +660,20 @@ bool head_supported(int ic, int oc1) {
 hipError_t launch_db_head(const HeadArgs &a, hipStream_t s) {
   const long n = (long)a.lanes * a.ih * a.iw;
   if (n <= 0) return hipSuccess;
-  // The float4 loads and stores need 16-byte aligned pixels.
+  // The float4 loads need 16-byte aligned pixels, the float2 stores 8-byte ones.
   if (!head_supported(a.ic, a.oc1) || (reinterpret_cast<uintptr_t>(a.y) & 15) || (a.y_lane_stride & 3) ||
       (reinterpret_cast<uintptr_t>(a.x) & 15) || (a.x_lane_stride & 3) || n > 0x7fffff00L)
     return hipErrorInvalidValue;
-  dim3 grid((unsigned)((n + 255) / 256), 2), block(256);
+  dim3 grid((unsigned)((n + 255) / 256), 4), block(256);
+  const bool db = a.act1 == ACT_RELU && a.act2 == ACT_SIGMOID;
   switch (a.oc1) {
-    case 8: hipLaunchKernelGGL(db_head_kernel<8>, grid, block, 0, s, a); break;
-    case 16: hipLaunchKernelGGL(db_head_kernel<16>, grid, block, 0, s, a); break;
-    case 24: hipLaunchKernelGGL(db_head_kernel<24>, grid, block, 0, s, a); break;
-    case 32: hipLaunchKernelGGL(db_head_kernel<32>, grid, block, 0, s, a); break;
+    case 8: hipLaunchKernelGGL((db_head_kernel<8, -1, -1>), grid, block, 0, s, a); break;
+    case 16: hipLaunchKernelGGL((db_head_kernel<16, -1, -1>), grid, block, 0, s, a); break;
+    case 24:
+      if (db) hipLaunchKernelGGL((db_head_kernel<24, ACT_RELU, ACT_SIGMOID>), grid, block, 0, s, a);
+      else hipLaunchKernelGGL((db_head_kernel<24, -1, -1>), grid, block, 0, s, a);
+      break;
+    case 32: hipLaunchKernelGGL((db_head_kernel<32, -1, -1>), grid, block, 0, s, a); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
