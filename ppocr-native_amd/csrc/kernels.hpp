@@ -259,6 +259,25 @@ struct EltArgs {
   float *y; long y_lane_stride;
 };
 hipError_t launch_eltwise(const EltArgs &a, hipStream_t s);
+
+// A chain of 2x nearest upsample-adds in one pass (a feature pyramid's
+// top-down path): level k (0 the finest) is
+//   y_k = act_k((b_k + b_k * g_k[c]) + y_{k+1}[oy / 2][ox / 2])
+// (without a gate: b_k + y_{k+1}...), y_levels being `top`. Each level's map
+// is h[k] x w[k] = 2 h[k+1] x 2 w[k+1]; top is (h / 2) x (w / 2) of the
+// coarsest level. Every level's output is written.
+constexpr int kChainMax = 3;
+struct ChainArgs {
+  int lanes, levels, c;
+  int h[kChainMax], w[kChainMax];
+  const float *top; long top_lane_stride;
+  const float *b[kChainMax]; long b_lane_stride[kChainMax];
+  const float *g[kChainMax]; long g_lane_stride[kChainMax];  // null: no gate
+  int act[kChainMax];
+  float *y[kChainMax]; long y_lane_stride[kChainMax];
+};
+bool upadd_chain_supported(const ChainArgs &a);
+hipError_t launch_upadd_chain(const ChainArgs &a, hipStream_t s);
 // Whether launch_eltwise takes four floats at a time (the same for every
 // member of a grouped launch).
 bool eltwise_vec(const EltArgs &a);

@@ -12,6 +12,8 @@
 // sums of one pixel (bias last, src/engine/kernels/pointwise.rs:135-185).
 // Channel means sum in f64 as the CPU does (layers.rs:391-406), in another
 // order.
+#include <algorithm>
+
 #include "act.hpp"
 #include "kernels.hpp"
 
@@ -576,6 +578,69 @@ __global__ __launch_bounds__(256) void eltwise_kernel(Group<EltArgs> grp) {
     }
     vstore<V>(a.y + (long)ln * a.y_lane_stride + off, v);
   }
+}
+
+// The upsample-add chain, four channels a thread over the finest map: the
+// thread forms its pixel's value at every level from the coarsest source
+// down, in each level the operations of the separate upsample-add (the
+// gated addend, then the upsampled value added, then the activation), and
+// stores level k where its pixel is the top-left one of its 2^k x 2^k block
+// (so each level's element is written once, with the bits its own launch
+// would give).
+template <int L>
+__global__ __launch_bounds__(256) void upadd_chain_kernel(ChainArgs a) {
+  const int cq = a.c / 4;
+  const long per = (long)a.h[0] * a.w[0] * cq, total = per * a.lanes;
+  const int top_w = a.w[L - 1] / 2;
+  for (long e = (long)blockIdx.x * 256 + threadIdx.x; e < total; e += (long)gridDim.x * 256) {
+    const int ln = (int)(e / per);
+    const long r = e - (long)ln * per;
+    const int q = (int)(r % cq);
+    const long pix = r / cq;
+    const int y = (int)(pix / a.w[0]), x = (int)(pix - (long)y * a.w[0]), ch = 4 * q;
+    f32x4 v = *reinterpret_cast<const f32x4 *>(a.top + (long)ln * a.top_lane_stride +
+                                              ((long)(y >> L) * top_w + (x >> L)) * a.c + ch);
+#pragma unroll
+    for (int k = L - 1; k >= 0; k--) {
+      const long o = ((long)(y >> k) * a.w[k] + (x >> k)) * a.c + ch;
+      f32x4 u = *reinterpret_cast<const f32x4 *>(a.b[k] + (long)ln * a.b_lane_stride[k] + o);
+      if (a.g[k]) {
+        const f32x4 g = *reinterpret_cast<const f32x4 *>(a.g[k] + (long)ln * a.g_lane_stride[k] + ch);
+#pragma unroll
+        for (int i = 0; i < 4; i++) u[i] = u[i] + u[i] * g[i];
+      }
+#pragma unroll
+      for (int i = 0; i < 4; i++) v[i] = u[i] + v[i];
+      if (a.act[k] != ACT_NONE) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) v[i] = act(v[i], a.act[k]);
+      }
+      if (((y | x) & ((1 << k) - 1)) == 0)
+        *reinterpret_cast<f32x4 *>(a.y[k] + (long)ln * a.y_lane_stride[k] + o) = v;
+    }
+  }
+}
+
+bool upadd_chain_supported(const ChainArgs &a) {
+  if (a.levels < 2 || a.levels > kChainMax || a.c % 4 || a.lanes < 1) return false;
+  auto a16 = [](const void *p) { return (uintptr_t(p) & 15) == 0; };
+  if (!a16(a.top) || a.top_lane_stride % 4) return false;
+  for (int k = 0; k < a.levels; k++) {
+    if (a.h[k] < 1 || a.w[k] < 1 || a.h[k] % 2 || a.w[k] % 2) return false;
+    if (k + 1 < a.levels && (a.h[k] != 2 * a.h[k + 1] || a.w[k] != 2 * a.w[k + 1])) return false;
+    if (!a16(a.b[k]) || !a16(a.y[k]) || (a.g[k] && !a16(a.g[k]))) return false;
+    if (a.b_lane_stride[k] % 4 || a.y_lane_stride[k] % 4 || (a.g[k] && a.g_lane_stride[k] % 4)) return false;
+  }
+  return true;
+}
+
+hipError_t launch_upadd_chain(const ChainArgs &a, hipStream_t s) {
+  if (!upadd_chain_supported(a)) return hipErrorInvalidValue;
+  const long total = (long)a.lanes * a.h[0] * a.w[0] * (a.c / 4);
+  const unsigned blocks = (unsigned)std::min<long>((total + 255) / 256, 65536L * 4);
+  if (a.levels == 2) hipLaunchKernelGGL(upadd_chain_kernel<2>, dim3(blocks), dim3(256), 0, s, a);
+  else hipLaunchKernelGGL(upadd_chain_kernel<3>, dim3(blocks), dim3(256), 0, s, a);
+  return hipGetLastError();
 }
 
 bool eltwise_vec(const EltArgs &a) {

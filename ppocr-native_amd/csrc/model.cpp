@@ -89,6 +89,9 @@ struct Step {
   int m_ln = -1, m_fc1 = -1, m_fc2 = -1, m_add = -1;  // S_ENC_BLOCK: its MLP's operations
   int head2 = -1;          // the narrow transposed convolution folded into S_HEAD
   int st2 = -1, st3 = -1, st_pool = -1;  // S_STEM: the two 2x2 layers and the pool
+  // S_ELT as an upsample-add chain: its levels' operations, finest first
+  // (chain[0] == op), and each level's residual-gate channelmul or -1.
+  std::vector<int> chain, chain_gate;
   bool dw_sums = false;    // S_DW: also sum its output per channel for the next step's mean
   bool patch = false;      // S_GEMM: a windowed convolution on halo tiles (conv_patch)
   bool ring = false;       // S_GEMM: a windowed convolution on the LDS ring (conv_ring)
@@ -203,8 +206,14 @@ struct Model {
   std::vector<size_t> step_reads(const Step &s) const;
   int enc_hidden(const Step &s) const { return s.kind == S_ENC_BLOCK ? int(plan.ops[s.m_fc1].oc) : 0; }
   size_t step_writes(const Step &s) const;
-  // A second output of the step (S_STEM's pool), else SIZE_MAX.
-  size_t step_writes2(const Step &s) const { return s.kind == S_STEM ? plan.ops[s.st_pool].y : SIZE_MAX; }
+  // The step's other outputs: S_STEM's pool, an upsample-add chain's
+  // coarser levels.
+  std::vector<size_t> step_writes_extra(const Step &s) const {
+    std::vector<size_t> r;
+    if (s.kind == S_STEM) r.push_back(plan.ops[s.st_pool].y);
+    for (size_t k = 1; k < s.chain.size(); k++) r.push_back(plan.ops[s.chain[k]].y);
+    return r;
+  }
 };
 
 Model::~Model() {
@@ -236,7 +245,16 @@ std::vector<size_t> Model::step_reads(const Step &s) const {
       }
       break;
     case S_ELT:
-      if (s.elt == ELT_RESGATE) {
+      if (!s.chain.empty()) {
+        r.push_back(plan.ops[s.chain.back()].x);
+        for (size_t k = 0; k < s.chain.size(); k++) {
+          if (s.chain_gate[k] >= 0) {
+            r.push_back(plan.ops[s.chain_gate[k]].x), r.push_back(plan.ops[s.chain_gate[k]].x2);
+          } else {
+            r.push_back(plan.ops[s.chain[k]].x2);
+          }
+        }
+      } else if (s.elt == ELT_RESGATE) {
         r = {plan.ops[s.resgate].x, plan.ops[s.resgate].x2};
       } else if (s.elt == ELT_UPSAMPLEADD_RESGATE) {
         r = {op.x, plan.ops[s.resgate].x, plan.ops[s.resgate].x2};
@@ -597,6 +615,45 @@ bool Model::build_steps(std::string &err) {
     a.m_ln = m.op, a.m_fc1 = m.fc1, a.m_fc2 = m.fc2, a.m_add = m.add, a.ln_out = m.ln_out;
     steps.erase(steps.begin() + k);
   }
+  // Chains of 2x upsample-adds, each level's map the next one's upsampled
+  // source (a feature pyramid's top-down sums): one step, in the finest
+  // level's place, that writes every level (upadd_chain). Every other reader
+  // of a coarser level must come after that place.
+  {
+    auto upadd = [&](const Step &t) {
+      return t.kind == S_ELT && t.chain.empty() && (t.elt == ELT_UPSAMPLEADD || t.elt == ELT_UPSAMPLEADD_RESGATE) &&
+             ops[t.op].sh == 2 && ops[t.op].sw == 2 && ops[t.op].oc % 4 == 0;
+    };
+    std::vector<int> prod(plan.pool.size(), -1);
+    std::vector<std::vector<int>> rd(plan.pool.size());
+    for (size_t k = 0; k < steps.size(); k++) {
+      prod[step_writes(steps[k])] = int(k);
+      for (size_t sl : step_reads(steps[k])) rd[sl].push_back(int(k));
+    }
+    std::vector<bool> drop(steps.size(), false);
+    for (int f = int(steps.size()) - 1; f >= 0; f--) {
+      if (drop[size_t(f)] || !upadd(steps[size_t(f)])) continue;
+      std::vector<int> lv{f};
+      while (lv.size() < size_t(kChainMax)) {
+        const int q = prod[ops[steps[size_t(lv.back())].op].x];
+        if (q < 0 || drop[size_t(q)] || !upadd(steps[size_t(q)]) || ops[steps[size_t(q)].op].oc != ops[steps[size_t(f)].op].oc)
+          break;
+        bool later = true;
+        for (int r : rd[ops[steps[size_t(q)].op].y]) later = later && (r == lv.back() || r > f);
+        if (!later) break;
+        lv.push_back(q);
+      }
+      if (lv.size() < 2) continue;
+      std::vector<int> ch, cg;
+      for (int k : lv) ch.push_back(steps[size_t(k)].op), cg.push_back(steps[size_t(k)].resgate);
+      steps[size_t(f)].chain = ch, steps[size_t(f)].chain_gate = cg;
+      for (size_t k = 1; k < lv.size(); k++) drop[size_t(lv[k])] = true;
+    }
+    std::vector<Step> kept;
+    for (size_t k = 0; k < steps.size(); k++)
+      if (!drop[k]) kept.push_back(steps[k]);
+    steps = kept;
+  }
   // A channel mean right after the depthwise convolution that produces its
   // input: the depthwise kernel sums its outputs per channel as it stores
   // them, and the mean step only joins those sums (no second read).
@@ -864,7 +921,7 @@ bool Model::arrange(Batch &b, std::string &err) {
   std::vector<std::vector<size_t>> slot_readers(p.pool.size());
   for (size_t i = 0; i < n; i++) {
     producer[step_writes(steps[i])] = i;
-    if (step_writes2(steps[i]) != SIZE_MAX) producer[step_writes2(steps[i])] = i;
+    for (size_t y2 : step_writes_extra(steps[i])) producer[y2] = i;
     for (size_t sl : step_reads(steps[i])) slot_readers[sl].push_back(i);
   }
   std::vector<std::vector<bool>> anc(n, std::vector<bool>(n, false));
@@ -909,8 +966,7 @@ bool Model::arrange(Batch &b, std::string &err) {
   for (size_t i = 0; i < n; i++) {
     size_t y = step_writes(steps[i]);
     b.home[y] = place(p.pool[y], i);
-    const size_t y2 = step_writes2(steps[i]);
-    if (y2 != SIZE_MAX) b.home[y2] = place(p.pool[y2], i);
+    for (size_t y2 : step_writes_extra(steps[i])) b.home[y2] = place(p.pool[y2], i);
     for (size_t sl : step_reads(steps[i]))
       if (last[sl] == i && std::find(freel.begin(), freel.end(), b.home[sl]) == freel.end()) {
         freel.push_back(b.home[sl]);
@@ -1130,6 +1186,26 @@ void Model::build_launches(Batch &b) {
         break;
       }
       case S_ELT: {
+        if (!s.chain.empty()) {
+          ChainArgs c{};
+          c.lanes = L, c.levels = int(s.chain.size()), c.c = int(op.oc);
+          const Op &top = p.ops[s.chain.back()];
+          c.top = b.dev(top.x), c.top_lane_stride = b.stride(top.x);
+          for (int k = 0; k < c.levels; k++) {
+            const Op &o = p.ops[s.chain[k]];
+            c.h[k] = int(o.oh), c.w[k] = int(o.ow), c.act[k] = o.fused;
+            const size_t addend = s.chain_gate[k] >= 0 ? p.ops[s.chain_gate[k]].x : o.x2;
+            c.b[k] = b.dev(addend), c.b_lane_stride[k] = b.stride(addend);
+            if (s.chain_gate[k] >= 0) {
+              const size_t g = p.ops[s.chain_gate[k]].x2;
+              c.g[k] = b.dev(g), c.g_lane_stride[k] = b.stride(g);
+            }
+            c.y[k] = b.dev(o.y), c.y_lane_stride[k] = b.stride(o.y);
+          }
+          b.launches.push_back({"upsample_add_chain", s.op, [c](hipStream_t st) { return launch_upadd_chain(c, st); }});
+          b.launches.back().member_ops.assign(s.chain.rbegin(), s.chain.rend());
+          break;
+        }
         EltArgs a{};
         a.mode = s.elt, a.lanes = L;
         a.oh = int(op.oh), a.ow = int(op.ow), a.c = int(op.oc);
@@ -1352,6 +1428,8 @@ void Model::build_launches(Batch &b) {
         a.pool = b.dev(pl.y), a.pool_lane_stride = b.stride(pl.y);
         a.y = Y, a.y_lane_stride = ys;
         b.launches.push_back({"stem_block", s.op, [a](hipStream_t st) { return launch_stem_block(a, st); }});
+        b.launches.back().member_ops = {s.op, s.st2, s.st3, s.st_pool};
+        std::sort(b.launches.back().member_ops.begin(), b.launches.back().member_ops.end());
         break;
       }
       case S_HEAD: {
@@ -1388,7 +1466,7 @@ void Model::link(Batch &b) const {
     std::vector<size_t> rd, wr;
     for (size_t slot : step_reads(s)) rd.push_back(b.home[slot]);
     wr.push_back(b.home[step_writes(s)]);
-    if (step_writes2(s) != SIZE_MAX) wr.push_back(b.home[step_writes2(s)]);
+    for (size_t y2 : step_writes_extra(s)) wr.push_back(b.home[y2]);
     const size_t ws = H + size_t(l.step);
     if (s.kind == S_MEAN || s.kind == S_CTC || s.kind == S_ATTN || s.kind == S_ENC_ATTN || s.kind == S_ENC_BLOCK)
       rd.push_back(ws), wr.push_back(ws);
@@ -1490,12 +1568,16 @@ void Model::group(Batch &b) const {
     if (mem.size() == 1) {
       out.push_back(b.launches[size_t(mem[0])]);
       out.back().members = mem;
-      out.back().member_ops = {out.back().op};
+      if (out.back().member_ops.empty()) out.back().member_ops = {out.back().op};
       continue;
     }
     Launch gl = b.launches[size_t(mem[0])];
     gl.members = mem;
-    for (int m : mem) gl.member_ops.push_back(b.launches[size_t(m)].op);
+    for (int m : mem) {
+      const Launch &ml = b.launches[size_t(m)];
+      if (ml.member_ops.empty()) gl.member_ops.push_back(ml.op);
+      else gl.member_ops.insert(gl.member_ops.end(), ml.member_ops.begin(), ml.member_ops.end());
+    }
     gl.flops = gl.bytes = 0;
     for (int m : mem) gl.flops += b.launches[size_t(m)].flops, gl.bytes += b.launches[size_t(m)].bytes;
     switch (gl.gk) {
@@ -1616,6 +1698,16 @@ void Model::account(Batch &b) const {
         break;
       case S_ELT: {
         double out = L * out_px * op.oc, src = L * in_px * op.ic;
+        if (!s.chain.empty()) {
+          const Op &top = p.ops[s.chain.back()];
+          double f = L * double(top.ih) * top.iw * top.ic;
+          for (size_t k = 0; k < s.chain.size(); k++) {
+            const Op &o = p.ops[s.chain[k]];
+            f += 2.0 * L * double(o.oh) * o.ow * o.oc + (s.chain_gate[k] >= 0 ? L * o.oc : 0.0);
+          }
+          l.bytes = F * f;
+          break;
+        }
         switch (s.elt) {
           case ELT_ADD: l.bytes = F * 3 * out; break;
           case ELT_CHANNELMUL: case ELT_RESGATE: l.bytes = F * (2 * out + L * op.oc); break;

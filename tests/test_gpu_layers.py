@@ -344,6 +344,36 @@ def test_elementwise_exact(oracle, mode):
     exact(got, want)
 
 
+@pytest.mark.parametrize("hw,c,levels,lanes", [((48, 64), 8, 3, 3), ((40, 24), 24, 3, 2), ((16, 8), 12, 2, 3),
+                                                 ((24, 40), 6, 3, 2)])
+def test_upsample_add_chain_exact(oracle, hw, c, levels, lanes):
+    # A feature pyramid's top-down sums: each level the gated addend plus the
+    # coarser level upsampled 2x, the finest addend ungated. With channels a
+    # multiple of 4 the levels run as one chain launch that writes each.
+    def build(b, t):
+        pyr = [t]
+        for _ in range(levels):
+            pyr.append(b.maxpool(pyr[-1], k=(2, 2), s=(2, 2), pad_after=(0, 0)))
+
+        def gated(x):
+            return b.add(x, b.channelmul(x, b.mean(x)))
+
+        outs, up = [], pyr[levels]
+        for k in range(levels - 1, -1, -1):
+            up = b.upsampleadd(up, gated(pyr[k]) if k else pyr[k], 2)
+            outs.append(up)
+        return outs
+
+    h, w = hw
+    b = PlanBuilder(h, w, c)
+    g = GpuModel.load(b.to_bytes(build(b, b.input)))
+    names = [name for name, _ in g.launches()]
+    g.close()
+    assert ("upsample_add_chain" in names) == (c % 4 == 0)
+    got, want = both(build, (h, w, c), oracle, lanes=lanes)
+    exact(got, want)
+
+
 @pytest.mark.parametrize("c", [20, 6])
 def test_pools_exact(oracle, c):
     # Four channels at a time when c % 4 == 0, else one.
