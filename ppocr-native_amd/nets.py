@@ -218,12 +218,14 @@ def detector_plan(*, h: int = 960, w: int = 960, seed: int = 3, init: str = "bas
 
 def recognizer_plan(*, h: int = 48, w: int = 320, vocab: int = 18385, dim: int = 120,
                     heads: int = 8, depth: int = 2, seed: int = 4, init: str = "baseline",
-                    sigma: float = 0.02) -> bytes:
+                    sigma: float = 0.02, logits: bool = False) -> bytes:
     """An SVTR-style CTC recogniser: LCNet-style backbone with stride-(2,1)
     stages, average pool of the 3 remaining rows to W/4 time steps, a 1x1
     projection to `dim`, `depth` pre-norm transformer blocks (LayerNorm eps
     1e-6, `heads`-head attention, MLP ratio 2 with swish), a final
-    LayerNorm and the CTC argmax head over `vocab` classes."""
+    LayerNorm and the CTC argmax head over `vocab` classes. With `logits`
+    the same weights end in a plain 1x1 layer whose output is the logits
+    (time steps x vocab), for checking them directly."""
     r = Init(seed, init, sigma, gain=1.6)
     b = PlanBuilder(h, w, 3)
     act = "hardswish"
@@ -255,7 +257,8 @@ def recognizer_plan(*, h: int = 48, w: int = 320, vocab: int = 18385, dim: int =
         f = b.conv(f, r.w((1, 1, 2 * dim, dim), 2 * dim, 1.0), r.b(dim))
         z = b.add(z, f)
     n = ln(z)
-    out = b.ctcargmax(n, r.w((dim, vocab), dim, 1.0), r.b(vocab))
+    wv, bv = r.w((dim, vocab), dim, 1.0), r.b(vocab)
+    out = b.conv(n, wv.reshape(1, 1, dim, vocab), bv) if logits else b.ctcargmax(n, wv, bv)
     return b.to_bytes([out])
 
 

@@ -70,6 +70,25 @@ def test_recognizer_batch(oracle, init, vocab):
         check_rec(got[i], m.run(lines[i])[0])
 
 
+@pytest.mark.parametrize("init", ["scaled", "baseline"])
+def test_recognizer_logits(oracle, init):
+    # The recogniser with its CTC head as a plain 1x1 layer: the 80 x 18385
+    # logits of every line within 1e-5 relative plus 1e-5 absolute.
+    plan = nets.recognizer_plan(init=init, logits=True)
+    lines = nets.line_images(16)
+    got = gpu_run(plan, list(lines))
+    m = oracle.OracleModel(plan)
+    worst = 0.0
+    for i in range(16):
+        want = m.run(lines[i])[0].astype(np.float64)
+        assert got[i].shape == want.shape == (80 * 18385,)
+        err = np.abs(got[i] - want)
+        lim = 1e-5 * np.abs(want) + 1e-5
+        assert (err <= lim).all(), f"line {i}: {(err > lim).sum()} logits outside, worst excess {(err - lim).max():.3g}"
+        worst = max(worst, float((err / lim).max()))
+    print(f"rec logits {init}: worst |d| / (1e-5 |y| + 1e-5) = {worst:.3f}")
+
+
 def test_recognizer_lanes_of_different_widths(oracle):
     plan = nets.recognizer_plan(init="scaled", vocab=6625)
     rng = np.random.default_rng(3)
