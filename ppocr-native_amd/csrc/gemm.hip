@@ -423,6 +423,7 @@ __global__ __launch_bounds__(256) void conv_mfma(ConvArgs a) {
 // float4s (its channel group of every 256 / (CB / 4)-th pixel) and weight
 // float4s (taps x its column pairs).
 constexpr int kPatchPer = 6;
+constexpr int kPatchPerR8W1 = 4;
 constexpr int kWeightPer = 9;
 
 // LDS layout of conv_patch. A ds_read_b128 on gfx950 (measured) serves lanes
@@ -455,7 +456,7 @@ __host__ __device__ inline int patch_col_stride(int taps, int row, int cb) {
 // (c = 0, 1: two instructions); the four lane groups' partial sums are added
 // at the end ((p0 + p1) + (p2 + p3), the same bits in every lane).
 template <int WR, int BN, int CB, bool R8>
-__global__ __launch_bounds__(256) void conv_patch(Group<ConvArgs> grp) {
+__device__ __forceinline__ void conv_patch_body(const Group<ConvArgs> &grp) {
   // Each XCD takes a contiguous run of tiles (xcd_tile): neighbouring tiles
   // share halo rows and columns, which then meet in one L2.
   const int bid = xcd_tile((int)blockIdx.x, (int)gridDim.x);
@@ -543,7 +544,11 @@ __global__ __launch_bounds__(256) void conv_patch(Group<ConvArgs> grp) {
   const int npx = PR * PC;
   constexpr int PAIRS = BN * CQ;
   constexpr int PPAIRS = (PAIRS + 255) / 256;
-  f32x4 rp[kPatchPer], rw[kWeightPer];
+  // R8 on one row block a wave: its patch takes at most kPatchPerR8W1
+  // float4s a thread (the launch checks), which keeps the registers of the
+  // remainder within three waves per SIMD.
+  constexpr int PP = R8 && WR == 1 ? kPatchPerR8W1 : kPatchPer;
+  f32x4 rp[PP], rw[kWeightPer];
   auto fetch = [&](int cc) {
     const int c = cc * CB + q * 4;
     const bool live_c = c < a.ctot;
@@ -555,7 +560,7 @@ __global__ __launch_bounds__(256) void conv_patch(Group<ConvArgs> grp) {
                           : f32x4{1.f, 1.f, 1.f, 1.f};
     int py = p0 / PC, px = p0 - (p0 / PC) * PC;
 #pragma unroll
-    for (int k = 0; k < kPatchPer; k++) {
+    for (int k = 0; k < PP; k++) {
       const int iy = iy0 + py, ix = ix0 + px;
       f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
       if (p0 + k * PSTEP < npx && live_c && iy >= 0 && iy < a.ih && ix >= 0 && ix < a.iw) {
@@ -580,7 +585,7 @@ __global__ __launch_bounds__(256) void conv_patch(Group<ConvArgs> grp) {
   };
   auto store = [&]() {
 #pragma unroll
-    for (int k = 0; k < kPatchPer; k++)
+    for (int k = 0; k < PP; k++)
       if (p0 + k * PSTEP < npx) *reinterpret_cast<f32x4 *>(P + (p0 + k * PSTEP) * S + q * 4) = rp[k];
 #pragma unroll
     for (int u = 0; u < PPAIRS; u++) {
@@ -701,6 +706,19 @@ __global__ __launch_bounds__(256) void conv_patch(Group<ConvArgs> grp) {
       }
     }
   }
+}
+
+template <int WR, int BN, int CB, bool R8>
+__global__ __launch_bounds__(256) void conv_patch(Group<ConvArgs> grp) {
+  conv_patch_body<WR, BN, CB, R8>(grp);
+}
+
+// One row block a wave and up to 32 columns, with or without the 8-column
+// remainder: held to three waves per SIMD (the occupancy its LDS leaves room
+// for; 64 columns would spill).
+template <int BN, int CB, bool R8>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void conv_patch_w1(Group<ConvArgs> grp) {
+  conv_patch_body<1, BN, CB, R8>(grp);
 }
 
 // One wave per row: join the row's tile partials, then y = (best, 1 / sum).
@@ -1463,6 +1481,9 @@ size_t patch_lds_bytes(const ConvArgs &a, int wr, int bk, int bn) {
 
 template <int WR, int BN, int CB, bool R8 = false>
 static hipError_t go_patch(const ConvArgs *as, int n, hipStream_t s) {
+  const void *kernel;
+  if constexpr (WR == 1 && BN <= 32) kernel = reinterpret_cast<const void *>(conv_patch_w1<BN, CB, R8>);
+  else kernel = reinterpret_cast<const void *>(conv_patch<WR, BN, CB, R8>);
   constexpr int TH = 4 * WR;
   Group<ConvArgs> grp{};
   grp.n = n;
@@ -1484,16 +1505,19 @@ static hipError_t go_patch(const ConvArgs *as, int n, hipStream_t s) {
   grp.first[n] = (int)blocks;
   if (shm > 160 * 1024) return hipErrorInvalidValue;
   if (shm > 64 * 1024) {
-    hipError_t e = allow_lds(reinterpret_cast<const void *>(conv_patch<WR, BN, CB, R8>), 160 * 1024);
+    hipError_t e = allow_lds(kernel, 160 * 1024);
     if (e != hipSuccess) return e;
   }
-  hipLaunchKernelGGL((conv_patch<WR, BN, CB, R8>), dim3((unsigned)blocks), dim3(256), shm, s, grp);
+  if constexpr (WR == 1 && BN <= 32)
+    hipLaunchKernelGGL((conv_patch_w1<BN, CB, R8>), dim3((unsigned)blocks), dim3(256), shm, s, grp);
+  else
+    hipLaunchKernelGGL((conv_patch<WR, BN, CB, R8>), dim3((unsigned)blocks), dim3(256), shm, s, grp);
   return hipGetLastError();
 }
 
 #define PPOCR_PATCH(WR, CB)                                        \
   if (bn == 16) return go_patch<WR, 16, CB>(as, n, s);           \
-  if (bn == 32 && r8 && WR == 2) return go_patch<2, 32, CB, true>(as, n, s); \
+  if (bn == 32 && r8) return go_patch<WR, 32, CB, true>(as, n, s);        \
   if (bn == 32) return go_patch<WR, 32, CB>(as, n, s);           \
   if (bn == 64) return go_patch<WR, 64, CB>(as, n, s);
 
@@ -1503,15 +1527,17 @@ hipError_t launch_conv_patch(const ConvArgs &a, int wr, int bk, int bn, hipStrea
 
 hipError_t launch_conv_patch_group(const ConvArgs *as, int n, int wr, int bk, int bn, hipStream_t s) {
   if (n < 1 || n > kGroupMax) return hipErrorInvalidValue;
-  // 17 to 24 columns on 32-column tiles of two row blocks a wave: the
-  // 8-column remainder (R8); the detector head's 3 x 3 went from 40 to 35
-  // us. With one row block a wave its registers (168 -> 240, or 16 spilled
-  // when held to 168) cost the third wave per SIMD the LDS leaves room for,
-  // and the neck's group went from 51 to 54 us.
-  bool r8 = bn == 32 && wr == 2;
+  // 17 to 24 columns on 32-column tiles: the 8-column remainder (R8); the
+  // detector head's 3 x 3 (two row blocks a wave) went from 40 to 35 us, the
+  // neck's group (one row block a wave, its patch within four float4s a
+  // thread and the kernel held to three waves per SIMD) from 51 to 46 us.
+  bool r8 = bn == 32;
   for (int p = 0; p < n; p++) {
     if (!patch_supported(as[p], wr, bk, bn)) return hipErrorInvalidValue;
     r8 = r8 && as[p].n > 16 && as[p].n <= 24;
+    // One row block a wave: the patch within kPatchPerR8W1 float4s a thread.
+    const int pr = 3 * as[p].sh + as[p].kh, pc = 15 * as[p].sw + as[p].kw;
+    if (wr == 1 && (pr * pc + 256 / (bk / 4) - 1) / (256 / (bk / 4)) > kPatchPerR8W1) r8 = false;
   }
   if (wr == 2) {
     if (bk == 32) { PPOCR_PATCH(2, 32) }
