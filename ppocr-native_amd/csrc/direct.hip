@@ -484,7 +484,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5))) void s
   if (tid < T * T) {
     const int oy = tid / T, ox = tid % T, Y = y0 + oy, X = x0 + ox;
     if (Y < a.oh && X < a.ow) {
-      f32x4 *dst = reinterpret_cast<f32x4 *>(a.pool + (long)ln * a.pool_lane_stride + ((long)Y * a.ow + X) * C1);
+      f32x4 *dst = reinterpret_cast<f32x4 *>(a.pool + (long)ln * a.pool_lane_stride + ((long)Y * a.ow + X) * a.pool_px);
 #pragma unroll
       for (int q = 0; q < C1 / 4; q++) {
         f32x4 m = reinterpret_cast<const f32x4 *>(m1 + (oy * R1 + ox) * P1)[q];
@@ -547,7 +547,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5))) void s
   for (int e = tid; e < T * T * (C3 / 4); e += 256) {
     const int m = e / (C3 / 4), q = e - m * (C3 / 4), oy = m / T, ox = m - oy * T, Y = y0 + oy, X = x0 + ox;
     if (Y < a.oh && X < a.ow)
-      reinterpret_cast<f32x4 *>(a.y + (long)ln * a.y_lane_stride + ((long)Y * a.ow + X) * C3)[q] =
+      reinterpret_cast<f32x4 *>(a.y + (long)ln * a.y_lane_stride + ((long)Y * a.ow + X) * a.y_px)[q] =
           reinterpret_cast<const f32x4 *>(st + m * C3)[q];
   }
 }
@@ -562,7 +562,8 @@ hipError_t launch_stem_block(const StemArgs &a, hipStream_t s) {
   // s1 is the 3x3 stride-2 pad-1 map of the input; float4 stores.
   if (a.oh != (a.ih - 1) / 2 + 1 || a.ow != (a.iw - 1) / 2 + 1) return hipErrorInvalidValue;
   if ((reinterpret_cast<uintptr_t>(a.pool) & 15) || (reinterpret_cast<uintptr_t>(a.y) & 15) ||
-      a.pool_lane_stride % 4 || a.y_lane_stride % 4)
+      a.pool_lane_stride % 4 || a.y_lane_stride % 4 || a.pool_px % 4 || a.y_px % 4 || a.pool_px < a.c1 ||
+      a.y_px < a.c3)
     return hipErrorInvalidValue;
   const long tiles = (long)a.lanes * ((a.oh + kStemT - 1) / kStemT) * ((a.ow + kStemT - 1) / kStemT);
   if (tiles == 0) return hipSuccess;

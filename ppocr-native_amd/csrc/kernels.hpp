@@ -477,8 +477,11 @@ struct StemArgs {
   const float *w1, *b1; int act1;
   const float *w2, *b2; int act2, first_end2;
   const float *w3, *b3; int act3, first_end3;
-  float *pool; long pool_lane_stride;
-  float *y; long y_lane_stride;
+  // Floats from one pixel to the next in each output: c1 and c3 for maps of
+  // their own, c1 + c3 when y sits c1 floats into the pool's pixels (one
+  // map of both, the next convolution's single source).
+  float *pool; long pool_lane_stride; int pool_px;
+  float *y; long y_lane_stride; int y_px;
 };
 // The stem block's kernels: C1 24, C2 12, C3 24, one activation, ReLU or
 // hard swish, for all three layers.

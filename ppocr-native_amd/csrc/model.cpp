@@ -89,6 +89,10 @@ struct Step {
   int m_ln = -1, m_fc1 = -1, m_fc2 = -1, m_add = -1;  // S_ENC_BLOCK: its MLP's operations
   int head2 = -1;          // the narrow transposed convolution folded into S_HEAD
   int st2 = -1, st3 = -1, st_pool = -1;  // S_STEM: the two 2x2 layers and the pool
+  // S_STEM: the pool's map also holds the second 2x2's channels after its
+  // own (one map, the next convolution's single source); only the pool's
+  // slot is written.
+  bool st_joint = false;
   // S_ELT as an upsample-add chain: its levels' operations, finest first
   // (chain[0] == op), and each level's residual-gate channelmul or -1.
   std::vector<int> chain, chain_gate;
@@ -210,7 +214,7 @@ struct Model {
   // coarser levels.
   std::vector<size_t> step_writes_extra(const Step &s) const {
     std::vector<size_t> r;
-    if (s.kind == S_STEM) r.push_back(plan.ops[s.st_pool].y);
+    if (s.kind == S_STEM && !s.st_joint) r.push_back(plan.ops[s.st_pool].y);
     for (size_t k = 1; k < s.chain.size(); k++) r.push_back(plan.ops[s.chain[k]].y);
     return r;
   }
@@ -285,7 +289,7 @@ std::vector<size_t> Model::step_reads(const Step &s) const {
 
 size_t Model::step_writes(const Step &s) const {
   if (s.kind == S_HEAD) return plan.ops[s.head2].y;
-  if (s.kind == S_STEM) return plan.ops[s.st3].y;
+  if (s.kind == S_STEM) return s.st_joint ? plan.ops[s.st_pool].y : plan.ops[s.st3].y;
   if (s.kind == S_MEAN && s.fc2 >= 0) return plan.ops[s.fc2].y;
   if ((s.kind == S_ENC_MLP || s.kind == S_ENC_BLOCK) && s.ln_out >= 0) return plan.ops[s.ln_out].y;
   if (s.kind == S_ENC_BLOCK) return plan.ops[s.m_add].y;
@@ -614,6 +618,21 @@ bool Model::build_steps(std::string &err) {
     a.kind = S_ENC_BLOCK;
     a.m_ln = m.op, a.m_fc1 = m.fc1, a.m_fc2 = m.fc2, a.m_add = m.add, a.ln_out = m.ln_out;
     steps.erase(steps.begin() + k);
+  }
+  // A stem block whose pool and second 2x2 only one convolution reads, as
+  // its two sources in that order: both written as one map (pool channels,
+  // then the 2x2's), the convolution's single source.
+  for (Step &st : steps) {
+    if (st.kind != S_STEM) continue;
+    const size_t yp = ops[st.st_pool].y, y3 = ops[st.st3].y;
+    if (readers[yp] != 1 || readers[y3] != 1) continue;
+    for (Step &c : steps) {
+      if (c.kind != S_GEMM || c.gate >= 0 || c.sources.size() != 2 || c.sources[0].slot != yp ||
+          c.sources[1].slot != y3 || c.sources[0].shift || c.sources[1].shift)
+        continue;
+      c.sources = {{yp, c.sources[0].c + c.sources[1].c, 0}};
+      st.st_joint = true;
+    }
   }
   // Chains of 2x upsample-adds, each level's map the next one's upsampled
   // source (a feature pyramid's top-down sums): one step, in the finest
@@ -965,7 +984,7 @@ bool Model::arrange(Batch &b, std::string &err) {
   b.home[p.in_slot] = place(p.pool[p.in_slot], SIZE_MAX);
   for (size_t i = 0; i < n; i++) {
     size_t y = step_writes(steps[i]);
-    b.home[y] = place(p.pool[y], i);
+    b.home[y] = place(p.pool[y] + (steps[i].st_joint ? p.pool[p.ops[steps[i].st3].y] : 0), i);
     for (size_t y2 : step_writes_extra(steps[i])) b.home[y2] = place(p.pool[y2], i);
     for (size_t sl : step_reads(steps[i]))
       if (last[sl] == i && std::find(freel.begin(), freel.end(), b.home[sl]) == freel.end()) {
@@ -1425,8 +1444,9 @@ void Model::build_launches(Batch &b) {
         a.first_end2 = o2.oc % 16 == 0 ? a.ow - a.ow % 4 : 0;
         a.w3 = W + o3.w0, a.b3 = o3.b1 ? W + o3.b0 : nullptr, a.act3 = o3.fused;
         a.first_end3 = o3.oc % 16 == 0 ? a.ow - a.ow % 4 : 0;
-        a.pool = b.dev(pl.y), a.pool_lane_stride = b.stride(pl.y);
-        a.y = Y, a.y_lane_stride = ys;
+        a.pool = b.dev(pl.y), a.pool_lane_stride = b.stride(pl.y), a.pool_px = a.c1;
+        a.y = Y, a.y_lane_stride = ys, a.y_px = a.c3;
+        if (s.st_joint) a.y = a.pool + a.c1, a.y_lane_stride = a.pool_lane_stride, a.pool_px = a.y_px = a.c1 + a.c3;
         b.launches.push_back({"stem_block", s.op, [a](hipStream_t st) { return launch_stem_block(a, st); }});
         b.launches.back().member_ops = {s.op, s.st2, s.st3, s.st_pool};
         std::sort(b.launches.back().member_ops.begin(), b.launches.back().member_ops.end());

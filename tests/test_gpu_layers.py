@@ -440,6 +440,34 @@ def test_stem_block(oracle, hw, biased, lanes):
     near([[g[1]] for g in got], [[w_[1]] for w_ in want])
 
 
+@pytest.mark.parametrize("hw,lanes", [((64, 70), 2), ((480, 452), 1)])
+def test_stem_block_joint_map(oracle, hw, lanes):
+    # The stem block whose pool and second 2x2 only the next 3x3 stride-2
+    # convolution reads (its two sources): one map of both, that
+    # convolution's single source. Within the MFMA tolerance.
+    rng = np.random.default_rng(8)
+    w1 = rng.normal(0, 0.3, (3, 3, 3, 24)).astype(np.float32)
+    w2 = rng.normal(0, 0.3, (2, 2, 24, 12)).astype(np.float32)
+    w3 = rng.normal(0, 0.3, (2, 2, 12, 24)).astype(np.float32)
+    w4 = rng.normal(0, 0.1, (3, 3, 48, 32)).astype(np.float32)
+    bs = [rng.normal(0, 0.3, c).astype(np.float32) for c in (24, 12, 24, 32)]
+
+    def build(b, t):
+        s1 = b.conv(t, w1, bs[0], k=(3, 3), s=(2, 2), pad=(1, 1, 1, 1), fused="hardswish")
+        s2 = b.conv(s1, w2, bs[1], k=(2, 2), pad=(0, 1, 0, 1), fused="hardswish")
+        s3 = b.conv(s2, w3, bs[2], k=(2, 2), pad=(0, 1, 0, 1), fused="hardswish")
+        return b.conv(b.maxpool(s1), w4, bs[3], k=(3, 3), s=(2, 2), pad=(1, 1, 1, 1), fused="hardswish", x2=s3)
+
+    h, w = hw
+    b = PlanBuilder(h, w, 3)
+    g = GpuModel.load(b.to_bytes([build(b, b.input)]))
+    names = [name for name, _ in g.launches()]
+    assert len(names) == 2 and names[0] == "stem_block", names
+    g.close()
+    got, want = both(build, (h, w, 3), oracle, lanes=lanes)
+    near(got, want)
+
+
 @pytest.mark.parametrize("oc1,hw", [(24, (9, 13)), (16, (6, 8))])
 def test_db_head_exact(oracle, oc1, hw):
     # A wide 2x2 transposed conv read only by a narrow one: one fused step.
