@@ -576,8 +576,10 @@ hipError_t launch_stem_block(const StemArgs &a, hipStream_t s) {
 }
 
 // Thread = one input pixel (iy, ix) of the first transposed convolution and
-// one of its four taps (ky, kx) (blockIdx.y = 2 ky + kx, so the weights a
-// wave reads are uniform: scalar operands from the scalar cache). It forms
+// one of its four taps (ky, kx) (one tap a workgroup, so the weights a wave
+// reads are uniform: scalar operands from the scalar cache; the four taps of
+// a block of 256 pixels are workgroups i, i + 8, i + 16, i + 24, which run
+// on one XCD and so read those pixels once from memory into its L2). It forms
 // the OC1 values of intermediate pixel (2iy+ky, 2ix+kx) as the engine's
 // pointwise call over one input row does (src/engine/layers.rs:600-680):
 // the bias first for a multiple-of-16 column count except the row's last
@@ -602,11 +604,12 @@ __global__ __launch_bounds__(256) void db_head_kernel(HeadArgs a) {
   // fuse their multiply-adds (columns below cols / 8 * 8 do).
   static_assert(COLS1 % 8 == 0, "every first-layer column fuses");
   typedef const __attribute__((address_space(4))) float cfloat;
-  const int ky = blockIdx.y >> 1, kx = blockIdx.y & 1;
+  const int blk = (int)blockIdx.x, tap = (blk >> 3) & 3, pb = (blk & 7) | ((blk >> 5) << 3);
+  const int ky = tap >> 1, kx = tap & 1;
   const int n0 = (ky * 2 + kx) * OC1;  // the columns of tap (ky, kx)
   cfloat *w1 = (cfloat *)a.w1 + n0, *w2 = (cfloat *)a.w2;
   const int per = a.ih * a.iw;
-  const int g = blockIdx.x * 256 + threadIdx.x;
+  const int g = pb * 256 + threadIdx.x;
   if (g >= a.lanes * per) return;
   const int ln = g / per;
   const int pix = g - ln * per;
@@ -665,7 +668,8 @@ hipError_t launch_db_head(const HeadArgs &a, hipStream_t s) {
   if (!head_supported(a.ic, a.oc1) || (reinterpret_cast<uintptr_t>(a.y) & 15) || (a.y_lane_stride & 3) ||
       (reinterpret_cast<uintptr_t>(a.x) & 15) || (a.x_lane_stride & 3) || n > 0x7fffff00L)
     return hipErrorInvalidValue;
-  dim3 grid((unsigned)((n + 255) / 256), 4), block(256);
+  // Pixel blocks in groups of 8, each group's four taps: 32 workgroups.
+  dim3 grid((unsigned)((n + 2047) / 2048 * 32)), block(256);
   const bool db = a.act1 == ACT_RELU && a.act2 == ACT_SIGMOID;
   switch (a.oc1) {
     case 8: hipLaunchKernelGGL((db_head_kernel<8, -1, -1>), grid, block, 0, s, a); break;
