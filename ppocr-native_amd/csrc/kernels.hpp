@@ -467,16 +467,16 @@ hipError_t launch_conv_direct(const DirectArgs &a, hipStream_t s);
 // The detector's stem block in one pass: s1 = 3x3 stride-2 convolution of
 // the RGB input (pad 1, 3 -> C1, the stem rule), then from s1 both a 2x2
 // stride-1 max pool cut at the bottom and right edges (`pool`) and two 2x2
-// stride-1 convolutions padded right and bottom, C1 -> C2 -> C3 (`y`). The
-// s1 map and the first 2x2's map stay in LDS. The input is ih x iw; s1 is
-// oh x ow, as are both outputs; first_end2/3: pixels left of it take the
-// bias first.
+// stride-1 convolutions padded right and bottom, C1 -> C2 -> C3 (`y`), on
+// MFMA with their biases added after the products. The s1 map and the first
+// 2x2's map stay in LDS. The input is ih x iw; s1 is oh x ow, as are both
+// outputs.
 struct StemArgs {
   int lanes, ih, iw, oh, ow, c1, c2, c3;
   const float *x; long x_lane_stride;
   const float *w1, *b1; int act1;
-  const float *w2, *b2; int act2, first_end2;
-  const float *w3, *b3; int act3, first_end3;
+  const float *w2, *b2; int act2;
+  const float *w3, *b3; int act3;
   // Floats from one pixel to the next in each output: c1 and c3 for maps of
   // their own, c1 + c3 when y sits c1 floats into the pool's pixels (one
   // map of both, the next convolution's single source).

@@ -1438,12 +1438,8 @@ void Model::build_launches(Batch &b) {
         a.c1 = int(op.oc), a.c2 = int(o2.oc), a.c3 = int(o3.oc);
         a.x = b.dev(op.x), a.x_lane_stride = b.stride(op.x);
         a.w1 = W + op.w0, a.b1 = bias, a.act1 = op.fused;
-        // kernels/dense.rs:38-147: a multiple-of-16 width starts from the
-        // bias except for the row's last ow % 4 pixels, else adds it last.
         a.w2 = W + o2.w0, a.b2 = o2.b1 ? W + o2.b0 : nullptr, a.act2 = o2.fused;
-        a.first_end2 = o2.oc % 16 == 0 ? a.ow - a.ow % 4 : 0;
         a.w3 = W + o3.w0, a.b3 = o3.b1 ? W + o3.b0 : nullptr, a.act3 = o3.fused;
-        a.first_end3 = o3.oc % 16 == 0 ? a.ow - a.ow % 4 : 0;
         a.pool = b.dev(pl.y), a.pool_lane_stride = b.stride(pl.y), a.pool_px = a.c1;
         a.y = Y, a.y_lane_stride = ys, a.y_px = a.c3;
         if (s.st_joint) a.y = a.pool + a.c1, a.y_lane_stride = a.pool_lane_stride, a.pool_px = a.y_px = a.c1 + a.c3;
