@@ -758,8 +758,8 @@ hipError_t launch_pool(const PoolArgs &a, hipStream_t s) {
 //     in order, fused multiply-adds for outputs below outputs / 8 * 8 and a
 //     separate product and sum past them, then the bias, then the activation
 //     (the engine's one-pixel 1x1 rule, src/engine/kernels/pointwise.rs:
-//     135-185), with the weights streamed through an LDS ring by direct
-//     loads (several chunks in flight: one workgroup moves them all).
+//     135-185), each thread streaming its outputs' weights from global
+//     memory into registers, many loads in flight.
 //
 // Counters go back to zero as soon as the last workgroup has read them, so
 // the next launch (or graph replay) finds them cleared. What workgroups hand
@@ -776,123 +776,90 @@ hipError_t launch_pool(const PoolArgs &a, hipStream_t s) {
 constexpr int kMeanSlice = 32;    // channels a summing workgroup covers
 constexpr int kMeanStrides = 8;   // loads in flight per thread while summing
 constexpr int kMeanMaxChunks = 64;
-constexpr int kSeBuf = 8192;      // floats of one LDS buffer of the SE ring
-constexpr int kSeLoads = kSeBuf / 1024;  // direct loads per thread per buffer
-constexpr int kSeRingMax = 4;
-// LDS floats for a layer's m inputs: read sixteen at a time from rows a
-// multiple of four, so up to fifteen past the last (loaded, never used).
-__host__ __device__ inline int se_in_floats(int m) { return ((m + 15) & ~15) + 16; }
+// LDS floats for a layer's m inputs: read 64 at a time, one iteration
+// (up to 128 inputs) ahead, so up to 255 past the last (never used).
+__host__ __device__ inline int se_in_floats(int m) { return ((m + 127) & ~127) + 128; }
 
 // One 1x1 layer over one pixel: out_j = act(sum_i in_i * w[i][j] + bias_j)
-// for j < n, inputs `in` (m floats, 16-byte aligned, readable 16 past m) in
-// LDS. The weights are packed in groups of four inputs, each output's four
-// weights together: w[((i / 4) * n + j) * 4 + i % 4], zero past m, so one
-// 16-byte LDS read gives a thread four inputs' weights. They travel in
-// chunks of whole groups (a multiple of 16 inputs, or of 4 for layers over
-// 512 wide, at most kSeBuf floats) through `nb` LDS buffers by direct loads,
-// nb - 1 chunks in flight; se_prefetch issues the first ones (the caller may
-// do so early), se_layer the rest. Each thread keeps NO outputs' sums
-// (j = t + 256 o) and reads sixteen inputs' weights while it sums the
-// previous sixteen. Reads past the chunk's last group are clamped to it and
-// their products dropped. FUSED: every output is below n / 8 * 8 (the
-// engine's fused columns); else each output picks fused or separate product
-// and sum. Outputs go to `out` (LDS or global memory).
-//
-// The waits count this wave's vector memory operations, which complete in
-// the order they were issued: any issued after a chunk's loads only make a
-// wait for that chunk more conservative.
-__host__ __device__ inline int se_rows(int n) {
-  const int r = kSeBuf / n;
-  return r >= 16 ? r & ~15 : r & ~3;
-}
-
-__device__ __forceinline__ void se_issue(const float *w, int m, int n, int q, float *ring, int nb) {
-  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const long total4 = (long)((m + 3) / 4) * n;  // float4 groups of the packed weights
-  const long g0 = (long)q * se_rows(n) * n / 4;
-  float *dst = ring + (q % nb) * kSeBuf;
-#pragma unroll
-  for (int l = 0; l < kSeLoads; l++) {
-    long g = g0 + (l * 4 + wave) * 64 + lane;
-    if (g >= total4) g = g0;  // past the weights: any valid group (never read)
-    __builtin_amdgcn_global_load_lds((const void *)(w + 4 * g), (lds_void *)(dst + (l * 4 + wave) * 256), 16, 0, 0);
-  }
-}
-
-// The chunks a layer's ring takes before its first multiply-add.
-__device__ __forceinline__ void se_prefetch(const float *w, int m, int n, float *ring, int nb) {
-  const int chunks = (m + se_rows(n) - 1) / se_rows(n);
-  for (int q = 0; q < nb - 1 && q < chunks; q++) se_issue(w, m, n, q, ring, nb);
-}
-
-template <int NO, bool FUSED>
+// for j < n, inputs `in` (m floats in LDS, readable as se_in_floats says).
+// The weights are packed in groups of four inputs, each output's four
+// weights together: w[((i / 4) * n + j) * 4 + i % 4], zero past m. Each
+// thread keeps NO outputs' sums (j = t + 256 o) and loads its outputs'
+// weights, a 16-byte group at a time, from global memory straight into a
+// rotating queue of QD groups in registers: the loads of a wave complete in
+// the order they were issued, so each group's multiply-adds wait for that
+// group alone while the next QD - 1 are in flight. `pre` runs after the
+// first QD loads have gone out (in every wave, those without outputs too,
+// which then return): the caller's wait for the layer's inputs overlaps
+// their latency. The inputs come from LDS 64 to a register and are
+// broadcast one at a time (readlane). Every sum runs from zero over the
+// inputs in order; FUSED: every output is below n / 8 * 8 (the engine's
+// fused columns); else each output picks fused or separate product and
+// sum. Outputs go to `out` (LDS or global memory).
+template <int NO, bool FUSED, typename Pre>
 __device__ __forceinline__ void se_layer_n(const float *w, const float *bias, int m, int n, int code,
-                                           const float *in, float *out, float *ring, int nb,
-                                           const float *w_next, int n_next) {
-  const int t = threadIdx.x;
-  const int rows = se_rows(n);
-  const int chunks = (m + rows - 1) / rows;
-  const int fused_end = n / 8 * 8;
+                                           const float *in, float *out, Pre pre) {
+  constexpr int QD = 32 / NO;             // groups in flight: 128 registers of weights
+  constexpr int IT = QD > 16 ? QD : 16;   // groups per iteration, a multiple of QD and of 16
+  constexpr int XR = IT / 16;             // input registers per iteration
+  const int t = threadIdx.x, lane = t & 63;
+  if (__builtin_amdgcn_readfirstlane(t >> 6) * 64 >= n) {
+    pre();
+    return;
+  }
+  const int groups = (m + 3) / 4, fused_end = n / 8 * 8;
+  const f32x4 *wv = reinterpret_cast<const f32x4 *>(w);
   bool has[NO], fz[NO];
   int col[NO];
 #pragma unroll
   for (int o = 0; o < NO; o++) {
     const int j = t + 256 * o;
-    has[o] = j < n, fz[o] = j < fused_end, col[o] = (j < n ? j : n - 1) * 4;
+    has[o] = j < n, fz[o] = j < fused_end, col[o] = j < n ? j : n - 1;
   }
   float acc[NO];
 #pragma unroll
   for (int o = 0; o < NO; o++) acc[o] = 0.0f;
-  for (int q = 0; q < chunks; q++) {
-    if (q + nb - 1 < chunks) se_issue(w, m, n, q + nb - 1, ring, nb);
-    ring_wait_chunks<kSeLoads, kSeRingMax - 1>(min(nb - 1, chunks - 1 - q));
-    ring_barrier();
-    const float *buf = ring + (q % nb) * kSeBuf;
-    const float *xin = in + q * rows;
-    const int cnt = min(rows, m - q * rows), last = (cnt + 3) / 4 - 1;  // last group of the chunk
-    auto fetch = [&](int u0, f32x4 (&xv)[4], f32x4 (&wv)[4][NO]) {
+  // Queue slot s holds group g with g % QD == s; past the last group the
+  // loads repeat the last one (never used).
+  f32x4 q[QD][NO];
 #pragma unroll
-      for (int v = 0; v < 4; v++) {
-        xv[v] = *reinterpret_cast<const f32x4 *>(xin + u0 + 4 * v);
-        const int g = min(u0 / 4 + v, last);
+  for (int s = 0; s < QD; s++) {
+    const f32x4 *row = wv + (long)min(s, groups - 1) * n;
 #pragma unroll
-        for (int o = 0; o < NO; o++) wv[v][o] = *reinterpret_cast<const f32x4 *>(buf + g * 4 * n + col[o]);
-      }
-    };
-    // The multiply-adds of sixteen inputs in order (all, or the first `live`).
-    auto sum = [&](const f32x4 (&xv)[4], const f32x4 (&wv)[4][NO], int live) {
-#pragma unroll
-      for (int v = 0; v < 4; v++)
-#pragma unroll
-        for (int e = 0; e < 4; e++)
-          if (live >= 16 || 4 * v + e < live)
-#pragma unroll
-            for (int o = 0; o < NO; o++) {
-              const float x = xv[v][e], wgt = wv[v][o][e];
-              acc[o] = FUSED || fz[o] ? fmaf(wgt, x, acc[o]) : acc[o] + x * wgt;
-            }
-    };
-    const int full = cnt / 16;  // whole batches of sixteen inputs
-    f32x4 xa[4], wa[4][NO], xb[4], wb[4][NO];
-    fetch(0, xa, wa);
-    int k = 0;
-    for (; k + 2 <= full; k += 2) {
-      fetch(16 * (k + 1), xb, wb);
-      sum(xa, wa, 16);
-      fetch(16 * min(k + 2, full), xa, wa);
-      sum(xb, wb, 16);
-    }
-    if (k < full) {
-      sum(xa, wa, 16);
-      k++;
-      fetch(16 * k, xa, wa);
-    }
-    if (16 * k < cnt) sum(xa, wa, cnt - 16 * k);
-    ring_barrier();
+    for (int o = 0; o < NO; o++) q[s][o] = row[col[o]];
   }
-  // Every buffer is free: the next layer's first chunks go out before this
-  // layer's outputs are written.
-  if (w_next) se_prefetch(w_next, n, n_next, ring, nb);
+  pre();
+  float xr[XR];
+#pragma unroll
+  for (int k = 0; k < XR; k++) xr[k] = in[64 * k + lane];
+  auto iteration = [&](int g0, auto tail_c) {
+    constexpr bool TAIL = decltype(tail_c)::value;
+    float xn[XR];  // the next iteration's inputs
+#pragma unroll
+    for (int k = 0; k < XR; k++) xn[k] = in[4 * (g0 + IT) + 64 * k + lane];
+#pragma unroll
+    for (int s = 0; s < IT; s++) {
+      const int slot = s % QD;
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        if (TAIL && 4 * (g0 + s) + e >= m) continue;
+        const float x = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(xr[s / 16]), (4 * s + e) & 63));
+#pragma unroll
+        for (int o = 0; o < NO; o++) {
+          const float wgt = q[slot][o][e];
+          acc[o] = FUSED || fz[o] ? fmaf(wgt, x, acc[o]) : acc[o] + x * wgt;
+        }
+      }
+      const f32x4 *row = wv + (long)min(g0 + s + QD, groups - 1) * n;
+#pragma unroll
+      for (int o = 0; o < NO; o++) q[slot][o] = row[col[o]];
+    }
+#pragma unroll
+    for (int k = 0; k < XR; k++) xr[k] = xn[k];
+  };
+  const int full = m / (4 * IT);  // iterations whose inputs are all below m
+  for (int it = 0; it < full; it++) iteration(it * IT, std::false_type{});
+  if (4 * IT * full < m) iteration(full * IT, std::true_type{});
 #pragma unroll
   for (int o = 0; o < NO; o++) {
     if (has[o]) {
@@ -903,22 +870,20 @@ __device__ __forceinline__ void se_layer_n(const float *w, const float *bias, in
   }
 }
 
-template <int NO>
-__device__ __forceinline__ void se_layer_f(const float *w, const float *bias, int m, int n, int code,
-                                           const float *in, float *out, float *ring, int nb,
-                                           const float *w_next, int n_next) {
-  if (n % 8 == 0) se_layer_n<NO, true>(w, bias, m, n, code, in, out, ring, nb, w_next, n_next);
-  else se_layer_n<NO, false>(w, bias, m, n, code, in, out, ring, nb, w_next, n_next);
-}
-
-// The layer whose first chunks se_prefetch has issued; w_next (n_next
-// outputs, over this layer's n) is the next layer's, prefetched at the end.
+template <typename Pre>
 __device__ __forceinline__ void se_layer(const float *w, const float *bias, int m, int n, int code,
-                                         const float *in, float *out, float *ring, int nb,
-                                         const float *w_next = nullptr, int n_next = 0) {
-  if (n <= 256) se_layer_f<1>(w, bias, m, n, code, in, out, ring, nb, w_next, n_next);
-  else if (n <= 512) se_layer_f<2>(w, bias, m, n, code, in, out, ring, nb, w_next, n_next);
-  else se_layer_f<4>(w, bias, m, n, code, in, out, ring, nb, w_next, n_next);
+                                         const float *in, float *out, Pre pre) {
+  const bool fused = n % 8 == 0;
+  if (n <= 256) {
+    if (fused) se_layer_n<1, true>(w, bias, m, n, code, in, out, pre);
+    else se_layer_n<1, false>(w, bias, m, n, code, in, out, pre);
+  } else if (n <= 512) {
+    if (fused) se_layer_n<2, true>(w, bias, m, n, code, in, out, pre);
+    else se_layer_n<2, false>(w, bias, m, n, code, in, out, pre);
+  } else {
+    if (fused) se_layer_n<4, true>(w, bias, m, n, code, in, out, pre);
+    else se_layer_n<4, false>(w, bias, m, n, code, in, out, pre);
+  }
 }
 
 // Whether this workgroup is the last of `of` to count in on `*cnt` (then the
@@ -949,14 +914,16 @@ __device__ __forceinline__ T get_shared(const T *p) {
   return __hip_atomic_load(const_cast<T *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <int V>
+// SE: some job of the group has a squeeze-and-excite (the layers' register
+// queues are compiled in only then).
+template <int V, bool SE>
 __global__ __launch_bounds__(256) void mean_se(Group<MeanJob> grp) {
   extern __shared__ __attribute__((aligned(16))) float dyn[];
   __shared__ double red[256 * V];
   __shared__ int flag;
   const int prob = group_problem(grp);
   const MeanJob &j = grp.a[prob];
-  const int cs = grp.x[prob] & 0xffff, nb = grp.x[prob] >> 16, S = grp.y[prob];
+  const int cs = grp.x[prob], S = grp.y[prob];
   const int c = j.c, P = j.chunks, t = threadIdx.x;
   const int K = j.x ? P : 1;
   const int blk = (int)blockIdx.x - grp.first[prob];
@@ -965,11 +932,6 @@ __global__ __launch_bounds__(256) void mean_se(Group<MeanJob> grp) {
   const int k = r / S, s = r - k * S;
   const int c0 = s * cs, cw = min(cs, c - c0);
   const MeanShape sh = mean_shape(j.x != nullptr, j.pixels, c, j.lanes, j.x ? 0 : P, j.has_se != 0);
-  // With an SE, any workgroup may be the one that runs its layers: each
-  // starts the first layer's weights on their way into its LDS ring now,
-  // while it sums (those that are not last drop them).
-  float *ring = dyn + se_in_floats(c) + se_in_floats(j.se.mid);
-  if (j.has_se) se_prefetch(j.se.w1, c, j.se.mid, ring, nb);
   double *pl = reinterpret_cast<double *>(j.work) + (long)ln * P * c;
   int *cnt = j.count;  // [lanes] for the SE, then [lanes][S] for the slices
   double tot = 0.0;  // threads below cw: the channel's sum
@@ -1052,26 +1014,43 @@ __global__ __launch_bounds__(256) void mean_se(Group<MeanJob> grp) {
   }
   const float mean = (float)(tot / (double)j.pixels);
   float *yl = j.y + (long)ln * j.y_lane_stride;
-  if (!j.has_se) {
+  if (!SE || !j.has_se) {
     if (t < cw) yl[c0 + t] = mean;
     return;
   }
   // The layers read their inputs sixteen at a time: room for 16 past each.
   float *in = dyn;                                   // c floats
-  float *hid = dyn + se_in_floats(c);                // mid floats, then the ring
+  float *hid = dyn + se_in_floats(c);                // mid floats
+  const float *means = nullptr;
   if (S > 1) {
-    float *means = j.work + sh.means_off + (long)ln * c;
-    if (t < cw) put_shared(means + c0 + t, mean);
+    float *mw = j.work + sh.means_off + (long)ln * c;
+    if (t < cw) put_shared(mw + c0 + t, mean);
     if (!count_in(cnt + ln, S, &flag)) return;
-    for (int i = t; i < c; i += 256) in[i] = get_shared(means + i);
+    means = mw;
   } else if (t < cw) {
     in[t] = mean;
   }
-  __syncthreads();
-  const SeArgs &se = j.se;
-  se_layer(se.w1, se.b1, c, se.mid, se.act1, in, hid, ring, nb, se.w2, se.cout);
-  __syncthreads();
-  se_layer(se.w2, se.b2, se.mid, se.cout, se.act2, hid, yl, ring, nb);
+  if constexpr (SE) {
+    const SeArgs &se = j.se;
+    // Each layer's first weights go out before the wait for its inputs: the
+    // lane's means (read from the other workgroups' stores, their loads
+    // issued first so that the wait covers them alone), then the first
+    // layer's outputs (published by the barrier).
+    float mv[4];  // c <= 1024
+    if (means) {
+#pragma unroll
+      for (int k = 0; k < 4; k++) mv[k] = t + 256 * k < c ? get_shared(means + t + 256 * k) : 0.0f;
+    }
+    se_layer(se.w1, se.b1, c, se.mid, se.act1, in, hid, [&] {
+      if (means) {
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+          if (t + 256 * k < c) in[t + 256 * k] = mv[k];
+      }
+      __syncthreads();
+    });
+    se_layer(se.w2, se.b2, se.mid, se.cout, se.act2, hid, yl, [] { __syncthreads(); });
+  }
 }
 
 __host__ __device__ MeanShape mean_shape(bool has_x, int pixels, int c, int lanes, int dw_rows, bool has_se) {
@@ -1101,15 +1080,8 @@ __host__ __device__ MeanShape mean_shape(bool has_x, int pixels, int c, int lane
   return m;
 }
 
-// The SE ring buffers one layer of `n` outputs over `m` inputs needs.
-static int se_chunks(int m, int n) {
-  const int rows = se_rows(n);
-  return rows > 0 ? (m + rows - 1) / rows : 0;
-}
-
 bool se_supported(int c, int mid, int cout) {
-  return c >= 1 && mid >= 1 && cout >= 1 && c <= 1024 && mid <= 1024 && cout <= 1024 && se_chunks(c, mid) > 0 &&
-         se_chunks(mid, cout) > 0;
+  return c >= 1 && mid >= 1 && cout >= 1 && c <= 1024 && mid <= 1024 && cout <= 1024;
 }
 
 hipError_t launch_mean_group(const MeanJob *jobs, int n, hipStream_t s) {
@@ -1117,9 +1089,10 @@ hipError_t launch_mean_group(const MeanJob *jobs, int n, hipStream_t s) {
   Group<MeanJob> g{};
   long blocks = 0;
   size_t shm = 0;
-  bool vec = true;
+  bool vec = true, any_se = false;
   for (int p = 0; p < n; p++) {
     const MeanJob &j = jobs[p];
+    any_se = any_se || j.has_se;
     if (j.lanes < 1 || j.c < 1 || j.pixels < 1 || !j.work || !j.y) return hipErrorInvalidValue;
     if (!j.x && j.chunks < 1) return hipErrorInvalidValue;
     if ((reinterpret_cast<uintptr_t>(j.work) & 15) != 0) return hipErrorInvalidValue;
@@ -1130,19 +1103,16 @@ hipError_t launch_mean_group(const MeanJob *jobs, int n, hipStream_t s) {
       jj.chunks = m.k;
       vec = vec && j.c % 4 == 0 && (reinterpret_cast<uintptr_t>(j.x) & 15) == 0 && j.x_lane_stride % 4 == 0;
     }
-    int nb = 0;
     if (j.has_se) {
       const SeArgs &se = j.se;
       if (!se.w1 || !se.w2 || !se_supported(j.c, se.mid, se.cout)) return hipErrorInvalidValue;
       if (((reinterpret_cast<uintptr_t>(se.w1) | reinterpret_cast<uintptr_t>(se.w2)) & 15) != 0)
         return hipErrorInvalidValue;
-      nb = std::min(kSeRingMax, std::max(se_chunks(j.c, se.mid), se_chunks(se.mid, se.cout)));
-      nb = std::max(nb, 1);
       const size_t in = size_t(se_in_floats(j.c)) + size_t(se_in_floats(se.mid));
-      shm = std::max(shm, (in + size_t(nb) * kSeBuf) * sizeof(float));
+      shm = std::max(shm, in * sizeof(float));
     }
     g.first[p] = (int)blocks;
-    g.x[p] = m.cs | (nb << 16);
+    g.x[p] = m.cs;
     g.y[p] = m.S;
     g.a[p] = jj;
     blocks += long(j.lanes) * m.S * m.k;
@@ -1150,15 +1120,15 @@ hipError_t launch_mean_group(const MeanJob *jobs, int n, hipStream_t s) {
   }
   g.n = n;
   g.first[n] = (int)blocks;
-  const void *fn = vec ? reinterpret_cast<const void *>(mean_se<4>) : reinterpret_cast<const void *>(mean_se<1>);
-  if (shm > 64 * 1024) {
-    hipError_t e = allow_lds(fn, (int)(kMaxLds - 256 * 4 * sizeof(double) - 64));
-    if (e != hipSuccess) return e;
-  }
-  if (vec)
-    hipLaunchKernelGGL(mean_se<4>, dim3((unsigned)blocks), dim3(256), shm, s, g);
+  const dim3 grid((unsigned)blocks);
+  if (vec && any_se)
+    hipLaunchKernelGGL((mean_se<4, true>), grid, dim3(256), shm, s, g);
+  else if (vec)
+    hipLaunchKernelGGL((mean_se<4, false>), grid, dim3(256), shm, s, g);
+  else if (any_se)
+    hipLaunchKernelGGL((mean_se<1, true>), grid, dim3(256), shm, s, g);
   else
-    hipLaunchKernelGGL(mean_se<1>, dim3((unsigned)blocks), dim3(256), shm, s, g);
+    hipLaunchKernelGGL((mean_se<1, false>), grid, dim3(256), shm, s, g);
   return hipGetLastError();
 }
 

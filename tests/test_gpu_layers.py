@@ -298,8 +298,9 @@ def test_mean_se_launch_shapes(oracle, hw, c, lanes, dw):
     # channel slices (the last chunk of a slice joins, the last slice of a
     # lane runs the SE layers), channels not a multiple of four (scalar
     # loads), a depthwise convolution's partial rows joined in slices of 4 to
-    # 32 channels, and SE layers streamed through the LDS ring in one to
-    # four buffers. The gate is the CPU's to the bit.
+    # 32 channels, and SE layers of one, two and four outputs a thread, fused
+    # and separate products, inputs a multiple of four or not. The gate is
+    # the CPU's to the bit.
     mid = max(1, c // 4)
     w1 = RNG.normal(0, 1 / np.sqrt(c), (1, 1, c, mid)).astype(np.float32)
     b1 = RNG.normal(0, 0.3, mid).astype(np.float32)
