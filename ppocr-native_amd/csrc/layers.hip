@@ -799,7 +799,12 @@ __host__ __device__ inline int se_in_floats(int m) { return ((m + 127) & ~127) +
 template <int NO, bool FUSED, typename Pre>
 __device__ __forceinline__ void se_layer_n(const float *w, const float *bias, int m, int n, int code,
                                            const float *in, float *out, Pre pre) {
-  constexpr int QD = 32 / NO;             // groups in flight: 128 registers of weights
+  // Groups in flight: 32 registers of weights. Queues of 16 / NO and
+  // 32 / NO groups measured slower on the SEs of both networks: their
+  // registers cost the summing workgroups occupancy (the kernel's register
+  // count is the deepest queue's), and the layers' own loads gained nothing
+  // from the depth.
+  constexpr int QD = 8 / NO;
   constexpr int IT = QD > 16 ? QD : 16;   // groups per iteration, a multiple of QD and of 16
   constexpr int XR = IT / 16;             // input registers per iteration
   const int t = threadIdx.x, lane = t & 63;
