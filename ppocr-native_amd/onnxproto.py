@@ -10,7 +10,9 @@ i = 3, s = 4, t = 5, floats = 7, ints = 8, type = 20; TensorProto dims = 1,
 data_type = 2, float_data = 4, int32_data = 5, int64_data = 7, name = 8,
 raw_data = 9, double_data = 10; ValueInfoProto name = 1, type = 2;
 TypeProto tensor_type = 1; Tensor elem_type = 1, shape = 2;
-TensorShapeProto dim = 1; Dimension dim_value = 1, dim_param = 2.
+TensorShapeProto dim = 1; Dimension dim_value = 1, dim_param = 2,
+denotation = 3 (ignored); TensorProto external_data = 13 and
+data_location = 14 are refused with the tensor's name.
 
 The graph comes back as plain Python objects (`Graph`, `Node`, `Value`)
 with initializers as numpy arrays; `encode_model` writes such a graph back
@@ -112,7 +114,7 @@ def _packed_floats(wt: int, v) -> list[float]:
 
 
 def read_tensor(buf: bytes) -> tuple[str, np.ndarray]:
-    dims, dtype, name, raw = [], 1, "", None
+    dims, dtype, name, raw, external = [], 1, "", None, False
     floats, ints32, ints64, doubles = [], [], [], []
     for num, wt, v in _fields(buf):
         if num == 1:
@@ -131,6 +133,11 @@ def read_tensor(buf: bytes) -> tuple[str, np.ndarray]:
             raw = v
         elif num == 10:
             doubles += list(struct.unpack(f"<{len(v) // 8}d", v)) if wt == 2 else [struct.unpack("<d", v)[0]]
+        elif num == 13 or (num == 14 and v == 1):  # external_data, data_location = EXTERNAL
+            external = True
+    if external:
+        raise ValueError(f"tensor {name or '(unnamed)'} keeps its data in an external file, which this "
+                         "reader does not follow; save the model with its weights inside")
     if dtype not in DTYPES:
         raise ValueError(f"tensor {name}: unsupported data type {dtype}")
     np_type = np.dtype(DTYPES[dtype]).newbyteorder("<")
@@ -208,9 +215,13 @@ def _read_value(buf: bytes) -> Value:
                         for n4, _, dim in _fields(tv):
                             if n4 != 1:
                                 continue
-                            d = None
+                            d = None  # neither set: an unknown extent
                             for n5, _, dv in _fields(dim):
-                                d = dv if n5 == 1 else dv.decode()
+                                if n5 == 1:
+                                    d = _signed(dv)
+                                elif n5 == 2:
+                                    d = dv.decode()
+                                # field 3, the denotation, names the axis and changes nothing
                             val.dims.append(d)
     return val
 

@@ -195,13 +195,16 @@ class PlanBuilder:
         op = Op("concatc", a.slot, 0, a.c, a.c + b.c, x2=b.slot, n2=b.c)
         return self.emit(op, a.h, a.w, a.c + b.c)
 
-    def upsample(self, x: Tensor, f: int) -> Tensor:
-        return self.emit(Op("upsample", x.slot, 0, x.c, x.c, sh=f, sw=f), x.h * f, x.w * f, x.c)
+    def upsample(self, x: Tensor, f) -> Tensor:
+        """Nearest upsampling by a whole factor, or (height, width) factors."""
+        fh, fw = (f, f) if isinstance(f, int) else f
+        return self.emit(Op("upsample", x.slot, 0, x.c, x.c, sh=fh, sw=fw), x.h * fh, x.w * fw, x.c)
 
-    def upsampleadd(self, x: Tensor, addend: Tensor, f: int) -> Tensor:
-        assert (addend.h, addend.w, addend.c) == (x.h * f, x.w * f, x.c)
-        op = Op("upsampleadd", x.slot, 0, x.c, x.c, x2=addend.slot, sh=f, sw=f)
-        return self.emit(op, x.h * f, x.w * f, x.c)
+    def upsampleadd(self, x: Tensor, addend: Tensor, f) -> Tensor:
+        fh, fw = (f, f) if isinstance(f, int) else f
+        assert (addend.h, addend.w, addend.c) == (x.h * fh, x.w * fw, x.c)
+        op = Op("upsampleadd", x.slot, 0, x.c, x.c, x2=addend.slot, sh=fh, sw=fw)
+        return self.emit(op, x.h * fh, x.w * fw, x.c)
 
     def layernorm(self, x: Tensor, gamma, beta, eps: float) -> Tensor:
         wts = np.concatenate([gamma, beta, [eps]]).astype(np.float32)
@@ -224,19 +227,26 @@ class PlanBuilder:
                 w=self.put(weight), b=b)
         return self.emit(op, x.h * kh, x.w * kw, oc)
 
-    def ctcargmax(self, x: Tensor, weight: np.ndarray, bias: np.ndarray) -> Tensor:
-        """CTC head keeping each step's best class; weight is [ic][vocab].
-        Panels of 16 columns, zero weights and -1e30 bias past the vocabulary
-        (tools/export_ocr.py:716-724)."""
+    def ctc(self, x: Tensor, weight: np.ndarray, bias: np.ndarray, argmax: bool = True) -> Tensor:
+        """CTC head over [ic][vocab] weights: each step's best class and its
+        probability (`ctcargmax`), or every class's probability (`ctchead`).
+        The engine reads the weights in panels of 16 columns, zero weights and
+        -1e30 bias past the vocabulary (tools/export_ocr.py:716-724)."""
         ci, vocab = weight.shape
         columns = -(-vocab // 16) * 16
         padded = np.zeros((ci, columns), np.float32)
         padded[:, :vocab] = weight
         panels = padded.reshape(ci, columns // 16, 16).transpose(1, 0, 2)
         b = np.full(columns, -1e30, np.float32)
-        b[:vocab] = bias
-        op = Op("ctcargmax", x.slot, 0, ci, 2, n2=vocab, w=self.put(panels), b=self.put(b))
-        return self.emit(op, x.h, x.w, 2)
+        b[:vocab] = np.asarray(bias, np.float32).reshape(-1)
+        if argmax:
+            op = Op("ctcargmax", x.slot, 0, ci, 2, n2=vocab, w=self.put(panels), b=self.put(b))
+            return self.emit(op, x.h, x.w, 2)
+        op = Op("ctchead", x.slot, 0, ci, vocab, w=self.put(panels), b=self.put(b))
+        return self.emit(op, x.h, x.w, vocab)
+
+    def ctcargmax(self, x: Tensor, weight: np.ndarray, bias: np.ndarray) -> Tensor:
+        return self.ctc(x, weight, bias, argmax=True)
 
     def to_bytes(self, outputs: list[Tensor]) -> bytes:
         weights = np.concatenate(self.blob) if self.blob else np.zeros(0, np.float32)

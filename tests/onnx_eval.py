@@ -95,6 +95,8 @@ def evaluate(g: Graph, x: np.ndarray) -> list[np.ndarray]:
             r = 1 / (1 + np.exp(-i[0]))
         elif t == "HardSigmoid":
             r = np.clip(a.get("alpha", 0.2) * i[0] + a.get("beta", 0.5), 0, 1)
+        elif t == "HardSwish":
+            r = i[0] * np.clip(i[0] / 6 + 0.5, 0, 1)
         elif t == "Erf":
             r = erf(i[0])
         elif t in ("Add", "Sub", "Mul", "Div", "Pow"):
@@ -103,11 +105,15 @@ def evaluate(g: Graph, x: np.ndarray) -> list[np.ndarray]:
         elif t == "Sqrt":
             r = np.sqrt(i[0])
         elif t == "ReduceMean":
-            r = i[0].mean(axis=tuple(a["axes"]), keepdims=bool(a.get("keepdims", 1)))
+            axes = a["axes"] if "axes" in a else [int(k) for k in i[1]]
+            r = i[0].mean(axis=tuple(axes), keepdims=bool(a.get("keepdims", 1)))
         elif t == "GlobalAveragePool":
             r = i[0].mean(axis=(2, 3), keepdims=True)
         elif t == "Resize":
-            fh, fw = (int(s) for s in i[2][2:])
+            if len(i) > 3 and i[3] is not None:
+                fh, fw = (int(s) // d for s, d in zip(i[3][2:], i[0].shape[2:]))
+            else:
+                fh, fw = (int(s) for s in i[2][2:])
             r = np.repeat(np.repeat(i[0], fh, axis=2), fw, axis=3)
         elif t == "ConvTranspose":
             w = i[1]
@@ -140,7 +146,12 @@ def evaluate(g: Graph, x: np.ndarray) -> list[np.ndarray]:
                 sl[int(ax)] = slice(int(s0), int(min(s1, 2 ** 62)))
             r = data[tuple(sl)]
         elif t == "Squeeze":
-            r = np.squeeze(i[0], axis=tuple(a["axes"]))
+            r = np.squeeze(i[0], axis=tuple(a["axes"] if "axes" in a else [int(k) for k in i[1]]))
+        elif t == "Gather":
+            r = np.take(i[0], i[1], axis=a.get("axis", 0))
+        elif t == "Flatten":
+            ax = a.get("axis", 1)
+            r = i[0].reshape(int(np.prod(i[0].shape[:ax])), -1)
         elif t == "Unsqueeze":
             r = np.expand_dims(i[0], axis=tuple(a["axes"]))
         elif t == "Reshape":
