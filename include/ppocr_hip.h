@@ -55,7 +55,10 @@ int ppocr_gpu_set_sizes(ppocr_gpu_model *model, const size_t *hw, size_t n_lanes
                         size_t err_len);
 
 /* Replaces `GpuModel::max_lanes` (src/engine/gpu/mod.rs:184): the most lanes one
- * run takes. */
+ * run takes, bounded by memory rather than descriptors: lanes of the first
+ * lane's size whose buffers (all at once, plus a quarter) fit in 80 % of the
+ * device's memory, and whose largest buffer over all lanes has fewer than
+ * 2^31 elements. ppocr_gpu_set_sizes refuses more lanes with a message. */
 size_t ppocr_gpu_max_lanes(const ppocr_gpu_model *model);
 
 /* Lanes the next run computes (no reference counterpart: the Rust model keeps
@@ -171,8 +174,10 @@ int ppocr_hip_channel_mean(const float *x, float *y, size_t pixels, size_t c, vo
  * GPU holds until the process ends (2 MiB and 4 KiB), so `c` is limited to
  * 4096 channels; larger shapes return nonzero with the reason in `err`.
  * Calls that overlap on one GPU share that array and race; calls in order
- * (one stream, or synchronised) do not. Same kernel and same results, bit
- * for bit, as ppocr_hip_channel_mean. */
+ * (one stream, or synchronised) do not. Each call zeroes the counters it
+ * uses on its stream before its kernel, so one overlapped or aborted call
+ * does not spoil the calls after it. Same kernel and same results, bit for
+ * bit, as ppocr_hip_channel_mean. */
 int ppocr_hip_channel_mean_noalloc(const float *x, float *y, size_t pixels, size_t c, void *stream, char *err,
                                    size_t err_len);
 

@@ -96,7 +96,8 @@ __global__ void zero_ints(int *p, int n) {
   if (i < n) p[i] = 0;
 }
 
-// This device's `scratch`, its counters zeroed (on `s`) the first time.
+// This device's `scratch`, its counters zeroed (on `s`) the first time
+// (each call also zeroes the counters it uses).
 hipError_t scratch_on_device(double **out, hipStream_t s) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
@@ -223,6 +224,15 @@ int ppocr_hip_channel_mean_noalloc(const float *x, float *y, size_t pixels, size
   j.y = y;
   j.work = reinterpret_cast<float *>(sc);
   j.count = reinterpret_cast<int *>(sc + kNoAllocPartials);
+  // The kernel leaves its counters at zero, but a call that overlapped
+  // another or was cut short may not have: every call starts them at zero
+  // on its own stream (a fill kernel, so the call stays capturable).
+  if (m.count_n) {
+    hipLaunchKernelGGL(zero_ints, dim3(unsigned((m.count_n + 255) / 256)), dim3(256), 0, hipStream_t(stream),
+                       j.count, int(m.count_n));
+    e = hipGetLastError();
+    if (e != hipSuccess) return fail(int(e), hipGetErrorString(e));
+  }
   e = launch_mean_group(&j, 1, hipStream_t(stream));
   if (e != hipSuccess) return fail(int(e), hipGetErrorString(e));
   return 0;

@@ -171,6 +171,7 @@ struct Model {
   int device = 0;
   std::string name;
   int integrated = 0;
+  size_t device_bytes = 0;
   hipStream_t stream = nullptr;
   // Whether independent launches of one kind run as grouped launches (in a
   // topological order of the groups); homes are then reused only where that
@@ -202,6 +203,7 @@ struct Model {
   bool build_steps(std::string &err);
   bool pack(std::string &err);
   bool set_sizes(const size_t *hw, size_t n, std::string &err);
+  size_t max_lanes() const;
   bool arrange(Batch &b, std::string &err);
   void build_launches(Batch &b);
   void account(Batch &b) const;
@@ -909,6 +911,7 @@ bool Model::load(const uint8_t *bytes, size_t len, std::string &err) {
   name = prop.name;
   if (name.empty()) name = prop.gcnArchName;
   integrated = prop.integrated;
+  device_bytes = prop.totalGlobalMem;
   HIPTRY(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking), "creating a stream");
   HIPTRY(hipMalloc(&dweights, std::max<size_t>(weights.size(), 1) * sizeof(float)),
          "allocating the weights");
@@ -1875,6 +1878,23 @@ bool Model::set_sizes(const size_t *hw, size_t n, std::string &err) {
   return true;
 }
 
+// The most lanes one run takes. The Vulkan backend is bounded by its
+// descriptor budget (src/engine/gpu/mod.rs:184-186); this one by memory and
+// by 32-bit element counts: lanes of the first lane's size (the load size
+// before any), each holding every plan buffer at once plus a quarter more
+// for the workspace (the arena reuses memory, so this over-counts), in 80 %
+// of the device's memory, and few enough that the largest buffer's
+// elements over all lanes still count in 31 bits.
+size_t Model::max_lanes() const {
+  const Plan &p = active_batches ? batches[0]->plan : plan;
+  size_t floats = 0, largest = 1;
+  for (size_t f : p.pool) floats += f, largest = std::max(largest, f);
+  const size_t per_lane = std::max<size_t>(1, (floats + floats / 4 + p.in_h * p.in_w * p.in_c) * sizeof(float));
+  const size_t by_memory = device_bytes / 10 * 8 / per_lane;
+  const size_t by_count = size_t(0x7fffffff) / largest;
+  return std::max<size_t>(1, std::min(by_memory, by_count));
+}
+
 void Model::drop_graph() {
   if (graph_exec) hipGraphExecDestroy(graph_exec);
   if (graph) hipGraphDestroy(graph);
@@ -2007,7 +2027,7 @@ int ppocr_gpu_set_input_size(ppocr_gpu_model *model, size_t height, size_t width
   return ppocr_gpu_set_sizes(model, hw, 1, err, err_len);
 }
 
-size_t ppocr_gpu_max_lanes(const ppocr_gpu_model *model) { return model ? 4096 : 0; }
+size_t ppocr_gpu_max_lanes(const ppocr_gpu_model *model) { return model ? model->m.max_lanes() : 0; }
 
 size_t ppocr_gpu_lanes(const ppocr_gpu_model *model) { return model ? model->m.lane_at.size() : 0; }
 

@@ -104,6 +104,16 @@ def test_encoder_long_line(oracle):
     near(got, want)
 
 
+def test_encoder_long_line_sum_read_elsewhere(oracle):
+    # 130 steps with each attention sum an output: the attention rows go to
+    # the workspace and the score spill sits right after them (the workspace
+    # holds no second sum here), then the projection, then the MLP.
+    plan = encoder_plan(130, 120, 8, 240, 2, "swish", seed=6, expose=True)
+    got, want, names = run_both(plan, 130, 120, 2, oracle, outs=3)
+    assert names == ["ln_linear", "attention", "ln_linear", "ln_mlp"] * 2, names
+    near(got, want)
+
+
 @pytest.mark.parametrize("c,heads,hidden,act", [(64, 4, 128, "gelu"), (32, 2, 96, "hardswish"),
                                                 (96, 8, 200, "relu")])
 def test_encoder_widths(oracle, c, heads, hidden, act):

@@ -162,3 +162,21 @@ def test_resize_between_runs(oracle):
     with pytest.raises(Exception):
         g.set_input_size(48, 40)  # not a multiple of 32: the neck's sums disagree
     g.close()
+
+
+def test_max_lanes_bounded_by_memory():
+    # The lane bound follows the plan's size: a 960 x 960 detector lane holds
+    # far more than a 48 x 320 line, so fewer of them fit; both leave room for
+    # the worker's batches of 16, and asking for more than the bound is
+    # refused with a message instead of failing in an allocation.
+    det = GpuModel.load(nets.detector_plan(h=960, w=960))
+    rec = GpuModel.load(nets.recognizer_plan())
+    try:
+        nd, nr = det.max_lanes(), rec.max_lanes()
+        assert 16 <= nd < nr, (nd, nr)
+        with pytest.raises(RuntimeError, match="more than the"):
+            det.set_sizes([(960, 960)] * (nd + 1))
+        rec.set_sizes([(48, 320)] * 16)
+    finally:
+        det.close()
+        rec.close()
