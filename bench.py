@@ -327,6 +327,15 @@ def bench_stages(P, nets, repeats: int = 20) -> dict:
         boxes = post.boxes_from_prob(big, 960, 960, 2550, 3300)
     out["db_boxes 960x960 (host)"] = {"ms": round((time.perf_counter() - t0) * 1e3 / 5, 4),
                                       "boxes": int(boxes.shape[0])}
+    # The same from the threshold as row bitmasks (what the detector's run
+    # hands the host with its DB mask set): the host's border following
+    # starts from the pixels where a row's bits change.
+    bits = post.pack_rows(big > np.float32(0.3))
+    t0 = time.perf_counter()
+    for _ in range(5):
+        boxes = post.boxes_from_bits(big, bits, 960, 960, 2550, 3300)
+    out["db_boxes_bits 960x960 (host)"] = {"ms": round((time.perf_counter() - t0) * 1e3 / 5, 4),
+                                           "boxes": int(boxes.shape[0])}
     d = post.Dictionary.from_metadata((gold / "characters.txt").read_text(encoding="utf-8"))
     pairs = [np.stack([rng.integers(0, 18710, 80).astype(np.float32),
                        rng.uniform(0.5, 1, 80).astype(np.float32)], 1) for _ in range(16)]

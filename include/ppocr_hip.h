@@ -122,6 +122,23 @@ int ppocr_gpu_run_device(ppocr_gpu_model *model, char *err, size_t err_len);
 int ppocr_gpu_run_device_async(ppocr_gpu_model *model, char *err, size_t err_len);
 int ppocr_gpu_wait(ppocr_gpu_model *model, char *err, size_t err_len);
 
+/* The DB threshold (src/det.rs:438, `prob > thresh` in f32) of output
+ * `output`, a one-channel map, written by every later run as row bitmasks
+ * beside the outputs: one launch on the GPU after the forward, 1/32 of the
+ * map's bytes to the host instead of a pass over the map there. It replaces
+ * the host-side threshold the reference's `boxes_from_prob` starts with
+ * (src/det.rs:430-452); ppocr_db_boxes_bits takes the result. `output` < 0
+ * stops it. The lanes keep their sizes (their memory is arranged again).
+ * Returns 0, or 1 with a message. */
+int ppocr_gpu_set_db_mask(ppocr_gpu_model *model, long output, float thresh, char *err, size_t err_len);
+
+/* Lane `lane`'s bitmasks from the last run: `*rows` rows of `*words_per_row`
+ * words, bit x % 64 of word x / 64 of a row set where the map exceeds the
+ * threshold (bits past the width zero); valid until the next run or
+ * set_sizes. NULL when no DB mask is set or the lane does not exist. */
+const uint64_t *ppocr_gpu_lane_db_mask(const ppocr_gpu_model *model, size_t lane, size_t *words_per_row,
+                                       size_t *rows);
+
 /* Runs record their launches in a HIP graph from the second run after the
  * lanes were set, and replay it (default, `enable` 1); with 0 every run
  * launches each kernel itself. Returns 0, or 1 for a NULL model. */
@@ -261,6 +278,16 @@ typedef struct ppocr_db_options {
 int ppocr_db_boxes(const float *prob, const uint8_t *mask, size_t map_w, size_t map_h, size_t dest_w,
                    size_t dest_h, const ppocr_db_options *options, float *boxes, size_t boxes_cap,
                    size_t *n_boxes, char *err, size_t err_len);
+
+/* The same boxes (src/det.rs:430-452, the threshold at :438 already taken)
+ * from the map and its threshold as row bitmasks: bit x % 64 of word
+ * y * words_per_row + x / 64 is prob[y][x] > thresh, bits past map_w zero,
+ * as ppocr_gpu_set_db_mask has the detector's run write them. The borders
+ * are followed from the pixels where a row's bits change; `prob` is read
+ * only inside the regions' bounding boxes. */
+int ppocr_db_boxes_bits(const float *prob, const uint64_t *bits, size_t words_per_row, size_t map_w, size_t map_h,
+                        size_t dest_w, size_t dest_h, const ppocr_db_options *options, float *boxes,
+                        size_t boxes_cap, size_t *n_boxes, char *err, size_t err_len);
 
 /* The DB threshold on the GPU (src/det.rs:438): mask[i] = prob[i] > thresh
  * (f32), n bytes, device pointers. */

@@ -73,6 +73,8 @@ def lib() -> C.CDLL:
         L.oracle_softmax_row.argtypes = [F32P, sz]
         L.oracle_row_argmax.argtypes = [F32P, F32P, sz, sz, C.c_int]
         L.oracle_max_threads.restype = C.c_int
+        L.oracle_find_contours.argtypes = [C.POINTER(C.c_uint8), sz, sz, vp, sz, vp, sz, szp, szp]
+        L.oracle_find_contours.restype = C.c_int
         _lib = L
     return _lib
 
@@ -296,3 +298,27 @@ def crop_text(image, quad) -> np.ndarray:
     assert L.oracle_crop_text(_u8p(src), src.shape[1], src.shape[0], qp, _u8p(out), out.size,
                               C.byref(w), C.byref(h))
     return out[:w.value * h.value * 3].reshape(h.value, w.value, 3)
+
+
+def find_contours(mask) -> list[list[list[int]]]:
+    """Region borders of a 2-D mask (oracle_find_contours: src/contour.rs:44-140):
+    each border's corners [x, y], in cv2.findContours's list order."""
+    m = np.ascontiguousarray(np.asarray(mask) != 0, np.uint8)
+    h, w = m.shape
+    pcap, ccap = 4096, 1024
+    while True:
+        pts = np.zeros(2 * pcap, np.int32)
+        lens = np.zeros(ccap, np.uint64)
+        np_, nc = C.c_size_t(), C.c_size_t()
+        rc = lib().oracle_find_contours(_u8p(m), w, h, pts.ctypes.data_as(C.c_void_p), pcap,
+                                        lens.ctypes.data_as(C.c_void_p), ccap, C.byref(np_), C.byref(nc))
+        if rc == 1:
+            pcap, ccap = max(pcap, np_.value), max(ccap, nc.value)
+            continue
+        if rc:
+            raise MemoryError("oracle_find_contours")
+        out, k = [], 0
+        for n in lens[:nc.value].astype(np.int64):
+            out.append(pts[2 * k:2 * (k + n)].reshape(-1, 2).tolist())
+            k += n
+        return out

@@ -13,6 +13,7 @@
  *   detector input           src/det.rs:195-224
  *   recogniser input         src/rec.rs:10-43
  *   text crop                src/crop.rs:1-127, src/det.rs:398-402
+ *   region borders           src/contour.rs:44-140
  *
  * Images are 8-bit, three channels, rows top to bottom (HWC).
  */
@@ -228,4 +229,162 @@ int oracle_crop_text(const uint8_t *img, size_t iw, size_t ih, const float *q, u
     *ow = turn ? height : width;
     *oh = turn ? width : height;
     return 1;
+}
+
+/* Region borders of a binary mask (src/contour.rs:44-140): Suzuki and Abe's
+ * border following over 8-connected foreground, every pixel visited in
+ * raster order, outer borders (foreground with background to the west) and
+ * hole borders (foreground, not marked east, with background to the east),
+ * each followed counter-clockwise on screen from the first foreground
+ * neighbour clockwise of the background pixel that revealed it, its pixels
+ * marked (marked-east where the walk passed background to the east), and
+ * reduced to the pixels where the step changes direction; the borders found
+ * last listed first. Steps are numbered counter-clockwise on screen from
+ * east, as the reference numbers them.
+ *
+ * Output: the corners of every border, x then y, one border after another
+ * (pts), and each border's corner count (lens), in list order. Returns 0;
+ * 1 when pts or lens is too small (n_pts and n_cont then hold the sizes
+ * needed); 2 when out of memory. */
+enum { BG = 0, UNSEEN = 1, MARKED = 2, MARKED_EAST = 3 };
+
+int oracle_find_contours(const uint8_t *mask, size_t width, size_t height, int32_t *pts, size_t pts_cap,
+                         size_t *lens, size_t lens_cap, size_t *n_pts, size_t *n_cont) {
+    static const int sx[8] = {1, 1, 0, -1, -1, -1, 0, 1}, sy[8] = {0, -1, -1, -1, 0, 1, 1, 1};
+    const int east = 0, west = 4;
+    const long stride = (long)width + 2;
+    uint8_t *state = calloc((size_t)stride * (height + 2), 1);
+    size_t chain_cap = 1024, found_cap = 1024, nf = 0, found_pts_cap = 4096, nfp = 0;
+    long *chain_at = malloc(chain_cap * sizeof(long));
+    int *chain_dir = malloc(chain_cap * sizeof(int));
+    size_t *found_len = malloc(found_cap * sizeof(size_t));
+    int32_t *found_pts = malloc(found_pts_cap * 2 * sizeof(int32_t));
+    int rc = 0;
+    if (!state || !chain_at || !chain_dir || !found_len || !found_pts) {
+        rc = 2;
+        goto done;
+    }
+    for (size_t y = 0; y < height; y++)
+        for (size_t x = 0; x < width; x++)
+            state[(y + 1) * stride + x + 1] = mask[y * width + x] ? UNSEEN : BG;
+    long off[8];
+    for (int d = 0; d < 8; d++) off[d] = sx[d] + sy[d] * stride;
+    for (size_t y = 1; y <= height; y++)
+        for (size_t x = 1; x <= width; x++) {
+            const long start = (long)y * stride + (long)x;
+            const uint8_t here = state[start];
+            int from;
+            if (here == UNSEEN && state[start - 1] == BG)
+                from = west;
+            else if ((here == UNSEEN || here == MARKED) && state[start + 1] == BG)
+                from = east;
+            else
+                continue;
+            int last_dir = -1;
+            for (int k = 0; k < 8 && last_dir < 0; k++) {
+                const int d = (from + 8 - k) % 8;
+                if (state[start + off[d]] != BG) last_dir = d;
+            }
+            size_t n = 0;
+            if (last_dir < 0) {
+                state[start] = MARKED_EAST;
+                chain_at[0] = start, chain_dir[0] = 0, n = 1;
+            } else {
+                const long last = start + off[last_dir];
+                long cur = start;
+                int back = last_dir;
+                for (;;) {
+                    int east_bg = 0, next_dir = back;
+                    for (int k = 1; k <= 8; k++) {
+                        const int d = (back + k) % 8;
+                        if (state[cur + off[d]] != BG) {
+                            next_dir = d;
+                            break;
+                        }
+                        if (d == east) east_bg = 1;
+                    }
+                    if (east_bg)
+                        state[cur] = MARKED_EAST;
+                    else if (state[cur] == UNSEEN)
+                        state[cur] = MARKED;
+                    if (n == chain_cap) {
+                        chain_cap *= 2;
+                        long *a = realloc(chain_at, chain_cap * sizeof(long));
+                        int *b = realloc(chain_dir, chain_cap * sizeof(int));
+                        if (a) chain_at = a;
+                        if (b) chain_dir = b;
+                        if (!a || !b) {
+                            rc = 2;
+                            goto done;
+                        }
+                    }
+                    chain_at[n] = cur, chain_dir[n] = next_dir, n++;
+                    const long next = cur + off[next_dir];
+                    if (next == start && cur == last) break;
+                    back = (next_dir + 4) % 8;
+                    cur = next;
+                }
+            }
+            /* The corners: a lone pixel is its own; else the pixels whose step
+             * differs from the one before (cyclically), from the first such. */
+            size_t first = 0, k = 0;
+            int any = 0;
+            if (last_dir >= 0)
+                for (; first < n; first++)
+                    if (chain_dir[first] != chain_dir[(first + n - 1) % n]) {
+                        any = 1;
+                        break;
+                    }
+            if (nf == found_cap) {
+                found_cap *= 2;
+                size_t *a = realloc(found_len, found_cap * sizeof(size_t));
+                if (!a) {
+                    rc = 2;
+                    goto done;
+                }
+                found_len = a;
+            }
+            for (size_t i = 0; i < n; i++) {
+                const size_t at = (first + i) % n;
+                const int keep = last_dir < 0 ? 1 : (any && chain_dir[at] != chain_dir[(at + n - 1) % n]);
+                if (!keep) continue;
+                if (nfp == found_pts_cap) {
+                    found_pts_cap *= 2;
+                    int32_t *a = realloc(found_pts, found_pts_cap * 2 * sizeof(int32_t));
+                    if (!a) {
+                        rc = 2;
+                        goto done;
+                    }
+                    found_pts = a;
+                }
+                found_pts[2 * nfp] = (int32_t)(chain_at[at] % stride) - 1;
+                found_pts[2 * nfp + 1] = (int32_t)(chain_at[at] / stride) - 1;
+                nfp++, k++;
+            }
+            found_len[nf++] = k;
+        }
+    *n_pts = nfp;
+    *n_cont = nf;
+    if (nfp > pts_cap || nf > lens_cap) {
+        rc = 1;
+        goto done;
+    }
+    /* List order: the last border found first. */
+    {
+        size_t end = nfp, o = 0;
+        for (size_t c = nf; c-- > 0;) {
+            const size_t begin = end - found_len[c];
+            memcpy(pts + 2 * o, found_pts + 2 * begin, found_len[c] * 2 * sizeof(int32_t));
+            o += found_len[c];
+            lens[nf - 1 - c] = found_len[c];
+            end = begin;
+        }
+    }
+done:
+    free(state);
+    free(chain_at);
+    free(chain_dir);
+    free(found_len);
+    free(found_pts);
+    return rc;
 }

@@ -93,6 +93,9 @@ def lib() -> C.CDLL:
         "ppocr_min_area_rect": ([C.POINTER(C.c_int32), sz, fp, fp], C.c_int),
         "ppocr_unclip": ([fp, C.c_double, C.POINTER(C.c_int32), sz, szp], C.c_int),
         "ppocr_db_boxes": ([fp, vp, sz, sz, sz, sz, vp, fp, sz, szp, cp, sz], C.c_int),
+        "ppocr_db_boxes_bits": ([fp, vp, sz, sz, sz, sz, sz, vp, fp, sz, szp, cp, sz], C.c_int),
+        "ppocr_gpu_set_db_mask": ([vp, C.c_long, C.c_float, cp, sz], C.c_int),
+        "ppocr_gpu_lane_db_mask": ([vp, sz, szp, szp], vp),
     }
     for name, (args, res) in sig.items():
         f = getattr(L, name)
@@ -189,6 +192,22 @@ class GpuModel:
     def run_device(self) -> None:
         """`run` over inputs already written on the device."""
         _call(lib().ppocr_gpu_run_device, self._h)
+
+    def set_db_mask(self, output: int = 0, thresh: float = 0.3) -> None:
+        """From the next run on, also write output `output`'s DB threshold
+        (prob > thresh) as row bitmasks; output < 0 stops it."""
+        _call(lib().ppocr_gpu_set_db_mask, self._h, output, thresh)
+
+    def lane_db_mask(self, lane: int = 0) -> np.ndarray:
+        """Lane `lane`'s DB bitmasks from the last run (a copy): rows x words
+        (uint64), bit x % 64 of word x / 64 set where the map exceeds the
+        threshold."""
+        wpr, rows = C.c_size_t(), C.c_size_t()
+        p = lib().ppocr_gpu_lane_db_mask(self._h, lane, C.byref(wpr), C.byref(rows))
+        if not p:
+            raise GpuError(f"no DB mask for lane {lane}")
+        n = wpr.value * rows.value
+        return np.ctypeslib.as_array((C.c_uint64 * n).from_address(p)).reshape(rows.value, wpr.value).copy()
 
     def run_device_async(self) -> None:
         """`run_device` queued on the model's stream; `wait()` ends it."""

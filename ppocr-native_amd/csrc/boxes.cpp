@@ -17,12 +17,20 @@
 //  - growth: shapely's area and length, pyclipper's round offset and the
 //    union that tidies it (src/geometry.rs:282-435);
 //  - scaling: numpy's f32 divide, multiply and round-half-even.
+#include <unistd.h>
+
 #include <algorithm>
+#include <array>
+#include <atomic>
 #include <cmath>
+#include <condition_variable>
 #include <cstdint>
 #include <cstring>
+#include <functional>
 #include <limits>
+#include <mutex>
 #include <numeric>
+#include <thread>
 #include <vector>
 
 #include "post.hpp"
@@ -60,13 +68,40 @@ int counterclockwise(int d, int k) { return (d - k) & 7; }
 // border, on a border, or on a border whose east neighbour was found to be
 // paper while the border was followed (that mark keeps a hole border from
 // starting there again).
+//
+// The mask comes in as row bitmasks (bit x % 64 of word x / 64 of a row is
+// pixel x; bits past the width are zero). A border can only start at ink
+// with paper to its west (an outer border) or to its east (a hole border),
+// and which pixels those are is fixed by the mask, since following a border
+// only relabels ink. So the scan visits, in raster order, just the pixels
+// where a row's bits change, and asks each the same two questions the full
+// raster scan asks of every pixel: the same borders, in the same order.
 class BorderTracer {
  public:
-  BorderTracer(const uint8_t *mask, size_t width, size_t height)
-      : w_(width), h_(height), pitch_(long(width) + 2), label_(size_t(pitch_) * (height + 2), kPaper) {
-    for (size_t y = 0; y < height; y++)
-      for (size_t x = 0; x < width; x++)
-        if (mask[y * width + x]) label_[at(long(x), long(y))] = kInk;
+  BorderTracer(const uint64_t *bits, size_t words_per_row, size_t width, size_t height)
+      : h_(height), pitch_(long(width) + 2), bits_(bits), wpr_(words_per_row),
+        label_(size_t(pitch_) * (height + 2), kPaper) {
+    // Eight pixels a table lookup: byte b of a word spreads to 8 labels.
+    static const std::array<uint64_t, 256> spread = [] {
+      std::array<uint64_t, 256> t{};
+      for (int v = 0; v < 256; v++)
+        for (int k = 0; k < 8; k++)
+          if (v >> k & 1) t[size_t(v)] |= uint64_t(kInk) << (8 * k);
+      return t;
+    }();
+    for (size_t y = 0; y < height; y++) {
+      uint8_t *row = label_.data() + at(0, long(y));
+      for (size_t k = 0; k < wpr_; k++) {
+        uint64_t v = bits_[y * wpr_ + k];
+        for (size_t b = 0; v; b++, v >>= 8) {
+          const size_t x = 64 * k + 8 * b;
+          if (!(v & 0xff)) continue;
+          const uint64_t lanes = spread[v & 0xff];
+          const size_t n = std::min<size_t>(8, width - x);
+          std::memcpy(row + x, &lanes, n);
+        }
+      }
+    }
     for (int d = 0; d < 8; d++) step_[d] = kNx[d] + long(kNy[d]) * pitch_;
   }
 
@@ -74,15 +109,25 @@ class BorderTracer {
   // in which a raster scan meets them.
   Contours all() {
     Contours found;
-    for (long y = 0; y < long(h_); y++)
-      for (long x = 0; x < long(w_); x++) {
-        const long p = at(x, y);
-        const uint8_t v = label_[p];
-        if (v == kInk && label_[p - 1] == kPaper)
-          found.push_back(follow(p, kWest));  // an outer border, paper to its west
-        else if ((v == kInk || v == kTraced) && label_[p + 1] == kPaper)
-          found.push_back(follow(p, kEast));  // a hole border, paper to its east
+    for (long y = 0; y < long(h_); y++) {
+      const uint64_t *row = bits_ + size_t(y) * wpr_;
+      for (size_t k = 0; k < wpr_; k++) {
+        const uint64_t ink = row[k];
+        if (!ink) continue;
+        // West neighbours' bits (bit 63 of the word before), east ones' (bit
+        // 0 of the word after); off the row is paper.
+        const uint64_t west = ink << 1 | (k ? row[k - 1] >> 63 : 0);
+        const uint64_t east = ink >> 1 | (k + 1 < wpr_ ? row[k + 1] << 63 : 0);
+        for (uint64_t edge = ink & ~(west & east); edge; edge &= edge - 1) {
+          const long p = at(long(64 * k) + __builtin_ctzll(edge), y);
+          const uint8_t v = label_[p];
+          if (v == kInk && label_[p - 1] == kPaper)
+            found.push_back(follow(p, kWest));  // an outer border, paper to its west
+          else if ((v == kInk || v == kTraced) && label_[p + 1] == kPaper)
+            found.push_back(follow(p, kEast));  // a hole border, paper to its east
+        }
       }
+    }
     std::reverse(found.begin(), found.end());
     return found;
   }
@@ -107,10 +152,10 @@ class BorderTracer {
       return {point(start)};
     }
     const long last = start + step_[closing];
-    path_.clear();
-    heading_.clear();
+    std::vector<Point> corners;
     long p = start;
     int came_from = closing;  // direction, seen from p, of the pixel before it
+    int first = -1, prev = -1;  // the headings of the first step and of the step before
     for (;;) {
       // Counter-clockwise from the pixel before, the first ink neighbour.
       int go = came_from;
@@ -127,26 +172,28 @@ class BorderTracer {
         label_[p] = kTracedEastPaper;
       else if (label_[p] == kInk)
         label_[p] = kTraced;
-      path_.push_back(p);
-      heading_.push_back(go);
+      // CHAIN_APPROX_SIMPLE: a corner wherever the heading changes; the
+      // first pixel's turn (from the last step) is settled at the end.
+      if (first < 0)
+        first = go;
+      else if (go != prev)
+        corners.push_back(point(p));
+      prev = go;
       const long next = p + step_[go];
       if (p == last && next == start) break;
       came_from = clockwise(go, 4);
       p = next;
     }
-    std::vector<Point> corners;
-    const size_t n = heading_.size();
-    for (size_t i = 0; i < n; i++)
-      if (heading_[i] != heading_[(i + n - 1) % n]) corners.push_back(point(path_[i]));
+    if (first != prev) corners.insert(corners.begin(), point(start));
     return corners;
   }
 
-  size_t w_, h_;
+  size_t h_;
   long pitch_;
+  const uint64_t *bits_;
+  size_t wpr_;
   std::vector<uint8_t> label_;
   long step_[8];
-  std::vector<long> path_;
-  std::vector<int> heading_;
 };
 
 // ---------------------------------------------------------------- hull
@@ -381,8 +428,97 @@ float f32_distance(const std::array<float, 2> &p, const std::array<float, 2> &q)
 
 }  // namespace
 
+namespace {
+
+// A few host threads for the regions' candidates. Each candidate depends
+// on its own border and the map alone, and the results are gathered in
+// region order, so the boxes never depend on how many threads ran them.
+// The workers live for the process (the pool is never destroyed, so no
+// join runs at exit); a process forked after they started runs the work
+// on its calling thread alone.
+class Workers {
+ public:
+  static Workers &get() {
+    static Workers *w = new Workers();
+    return *w;
+  }
+
+  // f(i) for every i below n, on the calling thread and the workers;
+  // returns when all are done. One job runs at a time.
+  void run(size_t n, const std::function<void(size_t)> &f) {
+    if (n < 2 || threads_ == 0 || getpid() != pid_) {
+      for (size_t i = 0; i < n; i++) f(i);
+      return;
+    }
+    std::lock_guard<std::mutex> one(job_mu_);
+    {
+      std::lock_guard<std::mutex> g(mu_);
+      job_ = &f, n_ = n, busy_ = threads_;
+      next_.store(0);
+      gen_++;
+    }
+    wake_.notify_all();
+    drain();
+    std::unique_lock<std::mutex> g(mu_);
+    idle_.wait(g, [&] { return busy_ == 0; });
+    job_ = nullptr;
+  }
+
+ private:
+  Workers() : pid_(getpid()) {
+    const unsigned hw = std::thread::hardware_concurrency();
+    threads_ = hw > 2 ? std::min(4u, hw - 1) : 0;
+    for (unsigned i = 0; i < threads_; i++) std::thread([this] { loop(); }).detach();
+  }
+
+  void drain() {
+    for (size_t i = next_.fetch_add(1); i < n_; i = next_.fetch_add(1)) (*job_)(i);
+  }
+
+  void loop() {
+    uint64_t seen = 0;
+    std::unique_lock<std::mutex> g(mu_);
+    for (;;) {
+      wake_.wait(g, [&] { return gen_ != seen; });
+      seen = gen_;
+      g.unlock();
+      drain();
+      g.lock();
+      if (--busy_ == 0) idle_.notify_one();
+    }
+  }
+
+  const pid_t pid_;
+  unsigned threads_ = 0;
+  std::mutex job_mu_, mu_;
+  std::condition_variable wake_, idle_;
+  const std::function<void(size_t)> *job_ = nullptr;
+  size_t n_ = 0;
+  unsigned busy_ = 0;
+  uint64_t gen_ = 0;
+  std::atomic<size_t> next_{0};
+};
+
+}  // namespace
+
+std::vector<uint64_t> pack_rows(const uint8_t *mask, const float *prob, float thresh, size_t width, size_t height) {
+  const size_t wpr = (width + 63) / 64;
+  std::vector<uint64_t> bits(wpr * height, 0);
+  for (size_t y = 0; y < height; y++)
+    for (size_t x = 0; x < width; x++) {
+      const size_t i = y * width + x;
+      if (mask ? mask[i] != 0 : prob[i] > thresh) bits[y * wpr + x / 64] |= uint64_t(1) << (x % 64);
+    }
+  return bits;
+}
+
+Contours find_contours_bits(const uint64_t *bits, size_t words_per_row, size_t width, size_t height) {
+  return BorderTracer(bits, words_per_row, width, height).all();
+}
+
 Contours find_contours(const uint8_t *mask, size_t width, size_t height) {
-  return BorderTracer(mask, width, height).all();
+  const std::vector<uint64_t> bits = pack_rows(mask, nullptr, 0.0f, width, height);
+  return find_contours_bits(bits.data(), (width + 63) / 64, width, height);
 }
 
 double contour_mean(const float *map, size_t width, size_t height, const std::vector<Point> &c) {
@@ -588,16 +724,20 @@ void sort_boxes(std::vector<Quad> &boxes) {
 
 std::vector<Quad> boxes_from_prob(const float *prob, const uint8_t *mask, size_t map_w, size_t map_h,
                                   size_t dest_w, size_t dest_h, const DbOptions &o) {
-  std::vector<uint8_t> thresholded;
-  if (!mask) {
-    thresholded.resize(map_w * map_h);
-    for (size_t i = 0; i < thresholded.size(); i++) thresholded[i] = prob[i] > o.thresh;
-    mask = thresholded.data();
-  }
-  const Contours regions = find_contours(mask, map_w, map_h);
+  const std::vector<uint64_t> bits = pack_rows(mask, prob, o.thresh, map_w, map_h);
+  return boxes_from_bits(prob, bits.data(), (map_w + 63) / 64, map_w, map_h, dest_w, dest_h, o);
+}
+
+std::vector<Quad> boxes_from_bits(const float *prob, const uint64_t *bits, size_t words_per_row, size_t map_w,
+                                  size_t map_h, size_t dest_w, size_t dest_h, const DbOptions &o) {
+  const Contours regions = find_contours_bits(bits, words_per_row, map_w, map_h);
+  const size_t n = std::min(regions.size(), o.max_candidates);
+  std::vector<Candidate> found(n);
+  Workers::get().run(n, [&](size_t i) {
+    found[i] = contour_candidate(prob, map_w, map_h, regions[i], dest_w, dest_h, o);
+  });
   std::vector<Quad> boxes;
-  for (size_t i = 0; i < regions.size() && i < o.max_candidates; i++) {
-    const Candidate c = contour_candidate(prob, map_w, map_h, regions[i], dest_w, dest_h, o);
+  for (const Candidate &c : found) {
     Quad q;
     if (c.kind == Candidate::kKept && order_and_clip(c.corners, dest_w, dest_h, q)) boxes.push_back(q);
   }

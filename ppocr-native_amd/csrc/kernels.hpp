@@ -504,6 +504,8 @@ hipError_t launch_db_head(const HeadArgs &a, hipStream_t s);
 
 // mask[i] = prob[i] > thresh over n floats (bytes out).
 hipError_t launch_db_mask(const float *prob, uint8_t *mask, long n, float thresh, hipStream_t s);
+hipError_t launch_db_bits(const float *map, long lane_stride, int w, int h, int lanes, float thresh,
+                          unsigned long long *bits, hipStream_t s);
 
 // ------------------------------------------------------------- image stages
 

@@ -1764,4 +1764,33 @@ hipError_t launch_db_mask(const float *prob, uint8_t *mask, long n, float thresh
   return hipGetLastError();
 }
 
+// The DB threshold as row bitmasks (src/det.rs:438, compared in f32): one
+// wave per 64-pixel word of a row, each lane one pixel, the wave's ballot
+// the word (bit x % 64 of word x / 64; pixels past the width are 0). The
+// map is `lanes` h x w maps, `lane_stride` floats apart; the words of a
+// lane follow each other row by row.
+__global__ __launch_bounds__(256) void db_bits_kernel(const float *map, long lane_stride, int w, int h, int words,
+                                                       float thresh, unsigned long long *bits, long total) {
+  const long word = (long)blockIdx.x * 4 + threadIdx.x / 64;
+  if (word >= total) return;  // whole waves leave together
+  const int lane = threadIdx.x % 64;
+  const long row = word / words;
+  const int x = int(word - row * words) * 64 + lane;
+  const long ln = row / h;
+  const float *src = map + ln * lane_stride + (row - ln * h) * w;
+  const bool ink = x < w && src[x] > thresh;
+  const unsigned long long b = __ballot(ink);
+  if (lane == 0) bits[word] = b;
+}
+
+hipError_t launch_db_bits(const float *map, long lane_stride, int w, int h, int lanes, float thresh,
+                          unsigned long long *bits, hipStream_t s) {
+  if (w <= 0 || h <= 0 || lanes <= 0) return hipErrorInvalidValue;
+  const int words = (w + 63) / 64;
+  const long total = long(lanes) * h * words;
+  hipLaunchKernelGGL(db_bits_kernel, dim3(unsigned((total + 3) / 4)), dim3(256), 0, s, map, lane_stride, w, h, words,
+                     thresh, bits, total);
+  return hipGetLastError();
+}
+
 }  // namespace ppocr

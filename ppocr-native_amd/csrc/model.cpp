@@ -160,6 +160,12 @@ struct Batch {
   size_t in_len = 0;
   std::vector<Launch> launches;
 
+  // The DB threshold's row bitmasks of one output (when the model is set to
+  // write them): in the arena after the workspace, and pinned on the host.
+  size_t bits_off = 0, bits_w = 0, bits_h = 0, bits_wpr = 0;
+  unsigned long long *host_bits = nullptr;
+  size_t host_bits_cap = 0;
+
   float *dev(size_t slot) const { return arena + home_off[home[slot]]; }
   float *ws(size_t step) const { return arena + ws_off + step_ws[step]; }
   long stride(size_t slot) const { return long(home_floats[home[slot]]); }
@@ -191,6 +197,10 @@ struct Model {
   // which also sets any kernel attribute outside the capture).
   bool use_graphs = true;
   int eager_runs = 0;
+  // The output whose DB threshold each run also writes as row bitmasks
+  // (-1: none), and that threshold.
+  long db_output = -1;
+  float db_thresh = 0.3f;
   hipGraph_t graph = nullptr;
   hipGraphExec_t graph_exec = nullptr;
 
@@ -209,6 +219,8 @@ struct Model {
   void account(Batch &b) const;
   void group(Batch &b) const;
   bool run(bool copy_in, bool copy_out, std::string &err, bool sync = true);
+  bool set_db_mask(long output, float thresh, std::string &err);
+  bool copy_out_all(std::string &err);
   std::vector<size_t> step_reads(const Step &s) const;
   int enc_hidden(const Step &s) const { return s.kind == S_ENC_BLOCK ? int(plan.ops[s.m_fc1].oc) : 0; }
   size_t step_writes(const Step &s) const;
@@ -228,6 +240,7 @@ Model::~Model() {
   for (auto &b : batches) {
     if (b->arena) hipFree(b->arena);
     if (b->host_in) hipHostFree(b->host_in);
+    if (b->host_bits) hipHostFree(b->host_bits);
     for (float *p : b->host_out)
       if (p) hipHostFree(p);
   }
@@ -1031,6 +1044,18 @@ bool Model::arrange(Batch &b, std::string &err) {
   }
   b.ws_off = off;
   off += round_up(std::max<size_t>(ws, 64), 64);
+  b.bits_w = b.bits_h = b.bits_wpr = 0;
+  if (db_output >= 0) {
+    // The map: the last operation writing that output, one channel.
+    const size_t slot = p.out_slot[size_t(db_output)];
+    const Op *map = nullptr;
+    for (const Op &o : p.ops)
+      if (o.y == slot) map = &o;
+    if (!map || map->oc != 1) return err = "the DB mask's output is not a one-channel map", false;
+    b.bits_w = map->ow, b.bits_h = map->oh, b.bits_wpr = (map->ow + 63) / 64;
+    b.bits_off = off;
+    off += round_up(2 * L * b.bits_h * b.bits_wpr, 64);
+  }
   if (off > b.arena_floats) {
     if (b.arena) {
       hipFree(b.arena);
@@ -1062,6 +1087,16 @@ bool Model::arrange(Batch &b, std::string &err) {
       HIPTRY(hipHostMalloc(&b.host_out[k], want * sizeof(float), hipHostMallocDefault), "allocating pinned output");
       b.host_out_cap[k] = want;
     }
+  }
+  const size_t bits_need = L * b.bits_h * b.bits_wpr;
+  if (b.host_bits_cap < bits_need) {
+    if (b.host_bits) hipHostFree(b.host_bits);
+    b.host_bits = nullptr;
+    b.host_bits_cap = 0;
+    const size_t want = bits_need + bits_need / 4;
+    HIPTRY(hipHostMalloc(&b.host_bits, want * sizeof(unsigned long long), hipHostMallocDefault),
+           "allocating the pinned DB mask");
+    b.host_bits_cap = want;
   }
   build_launches(b);
   // The channel means' counters start at zero (each launch leaves them so).
@@ -1957,18 +1992,57 @@ bool Model::run(bool copy_in, bool copy_out, std::string &err, bool sync) {
     }
   }
   if (!enqueue(err)) return false;
-  if (copy_out) {
+  // The DB threshold's bitmasks of the map, after the forward (outside the
+  // captured graph: one launch per batch on the same stream).
+  if (db_output >= 0)
     for (size_t g = 0; g < active_batches; g++) {
       Batch &b = *batches[g];
-      const Plan &p = b.plan;
-      for (size_t k = 0; k < p.out_slot.size(); k++)
-        HIPTRY(hipMemcpy2DAsync(b.host_out[k], p.out_n[k] * sizeof(float), b.dev(p.out_slot[k]),
-                                b.stride(p.out_slot[k]) * sizeof(float), p.out_n[k] * sizeof(float),
-                                b.lanes.size(), hipMemcpyDeviceToHost, stream),
-               "copying the results");
+      const size_t slot = b.plan.out_slot[size_t(db_output)];
+      HIPTRY(launch_db_bits(b.dev(slot), b.stride(slot), int(b.bits_w), int(b.bits_h), int(b.lanes.size()),
+                            db_thresh, reinterpret_cast<unsigned long long *>(b.arena + b.bits_off), stream),
+             "thresholding the map");
     }
-  }
+  if (copy_out && !copy_out_all(err)) return false;
   if (sync) HIPTRY(hipStreamSynchronize(stream), "running the plan");
+  return true;
+}
+
+// Every batch's outputs (and DB bitmasks) to the pinned host buffers, queued
+// on the model's stream.
+bool Model::copy_out_all(std::string &err) {
+  for (size_t g = 0; g < active_batches; g++) {
+    Batch &b = *batches[g];
+    const Plan &p = b.plan;
+    for (size_t k = 0; k < p.out_slot.size(); k++)
+      HIPTRY(hipMemcpy2DAsync(b.host_out[k], p.out_n[k] * sizeof(float), b.dev(p.out_slot[k]),
+                              b.stride(p.out_slot[k]) * sizeof(float), p.out_n[k] * sizeof(float),
+                              b.lanes.size(), hipMemcpyDeviceToHost, stream),
+             "copying the results");
+    if (db_output >= 0)
+      HIPTRY(hipMemcpyAsync(b.host_bits, b.arena + b.bits_off,
+                            b.lanes.size() * b.bits_h * b.bits_wpr * sizeof(unsigned long long),
+                            hipMemcpyDeviceToHost, stream),
+             "copying the DB mask");
+  }
+  return true;
+}
+
+// From the next run on, also write output `output`'s DB threshold as row
+// bitmasks (output < 0: stop). The lanes keep their sizes; their memory is
+// arranged again for the bitmasks.
+bool Model::set_db_mask(long output, float thresh, std::string &err) {
+  HIPTRY(hipSetDevice(device), "selecting the GPU");
+  if (output >= long(plan.out_slot.size())) return err = fmt("the plan has no output %ld", output), false;
+  const long before = db_output;
+  db_output = output < 0 ? -1 : output;
+  db_thresh = thresh;
+  if (before == db_output) return true;
+  drop_graph();
+  for (size_t g = 0; g < active_batches; g++)
+    if (!arrange(*batches[g], err)) {
+      db_output = before;
+      return false;
+    }
   return true;
 }
 
@@ -2050,6 +2124,23 @@ const float *ppocr_gpu_lane_output(const ppocr_gpu_model *model, size_t lane, si
   return b.host_out[index] + i * n;
 }
 
+int ppocr_gpu_set_db_mask(ppocr_gpu_model *model, long output, float thresh, char *err, size_t err_len) {
+  if (!model) return put_err("no model", err, err_len), 1;
+  std::string e;
+  if (!model->m.set_db_mask(output, thresh, e)) return put_err(e, err, err_len), 1;
+  return 0;
+}
+
+const uint64_t *ppocr_gpu_lane_db_mask(const ppocr_gpu_model *model, size_t lane, size_t *words_per_row,
+                                       size_t *rows) {
+  if (!model || model->m.db_output < 0 || lane >= model->m.lane_at.size()) return nullptr;
+  auto [g, i] = model->m.lane_at[lane];
+  const Batch &b = *model->m.batches[g];
+  if (words_per_row) *words_per_row = b.bits_wpr;
+  if (rows) *rows = b.bits_h;
+  return reinterpret_cast<const uint64_t *>(b.host_bits + i * b.bits_h * b.bits_wpr);
+}
+
 size_t ppocr_gpu_output_count(const ppocr_gpu_model *model) {
   return model ? model->m.plan.out_slot.size() : 0;
 }
@@ -2113,16 +2204,8 @@ int ppocr_gpu_download(ppocr_gpu_model *model, char *err, size_t err_len) {
   if (!model) return put_err("no model", err, err_len), 1;
   ppocr::Model &m = model->m;
   hipSetDevice(m.device);
-  for (size_t g = 0; g < m.active_batches; g++) {
-    Batch &b = *m.batches[g];
-    const ppocr::Plan &p = b.plan;
-    for (size_t k = 0; k < p.out_slot.size(); k++) {
-      hipError_t r = hipMemcpy2DAsync(b.host_out[k], p.out_n[k] * sizeof(float), b.dev(p.out_slot[k]),
-                                      b.stride(p.out_slot[k]) * sizeof(float), p.out_n[k] * sizeof(float),
-                                      b.lanes.size(), hipMemcpyDeviceToHost, m.stream);
-      if (r != hipSuccess) return put_err(std::string("copying the results: ") + hipGetErrorString(r), err, err_len), 1;
-    }
-  }
+  std::string e;
+  if (!m.copy_out_all(e)) return put_err(e, err, err_len), 1;
   hipError_t r = hipStreamSynchronize(m.stream);
   if (r != hipSuccess) return put_err(std::string("copying the results: ") + hipGetErrorString(r), err, err_len), 1;
   return 0;

@@ -131,4 +131,23 @@ int ppocr_db_boxes(const float *prob, const uint8_t *mask, size_t map_w, size_t 
   return 0;
 }
 
+int ppocr_db_boxes_bits(const float *prob, const uint64_t *bits, size_t words_per_row, size_t map_w, size_t map_h,
+                        size_t dest_w, size_t dest_h, const ppocr_db_options *options, float *boxes,
+                        size_t boxes_cap, size_t *n_boxes, char *err, size_t err_len) {
+  if ((!prob || !bits) && map_w * map_h) return say(err, err_len, "null argument"), 1;
+  if (!options) return say(err, err_len, "null argument"), 1;
+  if (!map_w || !map_h || !dest_w || !dest_h) return say(err, err_len, "empty map or page"), 1;
+  if (words_per_row < (map_w + 63) / 64) return say(err, err_len, "fewer bit words a row than the map is wide"), 1;
+  ppocr::DbOptions o;
+  o.thresh = options->thresh, o.box_thresh = options->box_thresh;
+  o.unclip_ratio = options->unclip_ratio, o.max_candidates = options->max_candidates;
+  const std::vector<ppocr::Quad> b =
+      ppocr::boxes_from_bits(prob, bits, words_per_row, map_w, map_h, dest_w, dest_h, o);
+  if (n_boxes) *n_boxes = b.size();
+  if (b.size() > boxes_cap || (b.size() && !boxes)) return say(err, err_len, "box buffer too small"), 2;
+  for (size_t i = 0; i < b.size(); i++)
+    for (int k = 0; k < 4; k++) boxes[8 * i + 2 * k] = b[i][k][0], boxes[8 * i + 2 * k + 1] = b[i][k][1];
+  return 0;
+}
+
 }  // extern "C"

@@ -36,6 +36,11 @@ bool ctc_decode(const uint32_t *best, const float *prob, size_t steps, const Dic
                 std::string &text, double &score);
 
 Contours find_contours(const uint8_t *mask, size_t width, size_t height);
+// The same from row bitmasks: bit x % 64 of word y * words_per_row + x / 64
+// is pixel (x, y); bits past the width must be zero.
+Contours find_contours_bits(const uint64_t *bits, size_t words_per_row, size_t width, size_t height);
+// Row bitmasks of mask[i] != 0, or of prob[i] > thresh when mask is null.
+std::vector<uint64_t> pack_rows(const uint8_t *mask, const float *prob, float thresh, size_t width, size_t height);
 double contour_mean(const float *map, size_t width, size_t height, const std::vector<Point> &contour);
 RotatedRect min_area_rect(const std::vector<Point> &points);
 Quad box_points(const RotatedRect &r);
@@ -61,5 +66,8 @@ void sort_boxes(std::vector<Quad> &boxes);
 // `mask` (map_w * map_h bytes, nonzero = text) may be null: then prob > thresh.
 std::vector<Quad> boxes_from_prob(const float *prob, const uint8_t *mask, size_t map_w, size_t map_h,
                                   size_t dest_w, size_t dest_h, const DbOptions &o);
+// The same with the threshold already taken, as row bitmasks (the GPU's).
+std::vector<Quad> boxes_from_bits(const float *prob, const uint64_t *bits, size_t words_per_row, size_t map_w,
+                                  size_t map_h, size_t dest_w, size_t dest_h, const DbOptions &o);
 
 }  // namespace ppocr

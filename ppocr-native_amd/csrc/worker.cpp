@@ -44,6 +44,9 @@ namespace {
 
 constexpr size_t kErr = 512;
 constexpr size_t kRecHeight = 48;
+// RapidOCR's DB options (src/det.rs:305-315): threshold, box threshold,
+// unclip ratio, candidates.
+constexpr ppocr_db_options kDb{0.3f, 0.5, 1.5, 1000};
 constexpr double kVerticalAspect = 1.5;  // src/crop.rs:67
 constexpr double kConfident = 0.90;      // ocr.rs:30
 constexpr double kMinGain = 0.05;        // ocr.rs:31
@@ -190,6 +193,8 @@ class Worker {
     if (ppocr_dictionary_load(text.data(), text.size(), &dict_, err, kErr)) die(o_.dict + ": " + err);
     if (ppocr_gpu_load(o_.det.c_str(), &det_, err, kErr) || ppocr_gpu_load(o_.rec.c_str(), &rec_, err, kErr))
       die(std::string("no GPU (") + err + "); the CPU engine is not part of this library");
+    // The detector's runs also write the map's DB threshold as row bitmasks.
+    if (ppocr_gpu_set_db_mask(det_, 0, kDb.thresh, err, kErr)) die(std::string("DB mask: ") + err);
     std::fprintf(stderr, "ppocr-native: running on %s\n", ppocr_gpu_device(det_));
   }
 
@@ -253,15 +258,15 @@ class Worker {
       refused_ = true;
       return false;
     }
-    size_t len = 0;
+    size_t len = 0, wpr = 0, rows = 0;
     const float *prob = ppocr_gpu_lane_output(det_, 0, 0, &len);
-    if (!prob || len != w * h) return fail("the detector gave no map");
-    const ppocr_db_options opt{0.3f, 0.5, 1.5, 1000};
+    const uint64_t *bits = ppocr_gpu_lane_db_mask(det_, 0, &wpr, &rows);
+    if (!prob || len != w * h || !bits || rows != h) return fail("the detector gave no map");
     std::vector<float> boxes(8 * 64);
     size_t nb = 0;
     for (;;) {
-      const int rc = ppocr_db_boxes(prob, nullptr, w, h, width, height, &opt, boxes.data(), boxes.size() / 8, &nb,
-                                    err, kErr);
+      const int rc = ppocr_db_boxes_bits(prob, bits, wpr, w, h, width, height, &kDb, boxes.data(),
+                                         boxes.size() / 8, &nb, err, kErr);
       if (rc == 2) {
         boxes.resize(8 * nb);
         continue;

@@ -5,8 +5,9 @@ It follows the worker's `detect` and `read` (src/bin/ppocr-native/ocr.rs:
 960 (the `Limit::Max` rule of src/det.rs:166-193 with the side fixed at the
 limit, `scaled_size` and `snap32` of src/det.rs:10-27), the detector input
 made on the GPU from the uploaded page (`det_input_hwc`, src/det.rs:228-289)
-straight into the detector's input, the detector, the DB boxes on the host
-(`boxes_from_prob`, src/det.rs:291-452, reading order), then for each box
+straight into the detector's input, the detector and its map's DB threshold
+as row bitmasks on the GPU (src/det.rs:438), the DB boxes on the host from
+those bitmasks (`boxes_from_prob`, src/det.rs:291-452, reading order), then for each box
 the perspective crop (`crop_text`, src/crop.rs:84-127) and the recogniser
 input (`rec_input`, src/rec.rs:19-43, the tensor at most 320 wide: wider
 crops are squeezed to 320) made on the GPU straight into the recogniser's
@@ -30,7 +31,7 @@ import numpy as np
 from . import GpuError, GpuModel, lib
 from .devmem import DeviceArray
 from .images import MEAN, STD, _check, _sig
-from .post import DbOptions, Dictionary, boxes_from_prob, ctc_decode_pairs
+from .post import DbOptions, Dictionary, boxes_from_bits, ctc_decode_pairs
 
 REC_HEIGHT = 48
 
@@ -89,6 +90,9 @@ class PagePipeline:
         self.dictionary = dictionary
         self.limit, self.batch, self.max_width = limit, batch, max_width
         self.options = options or DbOptions()
+        # The detector's runs also write the map's DB threshold as row
+        # bitmasks, which the host's border following starts from.
+        self.det.set_db_mask(0, self.options.thresh)
         self._det_hw: tuple[int, int] | None = None
         self._rec_sizes: list[list[tuple[int, int]]] = [[] for _ in self.recs]
         self.times = PageTimes()
@@ -144,10 +148,11 @@ class PagePipeline:
         """Page k's boxes: waits for its detector, queues page k + 1's, then
         the DB boxes on the host (none for a page too thin)."""
         t0 = time.perf_counter()
-        prob = None
+        prob = bits = None
         if sizes[k] is not None:
             self.det.wait()
             prob = self.det.lane_output(0, 0)
+            bits = self.det.lane_db_mask(0)
         if k + 1 < len(pages):
             sizes[k + 1] = self._detect(*pages[k + 1])
         t1 = time.perf_counter()
@@ -156,7 +161,7 @@ class PagePipeline:
             return np.zeros((0, 4, 2), np.float32)
         w, h = sizes[k]
         _, width, height = pages[k]
-        quads = boxes_from_prob(prob, w, h, width, height, self.options)
+        quads = boxes_from_bits(prob, bits, w, h, width, height, self.options)
         self.times.boxes += (time.perf_counter() - t1) * 1e3
         return quads
 

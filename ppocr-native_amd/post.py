@@ -176,3 +176,35 @@ def boxes_from_prob(prob, map_w: int, map_h: int, dest_w: int, dest_h: int,
         if rc:
             raise GpuError(err.value.decode())
         return boxes[:8 * n.value].reshape(-1, 4, 2)
+
+
+def boxes_from_bits(prob, bits, map_w: int, map_h: int, dest_w: int, dest_h: int,
+                    options: DbOptions | None = None) -> np.ndarray:
+    """`boxes_from_prob` with the threshold already taken as row bitmasks
+    (map_h x words uint64, bit x % 64 of word x / 64 is prob > thresh), as
+    the detector's run writes them (`GpuModel.set_db_mask`)."""
+    o = options or DbOptions()
+    opt = _DbOptions(o.thresh, o.box_thresh, o.unclip_ratio, o.max_candidates)
+    p = _f32(prob).reshape(-1)
+    b = np.ascontiguousarray(bits, np.uint64)
+    if p.size != map_w * map_h or b.ndim != 2 or b.shape[0] != map_h or b.shape[1] * 64 < map_w:
+        raise ValueError("map or bitmask size")
+    cap = max(1, o.max_candidates)
+    boxes, n, err = np.zeros(8 * cap, np.float32), C.c_size_t(), C.create_string_buffer(_ERR)
+    rc = lib().ppocr_db_boxes_bits(p.ctypes.data_as(C.POINTER(C.c_float)), b.ctypes.data_as(C.c_void_p),
+                                   b.shape[1], map_w, map_h, dest_w, dest_h, C.byref(opt),
+                                   boxes.ctypes.data_as(C.POINTER(C.c_float)), cap, C.byref(n), err, _ERR)
+    if rc:
+        raise GpuError(err.value.decode())
+    return boxes[:8 * n.value].reshape(-1, 4, 2)
+
+
+def pack_rows(mask) -> np.ndarray:
+    """Row bitmasks (rows x words, uint64) of a 2-D mask, bit x % 64 of word
+    x / 64 set where mask[y][x] != 0."""
+    m = np.asarray(mask) != 0
+    h, w = m.shape
+    words = (w + 63) // 64
+    padded = np.zeros((h, words * 64), np.uint8)
+    padded[:, :w] = m
+    return np.ascontiguousarray(np.packbits(padded, axis=1, bitorder="little")).view("<u8").astype(np.uint64)

@@ -16,7 +16,7 @@ from pathlib import Path
 import numpy as np
 import pytest
 
-from ppocr_native_amd import GpuModel, images, nets, post
+from ppocr_native_amd import GpuError, GpuModel, images, nets, post
 from ppocr_native_amd.devmem import DeviceArray
 from ppocr_native_amd.pipeline import PagePipeline, det_size
 
@@ -180,3 +180,31 @@ def test_read_pages_equals_single_reads(dictionary):
     assert sum(len(g) for g in got) >= 80
     one.close()
     many.close()
+
+
+def test_db_mask_written_by_the_detector_run():
+    # The detector's runs write the map's threshold as row bitmasks (one
+    # launch after the forward): equal to the host's threshold of the map the
+    # same run returns, lane by lane, on the eager first run and the graph
+    # replays after it; the boxes from them equal the boxes from the map.
+    h, w = 960, 736
+    m = GpuModel.load(nets.detector_plan(h=h, w=w, init="ink"))
+    m.set_sizes([(h, w)] * 2)
+    m.set_db_mask(0, 0.3)
+    for run in range(3):
+        for lane in range(2):
+            page = nets.letter_page(seed=run * 2 + lane)
+            m.lane_input_mut(lane)[:] = images.det_input(page, w, h, MEAN, STD).reshape(-1)
+        m.run()
+        for lane in range(2):
+            prob = m.lane_output(lane, 0)
+            bits = m.lane_db_mask(lane)
+            assert bits.shape == (h, (w + 63) // 64)
+            assert np.array_equal(bits, post.pack_rows(prob.reshape(h, w) > np.float32(0.3))), (run, lane)
+            want = post.boxes_from_prob(prob, w, h, 2550, 3300)
+            assert len(want) > 30 and np.array_equal(post.boxes_from_bits(prob, bits, w, h, 2550, 3300), want)
+    m.set_db_mask(-1)
+    m.run()
+    with pytest.raises(GpuError):
+        m.lane_db_mask(0)
+    m.close()

@@ -110,3 +110,24 @@ def test_checks_have_teeth():
     assert all(np.array_equal(_resize(noise, w, h), want) for w, h, want in cases)
     for kw in [{"sum_first": True}, {"corners": True}]:
         assert not all(np.array_equal(_resize(noise, w, h, **kw), want) for w, h, want in cases), kw
+
+
+@pytest.mark.parametrize("i", range(len(FX["contours"])))
+def test_oracle_contours_match_opencv(oracle, i):
+    # The oracle's border following (src/contour.rs:44-140) gives
+    # cv2.findContours's borders, corner for corner, in its list order.
+    case = FX["contours"][i]
+    assert oracle.find_contours(npy(case["file"])) == case["contours"]
+
+
+def test_oracle_contours_of_small_cases(oracle):
+    # A lone pixel is its own border; a 2 x 2 block has four corners; a ring
+    # has an outer border and a hole border, the hole (found second) listed
+    # first; pixels on the image edge count as border pixels.
+    assert oracle.find_contours(np.array([[0, 0, 0], [0, 1, 0], [0, 0, 0]])) == [[[1, 1]]]
+    assert oracle.find_contours(np.ones((2, 2))) == [[[0, 0], [0, 1], [1, 1], [1, 0]]]
+    ring = np.ones((5, 5), np.uint8)
+    ring[2, 2] = 0
+    got = oracle.find_contours(ring)
+    assert len(got) == 2 and got[1] == [[0, 0], [0, 4], [4, 4], [4, 0]]
+    assert sorted(map(tuple, got[0])) == [(1, 2), (2, 1), (2, 3), (3, 2)]

@@ -96,3 +96,60 @@ def test_db_boxes_match_rapidocr():
 
 def test_db_boxes_of_an_empty_map():
     assert post.boxes_from_prob(np.zeros((32, 32), np.float32), 32, 32, 64, 64).shape == (0, 4, 2)
+
+
+def _masks():
+    """Seeded masks that exercise the border scan: noise at several
+    densities, blobs with holes, single pixels and lines, widths on and
+    either side of the 64-pixel words."""
+    rng = np.random.default_rng(17)
+    out = []
+    for w in (1, 5, 63, 64, 65, 127, 130, 200):
+        for h in (1, 7, 33):
+            for density in (0.05, 0.5, 0.93):
+                out.append((rng.random((h, w)) < density).astype(np.uint8))
+    for _ in range(6):  # blobs with holes: thick rings and filled rectangles
+        m = np.zeros((90, 150), np.uint8)
+        for _ in range(12):
+            y, x = rng.integers(0, 80), rng.integers(0, 140)
+            hh, ww = rng.integers(3, 30), rng.integers(3, 60)
+            m[y:y + hh, x:x + ww] = 1
+            if hh > 6 and ww > 6:
+                m[y + 2:y + hh - 2, x + 2:x + ww - 2] = rng.integers(0, 2)
+        out.append(m)
+    return out
+
+
+def test_contours_equal_the_oracle_on_seeded_masks(oracle):
+    # The product follows borders from where a row's bits change; the
+    # oracle scans every pixel as the reference does (src/contour.rs:44-140).
+    for m in _masks():
+        h, w = m.shape
+        assert post.find_contours(m, w, h) == oracle.find_contours(m), (h, w)
+
+
+def test_db_boxes_from_bits_match_rapidocr():
+    # The golden map's boxes from its threshold as row bitmasks (the form the
+    # detector's run writes with set_db_mask): the same 11 boxes, bit for bit.
+    case = FX["boxes"]
+    prob = npy(case["file"])
+    h, w = prob.shape
+    dest_w, dest_h = case["dest"]
+    bits = post.pack_rows(prob > np.float32(0.3))
+    got = post.boxes_from_bits(prob, bits, w, h, dest_w, dest_h)
+    assert np.array_equal(got, np.asarray(case["boxes"], np.float32))
+
+
+def test_db_boxes_from_bits_equal_boxes_from_prob():
+    # Seeded blob maps (text-line-like bands of high probability over noise):
+    # every box equal whichever form the threshold comes in.
+    rng = np.random.default_rng(23)
+    for k in range(4):
+        h, w = 96 + 32 * k, 160 + 64 * k
+        prob = rng.uniform(0, 0.35, (h, w)).astype(np.float32)
+        for _ in range(8):
+            y, x = rng.integers(0, h - 12), rng.integers(0, w - 40)
+            prob[y:y + rng.integers(6, 12), x:x + rng.integers(20, 40)] = rng.uniform(0.5, 1.0)
+        want = post.boxes_from_prob(prob, w, h, 3 * w, 3 * h)
+        got = post.boxes_from_bits(prob, post.pack_rows(prob > np.float32(0.3)), w, h, 3 * w, 3 * h)
+        assert len(want) > 0 and np.array_equal(got, want)
