@@ -60,6 +60,12 @@ __device__ __forceinline__ CtcState ctc_join(CtcState x, CtcState y) {
   return r;
 }
 
+// The two largest of two (largest, second) pairs.
+__device__ __forceinline__ void top2(float a1, float a2, float b1, float b2, float &m1, float &m2) {
+  m1 = fmaxf(a1, b1);
+  m2 = a1 > b1 ? fmaxf(a2, b1) : (b1 > a1 ? fmaxf(b2, a1) : a1);
+}
+
 // The source holding channel c of a tap's concatenation.
 __device__ __forceinline__ ConvSrc pick_src(const ConvArgs &a, int c) {
   ConvSrc s = a.src[0];
@@ -115,10 +121,15 @@ __device__ __forceinline__ float row16_sum(float v) {
   return v + dpp16<0x140>(v);
 }
 
-template <int MT, int NT>
-__device__ __forceinline__ void ctc_rows(const f32x4 (&acc)[MT][NT], int m_first, int M, int n0, const float *bias,
-                                         int vocab, float *part, int ntn, int tn, int lane) {
-  const int li = lane & 15, lg = lane >> 4;
+// A CTC tile's per-row statistics from its logits (acc + bias, columns past
+// the vocabulary -inf): per row the maximum, the sum of exp(v - max) by
+// hardware exp2, the first column holding the maximum and the second value,
+// each the same in the 16 lanes of the row's DPP row, handed to `use` with
+// the row's block and index in it.
+template <int MT, int NT, typename Use>
+__device__ __forceinline__ void ctc_tile_rows(const f32x4 (&acc)[MT][NT], int n0, const float *bias, int vocab,
+                                              int lane, Use use) {
+  const int li = lane & 15;
   constexpr float L = 1.44269504088896341f;  // log2(e)
   float bn[NT];  // this lane's columns' bias, once for the tile's rows
 #pragma unroll
@@ -130,7 +141,6 @@ __device__ __forceinline__ void ctc_rows(const f32x4 (&acc)[MT][NT], int m_first
   for (int i = 0; i < MT; i++) {
 #pragma unroll
     for (int r = 0; r < 4; r++) {
-      const int m = m_first + i * 16 + lg * 4 + r;
       float v[NT];
       float lm = -__builtin_inff(), lb = __builtin_inff(), ls = -__builtin_inff();
 #pragma unroll
@@ -154,12 +164,36 @@ __device__ __forceinline__ void ctc_rows(const f32x4 (&acc)[MT][NT], int m_first
       for (int j = 0; j < NT; j++) sum += __builtin_amdgcn_exp2f(fmaf(v[j], L, -c));
       sum = row16_sum(sum);
       const float b = row16_min(lm == gm ? lb : __builtin_inff());
-      if (li == 0 && m < M) {
-        float4 *p = reinterpret_cast<float4 *>(part) + (long)m * ntn + tn;
-        *p = make_float4(gm, sum, b, g2);
-      }
+      use(i, r, make_float4(gm, sum, b, g2));
     }
   }
+}
+
+// One tile's per-row partials (max, sum of exp, first column of the max,
+// second value) to `part`, row m's tile tn at m * ntn + tn.
+template <int MT, int NT>
+__device__ __forceinline__ void ctc_rows(const f32x4 (&acc)[MT][NT], int m_first, int M, int n0, const float *bias,
+                                         int vocab, float *part, int ntn, int tn, int lane) {
+  const int li = lane & 15, lg = lane >> 4;
+  ctc_tile_rows<MT, NT>(acc, n0, bias, vocab, lane, [&](int i, int r, float4 rec) {
+    const int m = m_first + i * 16 + lg * 4 + r;
+    if (li == 0 && m < M) reinterpret_cast<float4 *>(part)[(long)m * ntn + tn] = rec;
+  });
+}
+
+// A run's partial of one row joined with its next tile's (`y`, columns
+// after x's; y's maximum is finite): the greater maximum, the sums rescaled
+// to it by hardware exp2 (the sum only makes the probability, held to
+// 1e-5 relative; the tiles' own sums use it too), the first column of the
+// maximum, and the second value of the two.
+__device__ __forceinline__ float4 ctc_join_partial(float4 x, float4 y) {
+  constexpr float L = 1.44269504088896341f;  // log2(e)
+  float m1, m2;
+  top2(x.x, x.w, y.x, y.w, m1, m2);
+  const float b = x.x > y.x ? x.z : (y.x > x.x ? y.z : fminf(x.z, y.z));
+  const float s = x.x > y.x ? x.y + y.y * __builtin_amdgcn_exp2f((y.x - x.x) * L)
+                            : y.y + x.y * __builtin_amdgcn_exp2f((x.x - y.x) * L);
+  return make_float4(m1, s, b, m2);
 }
 
 template <int WM, int BN, int BK, int LAY, bool CTC>
@@ -732,10 +766,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void c
 // further than the two orders ever differ.
 constexpr float kCtcTie = 1.0f / 1024.0f;
 
-__device__ __forceinline__ void top2(float a1, float a2, float b1, float b2, float &m1, float &m2) {
-  m1 = fmaxf(a1, b1);
-  m2 = a1 > b1 ? fmaxf(a2, b1) : (b1 > a1 ? fmaxf(b2, a1) : a1);
-}
 
 __global__ __launch_bounds__(256) void ctc_merge(const float4 *part, int rows, int ntiles, float *y,
                                                  long y_lane_stride, int rows_per_lane, CtcExact ex) {
@@ -842,7 +872,10 @@ __global__ __launch_bounds__(256) void ctc_merge(const float4 *part, int rows, i
 // from global memory straight into one of two LDS stages (direct loads, the
 // next tile's in flight while the MFMAs run on this one), and every wave
 // reads its B fragments from there, one 16-byte read per lane per block and
-// group. Each tile's per-row partials go to ctc_merge as before. The
+// group. Each row's partials are joined over runs of kCtcRunTiles tiles
+// (in column order, in registers) and go to ctc_merge as one record per row
+// and run, a sixth of the per-tile records; a workgroup walks one run or
+// more, as many as the row count needs for about kCtcTarget workgroups. The
 // workgroups of one run of columns take one XCD's consecutive slots, so the
 // run's weights meet in that XCD's L2. Reduction order: groups of 16 inputs
 // in order, within a group four steps of one input per lane group.
@@ -852,9 +885,10 @@ __global__ __launch_bounds__(256) void ctc_merge(const float4 *part, int rows, i
 constexpr int kCtcMt = 2;                 // row blocks of 16 a wave
 constexpr int kCtcRows = 64 * kCtcMt;     // rows a workgroup
 constexpr int kCtcTarget = 512;           // workgroups a launch aims at
+constexpr int kCtcRunTiles = 6;           // 64-column tiles a partial record joins
 
 template <int KQ>
-__global__ __launch_bounds__(256) void ctc_panel(CtcDirectArgs a, int row_tiles, int per_run) {
+__global__ __launch_bounds__(256) void ctc_panel(CtcDirectArgs a, int row_tiles, int per_run, int runs, int per_group) {
   constexpr int MT = kCtcMt, NT = 4, STAGE = NT * KQ * 64 * 4;  // floats
   extern __shared__ __attribute__((aligned(16))) float bs[];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -862,8 +896,8 @@ __global__ __launch_bounds__(256) void ctc_panel(CtcDirectArgs a, int row_tiles,
   const int M = a.rows_per_lane * a.lanes;
   const int ntn = (a.vocab + 63) / 64, nb = (a.vocab + 15) / 16;
   const int tile = xcd_tile(blockIdx.x, gridDim.x);
-  const int tm = tile % row_tiles, run = tile / row_tiles;
-  const int t0 = run * per_run, t1 = min(ntn, t0 + per_run);
+  const int tm = tile % row_tiles, group = tile / row_tiles;
+  const int t0 = group * per_group * per_run, t1 = min(ntn, t0 + per_group * per_run);
   const int m0 = tm * kCtcRows + wave * 16 * MT;
   if (t0 >= t1) return;
 
@@ -898,6 +932,8 @@ __global__ __launch_bounds__(256) void ctc_panel(CtcDirectArgs a, int row_tiles,
     }
   }
 
+  // The run's per-tile records of the workgroup's rows, joined at its end.
+  float4 *recs = reinterpret_cast<float4 *>(bs + 2 * STAGE);
   for (int t = t0; t < t1; t++) {
     const int st = (t - t0) & 1;
     // Every wave is done with the other stage (the tile before last).
@@ -928,29 +964,57 @@ __global__ __launch_bounds__(256) void ctc_panel(CtcDirectArgs a, int row_tiles,
           for (int j = 0; j < NT; j++)
             acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[i][q][e], bv[j][e], acc[i][j], 0, 0, 0);
     }
-    ctc_rows<MT, NT>(acc, m0, M, t * 64, a.bias, a.vocab, a.part, ntn, t, lane);
+    const int k = t % per_run;
+    ctc_tile_rows<MT, NT>(acc, t * 64, a.bias, a.vocab, lane, [&](int i, int r, float4 rec) {
+      if (li == 0) recs[(wave * 16 * MT + i * 16 + lg * 4 + r) * per_run + k] = rec;
+    });
+    // A run's last tile: each row's records joined in column order, one
+    // record out. (The next tile's stores wait behind its first barrier.)
+    if (k == per_run - 1 || t + 1 == t1) {
+      __syncthreads();
+      const int m = tm * kCtcRows + tid;
+      if (tid < kCtcRows && m < M) {
+        float4 run_rec = recs[tid * per_run];
+        for (int q = 1; q <= k; q++) run_rec = ctc_join_partial(run_rec, recs[tid * per_run + q]);
+        reinterpret_cast<float4 *>(a.part)[(long)m * runs + t / per_run] = run_rec;
+      }
+    }
   }
 }
 
 bool ctc_direct_supported(int ci) { return ci > 0 && ci <= 128 && ci % 4 == 0; }
 
+CtcRuns ctc_direct_runs(long rows, int vocab) {
+  const int row_tiles = (int)((rows + kCtcRows - 1) / kCtcRows), ntn = (vocab + 63) / 64;
+  CtcRuns r;
+  // The records' grouping of tiles is fixed, so that a row's joins, and so
+  // its bits, do not depend on how many rows the launch has; how many
+  // records a workgroup walks is what follows the row count: about
+  // kCtcTarget workgroups (two a CU, each holding two 32 KB stages).
+  r.per_run = std::min(kCtcRunTiles, ntn);
+  r.runs = (ntn + r.per_run - 1) / r.per_run;
+  r.columns = 64 * r.per_run;
+  r.per_group = std::max(1, int((long(row_tiles) * r.runs + kCtcTarget - 1) / kCtcTarget));
+  return r;
+}
+
 hipError_t launch_ctc_direct(const CtcDirectArgs &a, hipStream_t s) {
   if (!ctc_direct_supported(a.ci) || a.x_lane_stride % 4 || a.vocab <= 0) return hipErrorInvalidValue;
   const long M = (long)a.rows_per_lane * a.lanes;
   if (M <= 0 || M >= (1L << 31)) return hipErrorInvalidValue;
-  const int row_tiles = (int)((M + kCtcRows - 1) / kCtcRows), ntn = (a.vocab + 63) / 64;
-  // About two workgroups a CU (each holds two 32 KB stages).
-  const int runs = std::max(1, std::min(ntn, (kCtcTarget + row_tiles - 1) / row_tiles));
-  const int per_run = (ntn + runs - 1) / runs;
-  const unsigned blocks = (unsigned)(row_tiles * ((ntn + per_run - 1) / per_run));
+  const int row_tiles = (int)((M + kCtcRows - 1) / kCtcRows);
+  const CtcRuns r = ctc_direct_runs(M, a.vocab);
+  const int per_run = r.per_run, runs = r.runs;
+  const unsigned blocks = (unsigned)(row_tiles * ((runs + r.per_group - 1) / r.per_group));
   const int kq = enc_kpad(a.ci) / 16;
-  const size_t shm = (size_t)2 * 4 * kq * 64 * 16;
+  // Two weight stages, then the run's per-tile records.
+  const size_t shm = (size_t)2 * 4 * kq * 64 * 16 + size_t(kCtcRows) * per_run * 16;
   auto go = [&](auto kernel) {
     if (shm > 64 * 1024) {
       hipError_t e = allow_lds(reinterpret_cast<const void *>(kernel), int(shm));
       if (e != hipSuccess) return e;
     }
-    hipLaunchKernelGGL(kernel, dim3(blocks), dim3(256), shm, s, a, row_tiles, per_run);
+    hipLaunchKernelGGL(kernel, dim3(blocks), dim3(256), shm, s, a, row_tiles, per_run, runs, r.per_group);
     return hipGetLastError();
   };
   switch (kq) {

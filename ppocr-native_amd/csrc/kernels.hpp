@@ -191,7 +191,7 @@ struct CtcExact {
   long wt_k;
   const float *bias;   // per column
   int vocab;
-  int tile_n;          // columns per GEMM tile (the partials' width)
+  int tile_n;          // columns a partial record covers (a GEMM tile, or a run of tiles)
 };
 hipError_t launch_ctc_merge(const float *part, int rows, int ntiles, float *y, long y_lane_stride,
                             int rows_per_lane, const CtcExact &ex, hipStream_t s);
@@ -200,8 +200,9 @@ hipError_t launch_ctc_merge(const float *part, int rows, int ntiles, float *y, l
 // operands read straight into MFMA registers: the rows of x (ci floats,
 // rows_per_lane of them per lane) against the weights in enc_pack order
 // (kp = enc_kpad(ci), columns padded to 16), bias per column; per row and
-// 64-column tile a float4 partial (max, sum of exp, first column of the
-// max, second value) for launch_ctc_merge.
+// run of `columns` columns (ctc_direct_runs) a float4 partial (max, sum of
+// exp, first column of the max, second value), row m's run k at
+// part[m * runs + k], for launch_ctc_merge.
 struct CtcDirectArgs {
   const float *x;
   long x_lane_stride;
@@ -211,6 +212,13 @@ struct CtcDirectArgs {
   float *part;
 };
 bool ctc_direct_supported(int ci);
+struct CtcRuns {
+  int per_run;  // 64-column tiles a workgroup walks
+  int runs;     // runs over the columns: partial records per row
+  int columns;  // columns a record covers (the last run's may be fewer)
+  int per_group; // runs a workgroup walks
+};
+CtcRuns ctc_direct_runs(long rows, int vocab);
 hipError_t launch_ctc_direct(const CtcDirectArgs &a, hipStream_t s);
 
 // ---------------------------------------------------------------- depthwise

@@ -1218,16 +1218,18 @@ void Model::build_launches(Batch &b) {
         a.part = part;
         a.y = Y, a.y_lane_stride = ys;
         GemmTile t = s.tile;
-        int ntn = (a.n + t.bn - 1) / t.bn;
+        int ntn = (a.n + t.bn - 1) / t.bn, tile_n = t.bn;  // partial records per row, columns each
         int rows = L * int(op.iw), T = int(op.iw);
         if (ctc_direct_supported(int(op.ic))) {
           const CtcDirectArgs d{a.src[0].p, a.src[0].lane_stride, T, L, int(op.ic), dpacked + s.enc_w1, a.bias,
                                 a.vocab, part};
           b.launches.push_back({"ctc_gemm", s.op, [d](hipStream_t st) { return launch_ctc_direct(d, st); }});
+          const CtcRuns r = ctc_direct_runs(rows, a.vocab);
+          ntn = r.runs, tile_n = r.columns;
         } else {
           b.launches.push_back({"ctc_gemm", s.op, [a, t](hipStream_t st) { return launch_conv(a, t, st); }});
         }
-        const CtcExact ex{a.src[0].p, a.src[0].lane_stride, int(op.ic), a.wt, a.wt_k, a.bias, a.vocab, t.bn};
+        const CtcExact ex{a.src[0].p, a.src[0].lane_stride, int(op.ic), a.wt, a.wt_k, a.bias, a.vocab, tile_n};
         b.launches.push_back({"ctc_merge", s.op, [part, rows, ntn, Y, ys, T, ex](hipStream_t st) {
                                 return launch_ctc_merge(part, rows, ntn, Y, ys, T, ex, st);
                               }});
@@ -1740,6 +1742,7 @@ void Model::account(Batch &b) const {
       case S_CTC: {
         double M = L * op.iw, K = double(op.ic), N = double(op.n2);
         double ntn = double((s.gemm_n + s.tile.bn - 1) / s.tile.bn);
+        if (ctc_direct_supported(int(op.ic))) ntn = ctc_direct_runs(long(M), int(op.n2)).runs;
         l.flops = 2.0 * M * N * K;
         l.bytes = F * (M * K + K * N + N + 2 * M);
         Launch &merge = b.launches[li++];
