@@ -151,19 +151,24 @@ __global__ __launch_bounds__(MEAN ? TB : 256) void dwconv_fixed(DwArgs a) {
 #pragma unroll
     for (int o = 0; o < DX; o++) acc[o] = bias;
     const int left = ox0 * S - a.pl;
+    bool in[SPAN];
+#pragma unroll
+    for (int i = 0; i < SPAN; i++) in[i] = left + i >= 0 && left + i < a.iw;
+    // 3 x 3 windows: every row's loads are unconditional (a row outside the
+    // image reads the nearest one, whose taps are then skipped), so that the
+    // compiler issues all three rows' loads before the first multiply-add
+    // (one wait instead of three, 119 registers). Wider windows would need
+    // 256 registers that way: their rows load in turn.
+    constexpr bool kAllRows = K == 3;
 #pragma unroll
     for (int ky = 0; ky < K; ky++) {
       const int iy = oy * a.sh + ky - a.pt;
-      if (iy < 0 || iy >= a.ih) continue;
-      const float *row = x + (long)iy * a.iw * a.c;
+      const bool row_in = iy >= 0 && iy < a.ih;
+      if (!kAllRows && !row_in) continue;
+      const float *row = x + (long)min(max(iy, 0), a.ih - 1) * a.iw * a.c;
       f32x4 seg[SPAN], wk[K];
-      bool in[SPAN];
 #pragma unroll
-      for (int i = 0; i < SPAN; i++) {
-        const int ix = left + i;
-        in[i] = ix >= 0 && ix < a.iw;
-        seg[i] = in[i] ? *reinterpret_cast<const f32x4 *>(row + (long)ix * a.c) : zero;
-      }
+      for (int i = 0; i < SPAN; i++) seg[i] = in[i] ? *reinterpret_cast<const f32x4 *>(row + (long)(left + i) * a.c) : zero;
 #pragma unroll
       for (int kx = 0; kx < K; kx++) wk[kx] = *reinterpret_cast<const f32x4 *>(a.w + (long)(ky * K + kx) * a.c + ch);
 #pragma unroll
@@ -171,7 +176,7 @@ __global__ __launch_bounds__(MEAN ? TB : 256) void dwconv_fixed(DwArgs a) {
 #pragma unroll
         for (int o = 0; o < DX; o++) {
           const int i = o * S + kx;
-          if (in[i]) {
+          if (row_in && in[i]) {
             acc[o].x = fmaf(wk[kx].x, seg[i].x, acc[o].x);
             acc[o].y = fmaf(wk[kx].y, seg[i].y, acc[o].y);
             acc[o].z = fmaf(wk[kx].z, seg[i].z, acc[o].z);
