@@ -499,16 +499,20 @@ def trace_runs(P, nets, which: str, runs: int) -> None:
     one workload, inputs resident, then its launch list (kernel, plan
     operations, layer FLOPs and algorithmic bytes), one JSON line each, in
     dispatch order. `copy` is the plain copy kernel (activation code 0) over
-    1x256x240x240 floats that HBM counters are scaled by."""
-    if which == "copy":
+    1x256x240x240 floats that HBM counters are scaled by; `copy_lds` the same
+    copy through LDS by direct loads, the scale for kernels that load so."""
+    if which in ("copy", "copy_lds"):
         from ppocr_native_amd.devmem import DeviceArray, synchronize
         n = 240 * 240 * 256
         a = DeviceArray.of(np.random.default_rng(0).uniform(-1, 1, n).astype(np.float32))
         y = DeviceArray(4 * n)
         for _ in range(runs):
-            P.hip_activation(a.addr, y.addr, n, 0)
+            if which == "copy":
+                P.hip_activation(a.addr, y.addr, n, 0)
+            else:
+                P.hip_copy_lds(a.addr, y.addr, n)
         synchronize()
-        print(json.dumps({"name": "copy", "ops": [], "flops": 0, "bytes": 8 * n}), flush=True)
+        print(json.dumps({"name": which, "ops": [], "flops": 0, "bytes": 8 * n}), flush=True)
         return
     if which == "det":
         g = P.GpuModel.load(nets.detector_plan(h=960, w=960, init="baseline"))
@@ -538,7 +542,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--cpu-seconds", type=float, default=30.0)
     ap.add_argument("--only", choices=["det", "rec", "all"], default="all")
-    ap.add_argument("--trace", choices=["det", "rec", "block", "copy"],
+    ap.add_argument("--trace", choices=["det", "rec", "block", "copy", "copy_lds"],
                     help="only run --trace-runs eager passes of one workload (for rocprofv3) "
                          "and print its launch list")
     ap.add_argument("--trace-runs", type=int, default=3)

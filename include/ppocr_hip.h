@@ -180,6 +180,13 @@ int ppocr_hip_mul(const float *a, const float *b, float *y, size_t n, void *stre
 /* y = act(x) for one folded activation code (src/engine/conv.rs:59-71). */
 int ppocr_hip_activation(const float *x, float *y, size_t n, int act, void *stream);
 
+/* Measurement helper, no counterpart in the reference: y = x over n floats
+ * (n a multiple of 4, 16-byte aligned pointers) through LDS by direct
+ * global-to-LDS loads, the load path of the GEMM rings and the depthwise
+ * tiles; it calibrates the memory counters for kernels that load that way
+ * (ppocr_hip_activation with code 0 is the plain vector-load copy). */
+int ppocr_hip_copy_lds(const float *x, float *y, size_t n, void *stream);
+
 /* `Kind::Mean` (src/engine/layers.rs:391-406): y[c] = mean over `pixels` of
  * x[p][c], summed in f64. */
 int ppocr_hip_channel_mean(const float *x, float *y, size_t pixels, size_t c, void *stream);

@@ -75,6 +75,7 @@ def lib() -> C.CDLL:
         "ppocr_hip_add": ([vp, vp, vp, sz, C.c_int, vp], C.c_int),
         "ppocr_hip_mul": ([vp, vp, vp, sz, vp], C.c_int),
         "ppocr_hip_activation": ([vp, vp, sz, C.c_int, vp], C.c_int),
+        "ppocr_hip_copy_lds": ([vp, vp, sz, vp], C.c_int),
         "ppocr_hip_channel_mean": ([vp, vp, sz, sz, vp], C.c_int),
         "ppocr_hip_channel_mean_noalloc": ([vp, vp, sz, sz, vp, C.c_char_p, sz], C.c_int),
         "ppocr_hip_channel_mul": ([vp, vp, vp, sz, sz, vp], C.c_int),
@@ -285,6 +286,11 @@ def hip_mul(a: int, b: int, y: int, n: int, stream: int = 0) -> None:
 
 def hip_activation(x: int, y: int, n: int, act: int, stream: int = 0) -> None:
     _check(lib().ppocr_hip_activation(x, y, n, act, stream or None), "ppocr_hip_activation")
+
+
+def hip_copy_lds(x: int, y: int, n: int, stream: int = 0) -> None:
+    """y = x through LDS by direct loads (the counters' calibration copy)."""
+    _check(lib().ppocr_hip_copy_lds(x, y, n, stream or None), "ppocr_hip_copy_lds")
 
 
 def hip_channel_mean(x: int, y: int, pixels: int, c: int, stream: int = 0) -> None:

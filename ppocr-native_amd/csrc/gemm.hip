@@ -844,7 +844,9 @@ __global__ __launch_bounds__(256) void ctc_merge(const float4 *part, int rows, i
       if (part[(long)row * ntiles + t].x < st.m - tie) continue;
       const int c1 = min((t + 1) * ex.tile_n, ex.vocab);
       for (int c0 = t * ex.tile_n; c0 < c1; c0 += 64) {
-        c0s[nq] = c0, c1s[nq] = c1, nq++;
+        // A record over several tiles: only its tiles whose own maximum is close.
+        if (ex.tmax && ex.tmax[(long)(c0 / 64) * rows + row] < st.m - tie) continue;
+        c0s[nq] = c0, c1s[nq] = min(c0 + 64, c1), nq++;
         if (nq == 4) run();
       }
     }
@@ -966,7 +968,9 @@ __global__ __launch_bounds__(256) void ctc_panel(CtcDirectArgs a, int row_tiles,
     }
     const int k = t % per_run;
     ctc_tile_rows<MT, NT>(acc, t * 64, a.bias, a.vocab, lane, [&](int i, int r, float4 rec) {
-      if (li == 0) recs[(wave * 16 * MT + i * 16 + lg * 4 + r) * per_run + k] = rec;
+      const int row = wave * 16 * MT + i * 16 + lg * 4 + r;
+      if (li == 0) recs[row * per_run + k] = rec;
+      if (li == 0 && a.tmax && m0 + i * 16 + lg * 4 + r < M) a.tmax[(long)t * M + m0 + i * 16 + lg * 4 + r] = rec.x;
     });
     // A run's last tile: each row's records joined in column order, one
     // record out. (The next tile's stores wait behind its first barrier.)

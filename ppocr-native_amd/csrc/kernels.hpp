@@ -192,6 +192,8 @@ struct CtcExact {
   const float *bias;   // per column
   int vocab;
   int tile_n;          // columns a partial record covers (a GEMM tile, or a run of tiles)
+  const float *tmax;   // or per 64-column tile and row its maximum, tile t's row m at t * rows + m
+  int tmax_n;          // tiles
 };
 hipError_t launch_ctc_merge(const float *part, int rows, int ntiles, float *y, long y_lane_stride,
                             int rows_per_lane, const CtcExact &ex, hipStream_t s);
@@ -210,6 +212,7 @@ struct CtcDirectArgs {
   const float *wt, *bias;
   int vocab;
   float *part;
+  float *tmax;  // optional: per 64-column tile and row its maximum, tile t's row m at t * rows + m
 };
 bool ctc_direct_supported(int ci);
 struct CtcRuns {
@@ -512,6 +515,7 @@ hipError_t launch_db_head(const HeadArgs &a, hipStream_t s);
 
 // mask[i] = prob[i] > thresh over n floats (bytes out).
 hipError_t launch_db_mask(const float *prob, uint8_t *mask, long n, float thresh, hipStream_t s);
+hipError_t launch_copy_lds(const float *x, float *y, long n, hipStream_t s);
 hipError_t launch_db_bits(const float *map, long lane_stride, int w, int h, int lanes, float thresh,
                           unsigned long long *bits, hipStream_t s);
 

@@ -1769,6 +1769,36 @@ hipError_t launch_db_mask(const float *prob, uint8_t *mask, long n, float thresh
   return hipGetLastError();
 }
 
+// A copy of n4 float4s through LDS by direct loads (global_load_lds, 16
+// bytes a lane, 1024 float4s a block), the way the GEMM rings and the
+// depthwise tiles load: the memory counters' calibration for such kernels.
+__global__ __launch_bounds__(256) void copy_lds_kernel(const float *x, float *y, long n4) {
+  __shared__ __attribute__((aligned(16))) float buf[1024 * 4];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const long base = (long)blockIdx.x * 1024;
+#pragma unroll
+  for (int q = 0; q < 4; q++) {
+    const int ins = q * 4 + wave;  // the wave's direct load: float4s 64 ins .. 64 ins + 63
+    const long u = base + ins * 64 + lane;
+    const float *p = u < n4 ? x + 4 * u : kDwZeros;
+    __builtin_amdgcn_global_load_lds((const void *)p, (lds_void *)(buf + ins * 256), 16, 0, 0);
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+#pragma unroll
+  for (int q = 0; q < 4; q++) {
+    const long u = base + q * 256 + tid;
+    if (u < n4) reinterpret_cast<f32x4 *>(y)[u] = reinterpret_cast<const f32x4 *>(buf)[q * 256 + tid];
+  }
+}
+
+hipError_t launch_copy_lds(const float *x, float *y, long n, hipStream_t s) {
+  if (n <= 0 || n % 4 || (uintptr_t(x) & 15) || (uintptr_t(y) & 15)) return hipErrorInvalidValue;
+  const long n4 = n / 4;
+  hipLaunchKernelGGL(copy_lds_kernel, dim3(unsigned((n4 + 1023) / 1024)), dim3(256), 0, s, x, y, n4);
+  return hipGetLastError();
+}
+
 // The DB threshold as row bitmasks (src/det.rs:438, compared in f32): one
 // wave per 64-pixel word of a row, each lane one pixel, the wave's ballot
 // the word (bit x % 64 of word x / 64; pixels past the width are 0). The

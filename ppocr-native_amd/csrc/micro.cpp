@@ -188,6 +188,11 @@ int ppocr_hip_activation(const float *x, float *y, size_t n, int act, void *stre
   return code(launch_eltwise(flat(ELT_ACT, x, nullptr, y, n, act), hipStream_t(stream)));
 }
 
+int ppocr_hip_copy_lds(const float *x, float *y, size_t n, void *stream) {
+  if (n == 0) return 0;
+  return code(launch_copy_lds(x, y, long(n), hipStream_t(stream)));
+}
+
 int ppocr_hip_channel_mean(const float *x, float *y, size_t pixels, size_t c, void *stream) {
   if (pixels == 0 || c == 0 || pixels > 0x7fffffff || c > 0x7fffffff) return int(hipErrorInvalidValue);
   const MeanShape m = mean_shape(true, int(pixels), int(c), 1, 0, false);

@@ -1032,6 +1032,10 @@ bool Model::arrange(Batch &b, std::string &err) {
     if (s.kind == S_CTC) {
       size_t ntn = (s.gemm_n + s.tile.bn - 1) / s.tile.bn;
       need = L * op.iw * ntn * 4;
+      if (ctc_direct_supported(int(op.ic))) {  // run records, then the per-tile maxima
+        const CtcRuns r = ctc_direct_runs(long(L * op.iw), int(op.n2));
+        need = std::max(need, L * op.iw * (size_t(r.runs) * 4 + (op.n2 + 63) / 64));
+      }
     }
     if (s.kind == S_ATTN) need = attention_scratch_floats(int(op.iw), int(op.oc), int(op.n2), int(L));
     // Lines too long for the fused attention's LDS: attention rows, then the
@@ -1220,16 +1224,21 @@ void Model::build_launches(Batch &b) {
         GemmTile t = s.tile;
         int ntn = (a.n + t.bn - 1) / t.bn, tile_n = t.bn;  // partial records per row, columns each
         int rows = L * int(op.iw), T = int(op.iw);
+        float *tmax = nullptr;  // per-tile maxima after a run's records, for the near-tie recheck
+        int tiles = 0;
         if (ctc_direct_supported(int(op.ic))) {
-          const CtcDirectArgs d{a.src[0].p, a.src[0].lane_stride, T, L, int(op.ic), dpacked + s.enc_w1, a.bias,
-                                a.vocab, part};
-          b.launches.push_back({"ctc_gemm", s.op, [d](hipStream_t st) { return launch_ctc_direct(d, st); }});
           const CtcRuns r = ctc_direct_runs(rows, a.vocab);
+          tiles = (a.vocab + 63) / 64;
+          tmax = part + size_t(rows) * r.runs * 4;
+          const CtcDirectArgs d{a.src[0].p, a.src[0].lane_stride, T, L, int(op.ic), dpacked + s.enc_w1, a.bias,
+                                a.vocab, part, tmax};
+          b.launches.push_back({"ctc_gemm", s.op, [d](hipStream_t st) { return launch_ctc_direct(d, st); }});
           ntn = r.runs, tile_n = r.columns;
         } else {
           b.launches.push_back({"ctc_gemm", s.op, [a, t](hipStream_t st) { return launch_conv(a, t, st); }});
         }
-        const CtcExact ex{a.src[0].p, a.src[0].lane_stride, int(op.ic), a.wt, a.wt_k, a.bias, a.vocab, tile_n};
+        const CtcExact ex{a.src[0].p, a.src[0].lane_stride, int(op.ic), a.wt, a.wt_k, a.bias, a.vocab, tile_n,
+                          tmax, tiles};
         b.launches.push_back({"ctc_merge", s.op, [part, rows, ntn, Y, ys, T, ex](hipStream_t st) {
                                 return launch_ctc_merge(part, rows, ntn, Y, ys, T, ex, st);
                               }});

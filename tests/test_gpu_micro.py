@@ -131,3 +131,14 @@ def test_db_mask_gives_the_boxes(n):
         got = post.boxes_from_prob(full, 320, 320, 325, 323, mask=dm.download(n, np.uint8))
         assert np.array_equal(post.boxes_from_prob(full, 320, 320, 325, 323), got)
         assert got.shape == (11, 4, 2)
+
+
+@pytest.mark.parametrize("n", [240 * 240 * 256, 4 * 1000 + 4 * 513])
+def test_copy_through_lds(n):
+    # The counters' calibration copy by direct-to-LDS loads: every float in
+    # place, a partial last block included.
+    x = np.random.default_rng(3).uniform(-1, 1, n).astype(np.float32)
+    dx, dy = DeviceArray.of(x), DeviceArray(4 * n)
+    P.hip_copy_lds(dx.addr, dy.addr, n)
+    synchronize()
+    assert np.array_equal(dy.download(n).view(np.uint32), x.view(np.uint32))
