@@ -167,9 +167,16 @@ def bench_block(P, nets, steps, warmup):
     rows = profile(g, 20)
     g.close()
     flops = sum(r["flops"] for r in rows)
+    # Compulsory bytes: the block's input read once and its output written
+    # once (weights are a few hundred KB and stay in cache).
+    compulsory = 2 * 160 * 160 * 96 * 4
+    rate = compulsory / (ms * 1e-3) / 1e9
     return {"workload": "fused dw3x3+SE+pw block 1x96x160x160", "ms": round(ms, 4),
             "gflops_per_s": round(flops / (ms * 1e-3) / 1e9, 1),
-            "compulsory_gb_per_s": round(2 * 160 * 160 * 96 * 4 / (ms * 1e-3) / 1e9, 1),
+            "compulsory_bytes": compulsory,
+            "compulsory_gb_per_s": round(rate, 1),
+            "compulsory_frac": round(rate / PEAK_HBM_GBS, 4),
+            "compulsory_floor_ms": round(compulsory / (PEAK_HBM_GBS * 1e9) * 1e3, 4),
             "launches": by_kernel(rows)}
 
 
