@@ -1432,13 +1432,16 @@ bool ring_fits(const ConvArgs &a, const RingTile &t) {
   return ring_lds(a, t.mt, t.nt, t.st, t.bk) <= kMaxLdsBytes;
 }
 
+size_t ring_lds_bytes(const ConvArgs &a, const RingTile &t) { return ring_lds(a, t.mt, t.nt, t.st, t.bk); }
+
 #define PPOCR_RING(MT, NT, ST, BK) \
   if (t.mt == MT && t.nt == NT && t.st == ST && t.bk == BK) return go_ring<MT, NT, ST, BK>(as, n, s);
 
 // The tiles compiled (ring_tile in the model picks among them).
 #define PPOCR_RING_TILES                                                                         \
-  PPOCR_RING(1, 1, 3, 32) PPOCR_RING(1, 1, 4, 32) PPOCR_RING(1, 2, 3, 32) PPOCR_RING(1, 2, 4, 32) \
-  PPOCR_RING(1, 3, 3, 32) PPOCR_RING(1, 3, 4, 32)
+  PPOCR_RING(1, 1, 2, 32) PPOCR_RING(1, 1, 3, 32) PPOCR_RING(1, 1, 4, 32) PPOCR_RING(1, 2, 2, 32) \
+  PPOCR_RING(1, 2, 3, 32) PPOCR_RING(1, 2, 4, 32) PPOCR_RING(1, 3, 2, 32) PPOCR_RING(1, 3, 3, 32) \
+  PPOCR_RING(1, 3, 4, 32)
 
 hipError_t launch_conv_ring_group(const ConvArgs *as, int n, const RingTile &t, hipStream_t s) {
   if (n < 1 || n > kGroupMax) return hipErrorInvalidValue;

@@ -165,6 +165,7 @@ struct RingTile {
 };
 bool ring_supported(const ConvArgs &a);
 bool ring_fits(const ConvArgs &a, const RingTile &t);
+size_t ring_lds_bytes(const ConvArgs &a, const RingTile &t);  // dynamic LDS of one workgroup
 hipError_t launch_conv_ring(const ConvArgs &a, const RingTile &t, hipStream_t s);
 // n <= kGroupMax problems, each ring_supported with the same gate and window
 // kind and ring_fits for t, as one launch.

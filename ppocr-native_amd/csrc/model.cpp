@@ -734,6 +734,36 @@ static RingTile ring_tile(long M, int N) {
   return RingTile{1, nt, tiles(nt) >= 512 ? 3 : 4, 32};
 }
 
+// Rounds of workgroups a ring launch of `tiles` tiles takes: a CU holds as
+// many as its 160 KB of LDS and its 32 wave slots (eight workgroups of four
+// waves) allow.
+static long ring_rounds(long tiles, size_t lds) {
+  constexpr long kCUs = 256;  // MI355X
+  const long per_cu = std::max<long>(1, std::min<long>(8, long(160 * 1024 / std::max<size_t>(lds, 1))));
+  return (tiles + kCUs * per_cu - 1) / (kCUs * per_cu);
+}
+
+// ring_tile for the launch of `as` (M rows in all), with two stages instead
+// of three where that leaves room for enough workgroups a CU to run every
+// tile in fewer rounds: a launch one round longer than it needs waits out
+// its last workgroups with the GPU nearly idle (the fused block's gated
+// 96 -> 96 1x1 over 160 x 160 pixels: 800 tiles, 768 at once with three
+// stages, 1024 with two).
+static RingTile ring_tile(const std::vector<ConvArgs> &as, long M) {
+  RingTile t = ring_tile(M, as[0].n);
+  if (t.st != 3) return t;
+  long tiles = 0;
+  size_t lds3 = 0, lds2 = 0;
+  RingTile t2 = t;
+  t2.st = 2;
+  for (const ConvArgs &a : as) {
+    tiles += (long(a.lanes) * a.oh * a.ow + 31) / 32 * ((a.n + 32L * t.nt - 1) / (32L * t.nt));
+    lds3 = std::max(lds3, ring_lds_bytes(a, t));
+    lds2 = std::max(lds2, ring_lds_bytes(a, t2));
+  }
+  return ring_rounds(tiles, lds2) < ring_rounds(tiles, lds3) ? t2 : t;
+}
+
 // row n of the packed matrix holds column n's reduction in the kernel's chunk
 // order, zero where the padding of a chunk lies.
 //  - channel layout (every source's channels a multiple of 4): per tap, the
@@ -1188,8 +1218,8 @@ void Model::build_launches(Batch &b) {
         }
         long M = long(L) * a.oh * a.ow;
         a.xcd_rows = 1;
-        if ((t.pointwise || s.ring) && ring_supported(a) && ring_fits(a, ring_tile(M, a.n))) {
-          const RingTile rt = ring_tile(M, a.n);
+        if ((t.pointwise || s.ring) && ring_supported(a) && ring_fits(a, ring_tile({a}, M))) {
+          const RingTile rt = ring_tile({a}, M);
           const char *nm = op.kind == K_CONVTRANSPOSE ? "convt_gemm" : (t.pointwise ? "pointwise_gemm" : "conv_gemm");
           b.launches.push_back({nm, s.op, [a, rt](hipStream_t st) { return launch_conv_ring(a, rt, st); }});
           Launch &l = b.launches.back();
@@ -1662,7 +1692,7 @@ void Model::group(Batch &b) const {
           M += long(a.lanes) * a.oh * a.ow;
           same_n = same_n && a.n == as[0].n;
         }
-        RingTile t = same_n ? ring_tile(M, as[0].n) : gl.rt;
+        RingTile t = same_n ? ring_tile(as, M) : gl.rt;
         for (const ConvArgs &a : as)
           if (!ring_fits(a, t)) t = gl.rt;
         gl.fn = [as, t](hipStream_t st) { return launch_conv_ring_group(as.data(), int(as.size()), t, st); };
