@@ -1183,36 +1183,40 @@ __global__ __launch_bounds__(256) void conv_ring(Group<ConvArgs> grp) {
     b_src[i] = n < a.n ? a.wt + (long)n * a.wt_k + g * 4 : nullptr;
   }
 
+  // The fields the loads test, read once: `a` lives in the kernel
+  // arguments, which the compiler would otherwise read again for every
+  // chunk (its direct loads write memory), waiting on each read.
+  const int ctot = a.ctot, ih = a.ih, iw = a.iw, cpt = a.cpt, kw = a.kw;
   auto issue = [&](int q, int st) {
     const int k0 = q * BK;
     float *base = ring + st * STAGE;
     // Windowed: chunk q is channel block cc of tap (ky, kx).
     int ky = 0, kx = 0, cb = 0;
     if constexpr (WIN) {
-      const int tap = q / a.cpt;
-      cb = (q - tap * a.cpt) * BK;
-      ky = tap / a.kw;
-      kx = tap - ky * a.kw;
+      const int tap = q / cpt;
+      cb = (q - tap * cpt) * BK;
+      ky = tap / kw;
+      kx = tap - ky * kw;
     }
 #pragma unroll
     for (int i = 0; i < R::A_I; i++) {
       const float *p = kRingZeros;
       if constexpr (WIN) {
         const int c = cb + a_k[i], iy = a_y[i] + ky, ix = a_x[i] + kx;
-        if (c < a.ctot && iy >= 0 && iy < a.ih && ix >= 0 && ix < a.iw) {
+        if (c < ctot && iy >= 0 && iy < ih && ix >= 0 && ix < iw) {
           const ConvSrc s = pick_src(a, c);
-          const long pix = (long)(iy >> s.shift) * (a.iw >> s.shift) + (ix >> s.shift);
+          const long pix = (long)(iy >> s.shift) * (iw >> s.shift) + (ix >> s.shift);
           p = s.p + (long)a_ln[i] * s.lane_stride + pix * s.c + (c - s.coff);
         }
       } else {
-        if (a_src[i] && k0 + a_k[i] < a.ctot) p = a_src[i] + k0;
+        if (a_src[i] && k0 + a_k[i] < ctot) p = a_src[i] + k0;
       }
       __builtin_amdgcn_global_load_lds((const void *)p, (lds_void *)(base + (i * 4 + wave) * RPI * BK), 16, 0, 0);
     }
     // The packed rows are zero past each tap's channels.
 #pragma unroll
     for (int i = 0; i < R::B_I; i++) {
-      const float *p = b_src[i] && (WIN || k0 + b_k[i] < a.ctot) ? b_src[i] + k0 : kRingZeros;
+      const float *p = b_src[i] && (WIN || k0 + b_k[i] < ctot) ? b_src[i] + k0 : kRingZeros;
       __builtin_amdgcn_global_load_lds((const void *)p, (lds_void *)(base + (BM + (i * 4 + wave) * RPI) * BK), 16,
                                        0, 0);
     }
