@@ -955,13 +955,18 @@ bool Model::load(const uint8_t *bytes, size_t len, std::string &err) {
   if (name.empty()) name = prop.gcnArchName;
   integrated = prop.integrated;
   device_bytes = prop.totalGlobalMem;
-  HIPTRY(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking), "creating a stream");
+  // The weights go up (on the null stream) before the model's stream is
+  // created: HIP gives a process's streams its hardware queues in the order
+  // they are first used, and a null stream first used after the streams of
+  // several models that run at once (the page path: a detector and three
+  // recognisers) slowed them (1.47 -> 1.80 ms a page, with eight queues).
   HIPTRY(hipMalloc(&dweights, std::max<size_t>(weights.size(), 1) * sizeof(float)),
          "allocating the weights");
   if (!weights.empty())
     HIPTRY(hipMemcpy(dweights, weights.data(), weights.size() * sizeof(float),
                      hipMemcpyHostToDevice),
            "uploading the weights");
+  HIPTRY(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking), "creating a stream");
   if (!pack(err)) return false;
   size_t hw[2] = {plan.in_h, plan.in_w};
   return set_sizes(hw, 1, err);

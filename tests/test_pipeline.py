@@ -4,7 +4,7 @@ oracle's recogniser input with the tensor width capped at 320."""
 import numpy as np
 import pytest
 
-from ppocr_native_amd.pipeline import det_size
+from ppocr_native_amd.pipeline import default_recognisers, det_size
 
 
 def test_det_size_reference_cases():
@@ -44,3 +44,14 @@ def test_rec_input_capped_width(oracle):
     assert np.array_equal(oracle.rec_input(wide, 320), want)
     # No cap: the reference's width.
     assert oracle.rec_input(wide).shape == (48, 2167, 3)
+
+
+@pytest.mark.parametrize("queues,want", [(None, 2), ("4", 2), ("5", 3), ("8", 3), ("junk", 2)])
+def test_default_recognisers_follow_the_queue_count(monkeypatch, queues, want):
+    # Three recogniser handles only when every stream of the page path (the
+    # detector's, three recognisers' and the null stream) has a queue.
+    if queues is None:
+        monkeypatch.delenv("GPU_MAX_HW_QUEUES", raising=False)
+    else:
+        monkeypatch.setenv("GPU_MAX_HW_QUEUES", queues)
+    assert default_recognisers() == want
