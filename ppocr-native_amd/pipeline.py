@@ -142,8 +142,9 @@ class PagePipeline:
     def read_pages(self, pages: list[tuple[int, int, int]]) -> list[list[Line]]:
         """The text lines of each page (device address, width, height), in
         order. While the GPU reads a page's lines, the host finds the next
-        page's boxes (its detector queued meanwhile), so that host and GPU
-        work overlap."""
+        page's boxes (its detector queued meanwhile), and while it reads the
+        next page's lines, the host decodes this page's text, so that host
+        and GPU work overlap."""
         out: list[list[Line]] = []
         if not pages:
             return out
@@ -151,10 +152,14 @@ class PagePipeline:
         sizes: list[tuple[int, int] | None] = [None] * len(pages)
         sizes[0] = self._detect(*pages[0])
         quads = self._boxes(0, pages, sizes)
-        for k, (page, width, height) in enumerate(pages):
-            job = self._queue_page(page, width, height, quads)
+        job = self._queue_page(*pages[0], quads)
+        for k in range(len(pages)):
             following = self._boxes(k + 1, pages, sizes) if k + 1 < len(pages) else None
             pairs = self._finish_page(job)
+            # The next page's lines go to the GPU before this page's text is
+            # decoded on the host (its outputs are copies by now).
+            if following is not None:
+                job = self._queue_page(*pages[k + 1], following)
             t0 = time.perf_counter()
             out.append([Line(q, *ctc_decode_pairs(p, self.dictionary)) for q, p in zip(quads, pairs)])
             self.times.decode += (time.perf_counter() - t0) * 1e3
