@@ -868,7 +868,7 @@ __global__ __launch_bounds__(256) void ctc_merge(const float4 *part, int rows, i
 // ------------------------------------------------------------ CTC, panels
 
 // The CTC head's GEMM when the head's input is at most 128 wide. A
-// workgroup keeps 128 rows (four waves of 32) in its operand registers for
+// workgroup keeps 128 rows (eight waves of 16) in its operand registers for
 // the whole launch and walks a run of 64-column tiles: each tile's weights
 // (enc_pack order: four column blocks, 4 KB per group of 16 inputs) come
 // from global memory straight into one of two LDS stages (direct loads, the
@@ -881,17 +881,21 @@ __global__ __launch_bounds__(256) void ctc_merge(const float4 *part, int rows, i
 // workgroups of one run of columns take one XCD's consecutive slots, so the
 // run's weights meet in that XCD's L2. Reduction order: groups of 16 inputs
 // in order, within a group four steps of one input per lane group.
-// Measured on 1280 x 18385 x 120: 32-row waves (64-row waves: 72 -> 86 us,
-// their 230 VGPRs leave one wave a SIMD) and about 512 workgroups (256:
-// 88 us, 1024: 74 us).
-constexpr int kCtcMt = 2;                 // row blocks of 16 a wave
-constexpr int kCtcRows = 64 * kCtcMt;     // rows a workgroup
+// Measured on 1280 x 18385 x 120: 16-row waves, eight a workgroup (96
+// VGPRs, four waves a SIMD with two workgroups a CU; four waves of 32 rows:
+// 71.4 us at two waves a SIMD; of 64 rows: 86 us, their 230 VGPRs leave one
+// wave a SIMD) and about 512 workgroups (256: 88 us, 1024: 74 us, with four
+// waves of 32 rows).
+constexpr int kCtcRows = 128;             // rows a workgroup
+constexpr int kCtcWaves = 8;              // waves a workgroup, 128 / (16 * kCtcWaves) row blocks each
 constexpr int kCtcTarget = 512;           // workgroups a launch aims at
 constexpr int kCtcRunTiles = 6;           // 64-column tiles a partial record joins
 
 template <int KQ>
-__global__ __launch_bounds__(256) void ctc_panel(CtcDirectArgs a, int row_tiles, int per_run, int runs, int per_group) {
-  constexpr int MT = kCtcMt, NT = 4, STAGE = NT * KQ * 64 * 4;  // floats
+__global__ __launch_bounds__(64 * kCtcWaves) void ctc_panel(CtcDirectArgs a, int row_tiles, int per_run, int runs,
+                                                            int per_group) {
+  constexpr int W = kCtcWaves, MT = kCtcRows / (16 * W), NT = 4, STAGE = NT * KQ * 64 * 4;  // floats
+  constexpr int TPI = NT * KQ * 64 / (64 * W);  // direct loads a thread issues a tile
   extern __shared__ __attribute__((aligned(16))) float bs[];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int li = lane & 15, lg = lane >> 4;
@@ -909,12 +913,12 @@ __global__ __launch_bounds__(256) void ctc_panel(CtcDirectArgs a, int row_tiles,
   auto issue = [&](int t, int st) {
     const f32x4 *src = reinterpret_cast<const f32x4 *>(a.wt);
 #pragma unroll
-    for (int i = 0; i < NT * KQ / 4; i++) {
-      const int e = i * 256 + tid;  // 16-byte group of the tile
+    for (int i = 0; i < TPI; i++) {
+      const int e = i * 64 * W + tid;  // 16-byte group of the tile
       const int blk = min(t * 4 + e / (KQ * 64), nb - 1);
       const f32x4 *p = src + (long)blk * KQ * 64 + e % (KQ * 64);
-      __builtin_amdgcn_global_load_lds((const void *)p, (lds_void *)(bs + st * STAGE + (i * 256 + wave * 64) * 4), 16,
-                                       0, 0);
+      __builtin_amdgcn_global_load_lds((const void *)p, (lds_void *)(bs + st * STAGE + (i * 64 * W + wave * 64) * 4),
+                                       16, 0, 0);
     }
   };
   issue(t0, 0);
@@ -942,7 +946,7 @@ __global__ __launch_bounds__(256) void ctc_panel(CtcDirectArgs a, int row_tiles,
     ring_barrier();
     if (t + 1 < t1) {
       issue(t + 1, st ^ 1);
-      ring_wait<NT * KQ / 4>();
+      ring_wait<TPI>();
     } else {
       ring_wait<0>();
     }
@@ -1018,7 +1022,7 @@ hipError_t launch_ctc_direct(const CtcDirectArgs &a, hipStream_t s) {
       hipError_t e = allow_lds(reinterpret_cast<const void *>(kernel), int(shm));
       if (e != hipSuccess) return e;
     }
-    hipLaunchKernelGGL(kernel, dim3(blocks), dim3(256), shm, s, a, row_tiles, per_run, runs, r.per_group);
+    hipLaunchKernelGGL(kernel, dim3(blocks), dim3(64 * kCtcWaves), shm, s, a, row_tiles, per_run, runs, r.per_group);
     return hipGetLastError();
   };
   switch (kq) {
