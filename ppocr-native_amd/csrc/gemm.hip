@@ -757,14 +757,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void c
 
 // One wave per row: join the row's tile partials, then y = (best, 1 / sum).
 // The tiles also carry their second value: when the row's two largest
-// values lie within kCtcTie * max(1, |max|) of each other, the GPU's
-// summation order could have decided the argmax, so the wave recomputes the
-// logits of every column of every tile whose maximum is that close, in the
-// CPU's order (the bias, then a fused multiply-add per input in order,
-// src/engine/layers.rs:770-776), and takes the first column of their
-// maximum. Columns of the other tiles lie more than kCtcTie below on the GPU,
-// further than the two orders ever differ.
-constexpr float kCtcTie = 1.0f / 1024.0f;
+// values lie within `tie` of each other, the GPU's summation order could
+// have decided the argmax, so the wave recomputes the logits of every column
+// of every tile whose maximum is that close, in the CPU's order (the bias,
+// then a fused multiply-add per input in order, src/engine/layers.rs:770-776),
+// and takes the first column of their maximum.
+//
+// `tie` bounds how far the two orders can put two columns' logits apart:
+// each order computes bias + sum of ci products with at most n = ci + 1
+// roundings, so each lies within n u T of the exact sum (u = 2^-24, T =
+// |bias| + sum |w_i x_i| <= bias_max + wsum_max * max |x_i|), the two orders
+// within 2 n u T of each other, and two columns' differences within 4 n u T.
+// The test takes twice that (8 n u T, which also covers an accumulation that
+// rounds toward zero), so columns further below the maximum on the GPU are
+// below it in the CPU's order too.
+constexpr float kCtcUnit = 1.0f / 16777216.0f;  // 2^-24
 
 
 __global__ __launch_bounds__(256) void ctc_merge(const float4 *part, int rows, int ntiles, float *y,
@@ -796,14 +803,19 @@ __global__ __launch_bounds__(256) void ctc_merge(const float4 *part, int rows, i
   // Every lane holds the row's joined values: the check is uniform.
   const int ln = row / rows_per_lane, tr = row - ln * rows_per_lane;
   float best = st.b;
-  const float tie = kCtcTie * fmaxf(1.0f, fabsf(st.m));
+  const float *x = ex.x + (long)ln * ex.x_lane_stride + (long)tr * ex.ci;
+  float xm = 0.0f;  // max |x_i| of the row, the same in every lane
+  for (int i = lane; i < ex.ci; i += 64) xm = fmaxf(xm, fabsf(x[i]));
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) xm = fmaxf(xm, __shfl_xor(xm, d, 64));
+  const float terms = ex.bias_max + ex.wsum_max * xm;
+  const float tie = fmaxf(8.0f * float(ex.ci + 1) * kCtcUnit * terms * 1.0001f, 1e-30f);
   if (ex.wt && st.m - m2 <= tie) {
     // The candidate tiles' logits again, each column's multiply-adds in
     // channel order from its bias: 64-column chunks of the candidate tiles,
     // four at a time so that each lane runs four independent chains. The
     // lane keeps the greatest logit (the lowest column among equal ones);
     // the wave joins the lanes once at the end, the same total order.
-    const float *x = ex.x + (long)ln * ex.x_lane_stride + (long)tr * ex.ci;
     float bm = -__builtin_inff(), bb = __builtin_inff();
     int c0s[4] = {0, 0, 0, 0}, c1s[4] = {0, 0, 0, 0}, nq = 0;
     auto run = [&]() {

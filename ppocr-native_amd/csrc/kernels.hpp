@@ -195,6 +195,9 @@ struct CtcExact {
   int tile_n;          // columns a partial record covers (a GEMM tile, or a run of tiles)
   const float *tmax;   // or per 64-column tile and row its maximum, tile t's row m at t * rows + m
   int tmax_n;          // tiles
+  // Bounds of a column's terms for the near-tie test: the largest |bias| and
+  // the largest sum of a column's |weights|.
+  float bias_max, wsum_max;
 };
 hipError_t launch_ctc_merge(const float *part, int rows, int ntiles, float *y, long y_lane_stride,
                             int rows_per_lane, const CtcExact &ex, hipStream_t s);

@@ -107,6 +107,7 @@ struct Step {
   int gemm_n = 0, chunks = 0, ctot = 0, cpt = 0;
   size_t wt_off = 0, wt_k = 0;
   size_t se_w1 = 0, se_w2 = 0;  // S_MEAN with an SE: the 1x1 weights, 16-byte aligned in the packed arena
+  float ctc_bias_max = 0, ctc_wsum_max = 0;  // S_CTC: the largest |bias| and sum of a column's |weights|
   size_t enc_w1 = 0, enc_w2 = 0, enc_w3 = 0;  // encoder steps: their 1x1 weights in enc_pack order
 };
 
@@ -919,6 +920,17 @@ bool Model::pack(std::string &err) {
         }
       }
     }
+    if (s.kind == S_CTC) {
+      double bm = 0, wm = 0;
+      for (int nn = 0; nn < N; nn++) {
+        double ws = 0;
+        for (size_t k = 0; k < op.ic; k++) ws += std::fabs(double(w[(size_t(nn) / 16) * op.ic * 16 + k * 16 + nn % 16]));
+        wm = std::max(wm, ws);
+        if (op.b1) bm = std::max(bm, std::fabs(double(weights[op.b0 + size_t(nn)])));
+      }
+      // Rounded up to the next float.
+      s.ctc_bias_max = std::nextafter(float(bm), INFINITY), s.ctc_wsum_max = std::nextafter(float(wm), INFINITY);
+    }
     if (s.kind == S_CTC && ctc_direct_supported(int(op.ic))) {
       // The same weights in MFMA operand order for ctc_direct (the rows above
       // serve ctc_merge's exact recomputation of near ties): for column block
@@ -1273,7 +1285,7 @@ void Model::build_launches(Batch &b) {
           b.launches.push_back({"ctc_gemm", s.op, [a, t](hipStream_t st) { return launch_conv(a, t, st); }});
         }
         const CtcExact ex{a.src[0].p, a.src[0].lane_stride, int(op.ic), a.wt, a.wt_k, a.bias, a.vocab, tile_n,
-                          tmax, tiles};
+                          tmax, tiles, s.ctc_bias_max, s.ctc_wsum_max};
         b.launches.push_back({"ctc_merge", s.op, [part, rows, ntn, Y, ys, T, ex](hipStream_t st) {
                                 return launch_ctc_merge(part, rows, ntn, Y, ys, T, ex, st);
                               }});
