@@ -577,7 +577,8 @@ hipError_t launch_stem_block(const StemArgs &a, hipStream_t s) {
 
 // Thread = one input pixel (iy, ix) of the first transposed convolution and
 // one of its four taps (ky, kx) (one tap a workgroup, so the weights a wave
-// reads are uniform: scalar operands from the scalar cache; the four taps of
+// reads are uniform: the first layer's from LDS as broadcasts, the second's
+// scalar operands from the scalar cache; the four taps of
 // a block of 256 pixels are workgroups i, i + 8, i + 16, i + 24, which run
 // on one XCD and so read those pixels once from memory into its L2). It forms
 // the OC1 values of intermediate pixel (2iy+ky, 2ix+kx) as the engine's
@@ -607,7 +608,16 @@ __global__ __launch_bounds__(256) void db_head_kernel(HeadArgs a) {
   const int blk = (int)blockIdx.x, tap = (blk >> 3) & 3, pb = (blk & 7) | ((blk >> 5) << 3);
   const int ky = tap >> 1, kx = tap & 1;
   const int n0 = (ky * 2 + kx) * OC1;  // the columns of tap (ky, kx)
-  cfloat *w1 = (cfloat *)a.w1 + n0, *w2 = (cfloat *)a.w2;
+  cfloat *w2 = (cfloat *)a.w2;
+  // The tap's first-layer weights [ic][OC1] in LDS, read as broadcasts: read
+  // from the scalar cache, each channel's weights were waited for just
+  // before its multiply-adds.
+  __shared__ __attribute__((aligned(16))) float w1[kHeadMaxIc * OC1];
+  for (int e = threadIdx.x; e < a.ic * OC1; e += 256) {
+    const int i = e / OC1;
+    w1[e] = a.w1[(long)i * COLS1 + n0 + (e - i * OC1)];
+  }
+  __syncthreads();
   const int per = a.ih * a.iw;
   const int g = pb * 256 + threadIdx.x;
   if (g >= a.lanes * per) return;
@@ -633,7 +643,7 @@ __global__ __launch_bounds__(256) void db_head_kernel(HeadArgs a) {
     const float xv[8] = {cur0.x, cur0.y, cur0.z, cur0.w, cur1.x, cur1.y, cur1.z, cur1.w};
 #pragma unroll
     for (int ii = 0; ii < 8; ii++) {
-      cfloat *wr = w1 + (long)(i0 + ii) * COLS1;
+      const float *wr = w1 + (i0 + ii) * OC1;
 #pragma unroll
       for (int n = 0; n < OC1; n++) t[n] = fmaf(wr[n], xv[ii], t[n]);
     }
