@@ -406,6 +406,63 @@ __global__ __launch_bounds__(256) void conv_mfma(ConvArgs a) {
   if constexpr (CTC) {
     ctc_rows<MT, NT>(acc, m0 + wave * WM, M, n0, a.bias, a.vocab, a.part, ntn, tn, lane);
     return;
+  } else if (MT == 1 && BN <= 32 && a.pw_w) {
+    // The folded 1x1: each wave's 16 pixels x BN activated outputs go to
+    // LDS (the operand stages are free) and return as the A operand of a
+    // 16 x 16 x 4 chain over those BN channels against the 1x1's weights,
+    // up to 32 output columns; bias and activation, then its store. The
+    // launch checks the conditions (one column tile, no residual).
+    constexpr int TP = BN + 4;
+    float *T = &As[0][0] + wave * 16 * TP;
+    const int K2 = a.n, N2 = a.pw_n;
+    float w2[BN / 4][2];
+#pragma unroll
+    for (int s4 = 0; s4 < BN / 4; s4++)
+#pragma unroll
+      for (int j2 = 0; j2 < 2; j2++) {
+        const int k = 4 * s4 + lg, c = j2 * 16 + li;
+        w2[s4][j2] = k < K2 && c < N2 ? a.pw_w[(long)k * N2 + c] : 0.0f;
+      }
+#pragma unroll
+    for (int j = 0; j < NT; j++) {
+      const int n = j * 16 + li;
+      const float bv = a.bias && n < a.n ? a.bias[n] : 0.0f;
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        float v = 0.0f;
+        if (n < a.n) {
+          v = acc[0][j][r];
+          if (a.bias) v = v + bv;
+          v = act(v, a.act);
+        }
+        T[(lg * 4 + r) * TP + n] = v;
+      }
+    }
+    __syncthreads();
+    f32x4 acc2[2];
+    acc2[0] = acc2[1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s4 = 0; s4 < BN / 4; s4++) {
+      const float x = T[li * TP + 4 * s4 + lg];
+#pragma unroll
+      for (int j2 = 0; j2 < 2; j2++) acc2[j2] = __builtin_amdgcn_mfma_f32_16x16x4f32(x, w2[s4][j2], acc2[j2], 0, 0, 0);
+    }
+#pragma unroll
+    for (int j2 = 0; j2 < 2; j2++) {
+      const int c = j2 * 16 + li;
+      if (c >= N2) continue;
+      const float b2 = a.pw_b ? a.pw_b[c] : 0.0f;
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const int m = m0 + wave * WM + lg * 4 + r;
+        if (m >= M) continue;
+        const int ln = m / per_lane, rem = m - ln * per_lane;
+        float v = acc2[j2][r];
+        if (a.pw_b) v = v + b2;
+        a.y[(long)ln * a.y_lane_stride + (long)rem * N2 + c] = act(v, a.pw_act);
+      }
+    }
+    return;
   } else {
 #pragma unroll
     for (int i = 0; i < MT; i++) {
@@ -1506,6 +1563,14 @@ static hipError_t go(const ConvArgs &a, hipStream_t s) {
   if (t.bk == 16) { PPOCR_TILES(16, LAY) }              \
   if (t.bk == 8) { PPOCR_TILES(8, LAY) }
 
+bool conv_pw_supported(const ConvArgs &a, const GemmTile &t) {
+  // One tile's columns are every output column (a 16 x 16 x 4 chain over
+  // them), 16-row MFMA blocks a wave, the LDS stages large enough to hold
+  // four waves' 16 x (BN + 4) floats, no residual.
+  return a.mode == GEMM_STORE && !a.res && t.wm == 16 && (t.bn == 16 || t.bn == 32) && a.n <= t.bn && t.bk >= 16 &&
+         a.pw_n >= 1 && a.pw_n <= 32;
+}
+
 bool gemm_tile_supported(const GemmTile &t) {
   if (t.bk == 64) return t.vec && t.wm == 16 && (t.bn == 16 || t.bn == 32 || t.bn == 64);
   // One chunk per tap of 48 or 96 channels: windowed, 64-row tiles.
@@ -1518,6 +1583,7 @@ bool gemm_tile_supported(const GemmTile &t) {
 }
 
 hipError_t launch_conv(const ConvArgs &a, const GemmTile &t, hipStream_t s) {
+  if (a.pw_w && !conv_pw_supported(a, t)) return hipErrorInvalidValue;
   if (a.mode == GEMM_CTC) {
     if (!t.pointwise || !t.vec || t.bn != 64) return hipErrorInvalidValue;
     if (t.wm == 32 && t.bk == 8) return go<32, 64, 8, L_POINTWISE, true>(a, s);

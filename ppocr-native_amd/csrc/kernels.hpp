@@ -144,6 +144,12 @@ struct ConvArgs {
   float *part;          // GEMM_CTC: per row and column tile (max, sum, best)
   int vocab;
   int xcd_rows;         // 1: give each XCD a contiguous run of tiles (see xcd_tile)
+  // A 1x1 convolution of this one's output folded into the epilogue (its
+  // weights [n][pw_n] as the plan stores them, bias, activation): the tile's
+  // activated outputs are its input and only its output is stored, pw_n
+  // columns a pixel. Null pw_w: none.
+  const float *pw_w, *pw_b;
+  int pw_n, pw_act;
 };
 
 struct GemmTile {
@@ -155,6 +161,8 @@ struct GemmTile {
 // Tiles launch_conv has compiled: BK 8, 16, 32 with WM 32 (BN 16, 32, 64) or
 // WM 16 (BN 64); BK 64 (channel layout) with WM 16 and BN 16, 32, 64.
 bool gemm_tile_supported(const GemmTile &t);
+// Whether launch_conv takes a.pw_w (a folded 1x1) on tile t.
+bool conv_pw_supported(const ConvArgs &a, const GemmTile &t);
 hipError_t launch_conv(const ConvArgs &a, const GemmTile &t, hipStream_t s);
 // The 1x1 convolution (GEMM_STORE or GEMM_SPREAD, one source of ctot
 // channels, a multiple of 4) with its operand chunks in an LDS ring fed by

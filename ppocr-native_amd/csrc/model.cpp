@@ -84,6 +84,9 @@ struct Step {
   int gate = -1;     // Channelmul folded into a convolution's first input
   int add = -1;      // Add folded into a convolution's output / of a residual gate
   int resgate = -1;  // Channelmul of a residual gate, x + x * g
+  // S_GEMM: a 1x1 convolution of this step's output folded into its
+  // epilogue (the step then writes that 1x1's output), or -1.
+  int pw1 = -1;
   int fc1 = -1, fc2 = -1;  // squeeze-and-excite 1x1 layers after a Mean; an encoder step's 1x1 layers
   int ln_out = -1;         // S_ENC_MLP, S_ENC_BLOCK: the LayerNorm of its sum, written in its place
   int m_ln = -1, m_fc1 = -1, m_fc2 = -1, m_add = -1;  // S_ENC_BLOCK: its MLP's operations
@@ -305,6 +308,7 @@ std::vector<size_t> Model::step_reads(const Step &s) const {
 
 size_t Model::step_writes(const Step &s) const {
   if (s.kind == S_HEAD) return plan.ops[s.head2].y;
+  if (s.pw1 >= 0) return plan.ops[s.pw1].y;
   if (s.kind == S_STEM) return s.st_joint ? plan.ops[s.st_pool].y : plan.ops[s.st3].y;
   if (s.kind == S_MEAN && s.fc2 >= 0) return plan.ops[s.fc2].y;
   if ((s.kind == S_ENC_MLP || s.kind == S_ENC_BLOCK) && s.ln_out >= 0) return plan.ops[s.ln_out].y;
@@ -328,6 +332,9 @@ size_t Model::step_writes(const Step &s) const {
 //    535-605).
 //  - An Add that is the only reader of a convolution's output: the
 //    convolution's epilogue (gpu/mod.rs:522-526).
+//  - A 1x1 convolution that is the only reader of the implicit-GEMM
+//    convolution just before it: that convolution's epilogue (decided in
+//    pack, once the convolution's tile is known).
 // The depthwise launch shape of an operation (pointers unset).
 static DwArgs dw_shape(const Op &op) {
   DwArgs a{};
@@ -954,6 +961,36 @@ bool Model::pack(std::string &err) {
   HIPTRY(hipMalloc(&dpacked, packed.size() * sizeof(float)), "allocating packed weights");
   HIPTRY(hipMemcpy(dpacked, packed.data(), packed.size() * sizeof(float), hipMemcpyHostToDevice),
          "uploading packed weights");
+  // A 1x1 convolution whose input only the implicit-GEMM convolution just
+  // before it writes and nothing else reads: folded into that convolution's
+  // epilogue, whose tile holds every output column of its pixels (16-row
+  // MFMA blocks a wave); the 1x1's map is then the only one stored.
+  {
+    const auto &ops = plan.ops;
+    std::vector<size_t> readers(plan.pool.size(), 0);
+    for (const Op &o : ops) {
+      readers[o.x]++;
+      size_t x2;
+      if (o.has_second(&x2)) readers[x2]++;
+    }
+    for (size_t sl : plan.out_slot) readers[sl]++;
+    for (size_t k = 0; k + 1 < steps.size(); k++) {
+      Step &g = steps[k];
+      const Step &c = steps[k + 1];
+      const Op &go = ops[size_t(g.op)], &co = ops[size_t(c.op)];
+      if (g.kind != S_GEMM || c.kind != S_GEMM || g.patch || g.ring || g.add >= 0 || g.pw1 >= 0) continue;
+      if (go.kind != K_CONV || co.kind != K_CONV || !co.is_pointwise() || co.n2 || co.x != go.y) continue;
+      if (readers[go.y] != 1 || c.gate >= 0 || c.add >= 0 || c.sources.size() != 1 || c.sources[0].shift) continue;
+      GemmTile t = g.tile;
+      t.wm = 16;
+      ConvArgs probe{};
+      probe.mode = GEMM_STORE, probe.n = g.gemm_n, probe.pw_n = int(co.oc);
+      if (!gemm_tile_supported(t) || !conv_pw_supported(probe, t)) continue;
+      g.tile = t;
+      g.pw1 = c.op;
+      steps.erase(steps.begin() + long(k) + 1);
+    }
+  }
   return true;
 }
 
@@ -1216,6 +1253,11 @@ void Model::build_launches(Batch &b) {
           a.act2 = ad.fused;
         }
         a.y = Y, a.y_lane_stride = ys;
+        if (s.pw1 >= 0) {
+          const Op &q = p.ops[s.pw1];
+          a.pw_w = W + q.w0, a.pw_b = q.b1 ? W + q.b0 : nullptr;
+          a.pw_n = int(q.oc), a.pw_act = q.fused;
+        }
         GemmTile t = s.tile;
         if (s.patch) {
           // Tiles of 8 rows (each wave two MFMA row blocks: half the LDS reads
@@ -1248,6 +1290,7 @@ void Model::build_launches(Batch &b) {
         if (tiles < 1024) t.wm = 16;
         const char *nm = op.kind == K_CONVTRANSPOSE ? "convt_gemm" : (t.pointwise ? "pointwise_gemm" : "conv_gemm");
         b.launches.push_back({nm, s.op, [a, t](hipStream_t st) { return launch_conv(a, t, st); }});
+        if (s.pw1 >= 0) b.launches.back().member_ops = {s.op, s.pw1};
         break;
       }
       case S_CTC: {
@@ -1793,6 +1836,13 @@ void Model::account(Batch &b) const {
         }
         l.flops = 2.0 * M * N * K;
         l.bytes = F * (in + M * N + K * N + (op.b1 ? N : 0));
+        if (s.pw1 >= 0) {
+          // The folded 1x1: its product, its weights, and its map stored in
+          // place of this layer's.
+          const Op &q = p.ops[size_t(s.pw1)];
+          l.flops += 2.0 * M * double(q.oc) * N;
+          l.bytes = F * (in + M * double(q.oc) + K * N + (op.b1 ? N : 0) + N * double(q.oc) + (q.b1 ? q.oc : 0));
+        }
         break;
       }
       case S_CTC: {

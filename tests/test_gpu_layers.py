@@ -119,6 +119,33 @@ def test_ring_windowed(oracle, k, s, pad, ci, co, hw, lanes, two):
     near(got, want)
 
 
+@pytest.mark.parametrize("ci,co,co2,hw,lanes", [
+    (16, 24, 20, (260, 262), 1),   # the detector stem's shape: a 3 x 3 stride-2 conv, then its 1 x 1
+    (16, 32, 32, (258, 256), 2),
+    (16, 12, 7, (262, 258), 1),    # columns past the tile's and the 1 x 1's last
+])
+def test_conv_then_pointwise_folded(oracle, ci, co, co2, hw, lanes):
+    # A 1 x 1 convolution whose input only the implicit-GEMM convolution
+    # before it writes: one launch, the 1 x 1 in its epilogue on the tile's
+    # activated outputs, only the 1 x 1's map stored.
+    w = RNG.normal(0, 1 / np.sqrt(9 * ci), (3, 3, ci, co)).astype(np.float32)
+    bias = RNG.normal(0, 0.3, co).astype(np.float32)
+    w2 = RNG.normal(0, 1 / np.sqrt(co), (1, 1, co, co2)).astype(np.float32)
+    b2 = RNG.normal(0, 0.3, co2).astype(np.float32)
+
+    def build(b, t):
+        y = b.conv(t, w, bias, k=(3, 3), s=(2, 2), pad=(1, 1, 1, 1), fused="hardswish")
+        return b.conv(y, w2, b2, fused="hardswish")
+
+    b = PlanBuilder(*hw, ci)
+    g = GpuModel.load(b.to_bytes([build(b, b.input)]))
+    launches, ops = g.launches(), g.launch_ops()
+    g.close()
+    assert [n for n, _ in launches] == ["conv_gemm"] and ops == [[0, 1]], (launches, ops)
+    got, want = both(build, (*hw, ci), oracle, lanes=lanes)
+    near(got, want)
+
+
 def test_ring_upsampled_sources(oracle):
     # A 5 x 5 convolution (on the LDS ring) over a map upsampled by 2 stacked
     # with a full-size one: the direct loads read the small map at (y/2, x/2).
