@@ -256,6 +256,22 @@ hipError_t launch_dwconv(const DwArgs &a, hipStream_t s);
 bool dw_mean_supported(const DwArgs &a);
 int dw_mean_blocks(const DwArgs &a);
 
+// A depthwise layer and the 1x1 convolution that alone reads its output, in
+// one launch (the depthwise map never stored). d.y is unused.
+struct DwPwArgs {
+  DwArgs d;
+  const float *pw;    // the 1x1's weights packed by enc_pack with kp = d.c
+  const float *pw_b;  // its bias or null
+  int n, pw_act;      // its output channels and activation
+  const float *res;   // added after the activation, or null
+  long res_lane_stride;
+  int act2;           // applied after the residual
+  float *y;
+  long y_lane_stride;
+};
+bool dwpw_supported(const DwArgs &d, int n, bool res);
+hipError_t launch_dwpw(const DwPwArgs &a, hipStream_t s);
+
 // ---------------------------------------------------------------- elementwise
 
 enum EltMode : int {

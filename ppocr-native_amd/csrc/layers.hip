@@ -436,6 +436,307 @@ static hipError_t launch_dw_tile(const DwArgs &a, const DwTile &t, hipStream_t s
   return t.cg == 8 ? go_dw_tile<8, false>(a, t, s) : go_dw_tile<4, false>(a, t, s);
 }
 
+// ------------------------------------------- depthwise, then a 1x1, on tiles
+
+// A depthwise layer and the 1x1 convolution that alone reads its output, in
+// one launch. A workgroup takes a tile of TR x TW output pixels of one lane
+// (at most P = 16 * RB: the MFMA rows) and every channel. The tile's input
+// window (zero outside the image), the depthwise taps and bias, and the
+// residual rows go into LDS by direct loads, all in flight together with
+// the 1x1's weights (from the MFMA operand packing straight into B
+// registers) and its bias. Each thread then computes depthwise outputs
+// (pixel, channel quad) from LDS in dwconv_fixed's arithmetic (from the
+// bias, taps row by row, one fused multiply-add each, taps outside the image
+// skipped) into rows of c + 4 floats, and wave w multiplies every row block
+// by column blocks w, w + 4, ... on v_mfma_f32_16x16x4_f32 (input group q of
+// 16 channels, lane group g supplying channels 16q + 4g + e to step e). The
+// products (plus the bias) go back to LDS over the spent window, and every
+// thread finishes float4s of output rows: activation, residual, second
+// activation, one coalesced store. Loops over pixels run rolled, so each
+// activation is compiled once.
+constexpr int kDwPwKq = 8;  // channel groups of 16 a workgroup holds: c <= 128
+
+struct DwPwLds {
+  int x, a, r, total;  // float offsets of the window / products, the depthwise rows, the residual
+};
+
+__host__ __device__ inline DwPwLds dwpw_lds(const DwArgs &d, int n, int tr, int tw, int p, bool res) {
+  DwPwLds l;
+  l.x = ((d.kh * d.kw + 1) * (d.c / 4) + 63) / 64 * 256;  // taps and bias, whole loads
+  const int win = (dw_tile_rows(d, tr) * dw_tile_cols(d, tw) * (d.c / 4) + 63) / 64 * 256;
+  const int prod = p * ((n + 15) / 16 * 16 + 4);
+  l.a = l.x + (std::max(win, prod) + 63) / 64 * 64;
+  l.r = l.a + (p * (d.c + 4) + 63) / 64 * 64;
+  l.total = l.r + (res ? (p * (n / 4) + 63) / 64 * 256 : 0);
+  return l;
+}
+
+// An activation of four values, dispatched once for the four (the common
+// codes fold to their own few instructions).
+__device__ __forceinline__ f32x4 act4(f32x4 v, int a) {
+  switch (a) {
+    case ACT_NONE: return v;
+    case ACT_RELU: return f32x4{act(v.x, ACT_RELU), act(v.y, ACT_RELU), act(v.z, ACT_RELU), act(v.w, ACT_RELU)};
+    case ACT_HARDSWISH:
+      return f32x4{act(v.x, ACT_HARDSWISH), act(v.y, ACT_HARDSWISH), act(v.z, ACT_HARDSWISH), act(v.w, ACT_HARDSWISH)};
+    default: return f32x4{act(v.x, a), act(v.y, a), act(v.z, a), act(v.w, a)};
+  }
+}
+
+// The 1x1's products over KQ groups of 16 channels: wave-uniform, every
+// column block of the wave (blocks past the last are computed and dropped),
+// no branch inside the chain.
+template <int KQ, int RB, int NBW>
+__device__ __forceinline__ void dwpw_mfma(f32x4 (&acc)[RB][NBW], const float *A, int AS,
+                                          const f32x4 (&bw)[NBW][kDwPwKq], int li, int lg) {
+#pragma unroll
+  for (int q = 0; q < KQ; q++) {
+    f32x4 af[RB];
+#pragma unroll
+    for (int rb = 0; rb < RB; rb++) af[rb] = *reinterpret_cast<const f32x4 *>(A + (16 * rb + li) * AS + 16 * q + 4 * lg);
+#pragma unroll
+    for (int e = 0; e < 4; e++)
+#pragma unroll
+      for (int jj = 0; jj < NBW; jj++)
+#pragma unroll
+        for (int rb = 0; rb < RB; rb++)
+          acc[rb][jj] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[rb][e], bw[jj][q][e], acc[rb][jj], 0, 0, 0);
+  }
+}
+
+template <int K, int S, int RB, int NBW>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void dwpw_tile(DwPwArgs a, DwTile tt) {
+  constexpr int P = 16 * RB;
+  extern __shared__ __attribute__((aligned(16))) float lds[];
+  const DwArgs &d = a.d;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int li = lane & 15, lg = lane >> 4;
+  const int C = d.c, C4 = C / 4, KQ = C / 16, N = a.n, N4 = N / 4, NB = (N + 15) / 16;
+  const int AS = C + 4, ON = NB * 16 + 4;
+  // Tiles numbered XCD by XCD: neighbours, which share halo rows, meet in one L2.
+  int b = xcd_tile((int)blockIdx.x, (int)gridDim.x);
+  const int tx = b % tt.tiles_x;
+  b /= tt.tiles_x;
+  const int ty = b % tt.tiles_y, ln = b / tt.tiles_y;
+  const int oy0 = ty * tt.tr, ox0 = tx * tt.tw;
+  const int IC = dw_tile_cols(d, tt.tw);
+  const int iy0 = oy0 * d.sh - d.pt, ix0 = ox0 * S - d.pl;
+  const int wq = (K * K + 1) * C4, win = dw_tile_rows(d, tt.tr) * IC * C4;
+  const DwPwLds L = dwpw_lds(d, N, tt.tr, tt.tw, P, a.res != nullptr);
+  float *W = lds;          // taps [K * K][C], then the bias [C]
+  float *X = lds + L.x;    // the window; later the products, rows of ON
+  float *A = lds + L.a;    // the depthwise rows, AS apart
+  float *R = lds + L.r;    // the residual rows, N apart
+  // Output pixel p of the tile: its place in the lane's map, or -1 past the
+  // tile or the map.
+  auto out_at = [&](int p) {
+    const int r = p / tt.tw, col = p - r * tt.tw;
+    const int oy = oy0 + r, ox = ox0 + col;
+    return r < tt.tr && oy < d.oh && ox < d.ow ? oy * d.ow + ox : -1;
+  };
+  const float *xl = d.x + (long)ln * d.x_lane_stride;
+  for (int q = wave; q * 64 < wq; q += 4) {
+    const int u = q * 64 + lane;
+    const int tap = u / C4, g = u - tap * C4;
+    const float *p = u >= wq ? kDwZeros
+                     : tap < K * K ? d.w + (long)tap * C + 4 * g
+                                   : (d.bias ? d.bias + 4 * g : kDwZeros);
+    __builtin_amdgcn_global_load_lds((const void *)p, (lds_void *)(W + q * 256), 16, 0, 0);
+  }
+  for (int q = wave; q * 64 < win; q += 4) {
+    const int u = q * 64 + lane;
+    const int pix = u / C4, g = u - pix * C4;
+    const int r = pix / IC, col = pix - r * IC;
+    const int iy = iy0 + r, ix = ix0 + col;
+    const float *p = u < win && iy >= 0 && iy < d.ih && ix >= 0 && ix < d.iw
+                         ? xl + ((long)iy * d.iw + ix) * C + 4 * g
+                         : kDwZeros;
+    __builtin_amdgcn_global_load_lds((const void *)p, (lds_void *)(X + q * 256), 16, 0, 0);
+  }
+  if (a.res) {
+    const float *rl = a.res + (long)ln * a.res_lane_stride;
+    for (int q = wave; q * 64 < P * N4; q += 4) {
+      const int u = q * 64 + lane, p = u / N4, c4 = u - p * N4;
+      const int at = u < P * N4 ? out_at(p) : -1;
+      const float *src = at >= 0 ? rl + (long)at * N + 4 * c4 : kDwZeros;
+      __builtin_amdgcn_global_load_lds((const void *)src, (lds_void *)(R + q * 256), 16, 0, 0);
+    }
+  }
+  // The 1x1's B operands and bias, in flight beside the window. Every load
+  // is unconditional (indices clamped; the operands past the last column
+  // block or channel group are never used), so that none waits at a branch.
+  const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+  f32x4 bw[NBW][kDwPwKq];
+  float pb[NBW];
+  const float *bsrc = a.pw_b ? a.pw_b : a.pw;
+#pragma unroll
+  for (int jj = 0; jj < NBW; jj++) {
+    const int j = min(wave + 4 * jj, NB - 1);
+    const f32x4 *src = reinterpret_cast<const f32x4 *>(a.pw) + (long)j * KQ * 64 + lane;
+#pragma unroll
+    for (int q = 0; q < kDwPwKq; q++) bw[jj][q] = src[min(q, KQ - 1) * 64];
+    pb[jj] = bsrc[min(16 * j + li, N - 1)];
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+
+  // Thread t takes channel quad g = t % C4 of pixels t / C4, t / C4 + slots,
+  // ... (slots = 256 / C4; threads past slots * C4 rest), so that a 3 x 3
+  // window's taps and the bias stay in its registers.
+  const int slots = 256 / C4, g = tid % C4, p0 = tid / C4;
+  constexpr int KR = K <= 3 ? K * K : 1;
+  f32x4 wk[KR];
+  const f32x4 bias4 = *reinterpret_cast<const f32x4 *>(W + K * K * C + 4 * g);
+  if constexpr (K <= 3) {
+#pragma unroll
+    for (int k = 0; k < KR; k++) wk[k] = *reinterpret_cast<const f32x4 *>(W + k * C + 4 * g);
+  }
+#pragma unroll 1
+  for (int p = p0; p0 < slots && p < P; p += slots) {
+    f32x4 v = zero;
+    if (out_at(p) >= 0) {
+      const int r = p / tt.tw, col = p - r * tt.tw;
+      const int ry = r * d.sh, cx = col * S;
+      f32x4 acc = bias4;
+      // Every tap's operands are read (the window holds zeros outside the
+      // image); a tap outside the image leaves the sum as it is, by select,
+      // so that the reads issue together and no lane branches.
+      auto row = [&](int ky) {
+        const int iy = iy0 + ry + ky;
+        const bool in_y = iy >= 0 && iy < d.ih;
+        const float *xr = X + ((ry + ky) * IC + cx) * C + 4 * g;
+#pragma unroll
+        for (int kx = 0; kx < K; kx++) {
+          const int ix = ix0 + cx + kx;
+          const bool in = in_y && ix >= 0 && ix < d.iw;
+          f32x4 wv;
+          if constexpr (K <= 3) wv = wk[ky * K + kx];
+          else wv = *reinterpret_cast<const f32x4 *>(W + (ky * K + kx) * C + 4 * g);
+          const f32x4 xv = *reinterpret_cast<const f32x4 *>(xr + kx * C);
+          const f32x4 t = {fmaf(wv.x, xv.x, acc.x), fmaf(wv.y, xv.y, acc.y), fmaf(wv.z, xv.z, acc.z),
+                           fmaf(wv.w, xv.w, acc.w)};
+          acc = in ? t : acc;
+        }
+      };
+      // A 3 x 3 window's rows unrolled; wider windows row by row, their taps
+      // from LDS (all their operands at once would take more registers than
+      // two waves a SIMD have).
+      if constexpr (K <= 3) {
+#pragma unroll
+        for (int ky = 0; ky < K; ky++) row(ky);
+      } else {
+#pragma unroll 1
+        for (int ky = 0; ky < K; ky++) row(ky);
+      }
+      v = act4(acc, d.act);
+    }
+    *reinterpret_cast<f32x4 *>(A + p * AS + 4 * g) = v;
+  }
+  __syncthreads();  // the depthwise rows are whole; the window is spent
+
+  f32x4 acc[RB][NBW];
+#pragma unroll
+  for (int rb = 0; rb < RB; rb++)
+#pragma unroll
+    for (int jj = 0; jj < NBW; jj++) acc[rb][jj] = zero;
+  switch (KQ) {
+    case 1: dwpw_mfma<1>(acc, A, AS, bw, li, lg); break;
+    case 2: dwpw_mfma<2>(acc, A, AS, bw, li, lg); break;
+    case 3: dwpw_mfma<3>(acc, A, AS, bw, li, lg); break;
+    case 4: dwpw_mfma<4>(acc, A, AS, bw, li, lg); break;
+    case 5: dwpw_mfma<5>(acc, A, AS, bw, li, lg); break;
+    case 6: dwpw_mfma<6>(acc, A, AS, bw, li, lg); break;
+    case 7: dwpw_mfma<7>(acc, A, AS, bw, li, lg); break;
+    default: dwpw_mfma<8>(acc, A, AS, bw, li, lg); break;
+  }
+#pragma unroll
+  for (int jj = 0; jj < NBW; jj++) {
+    const int j = wave + 4 * jj;
+    if (j >= NB) continue;
+#pragma unroll
+    for (int rb = 0; rb < RB; rb++)
+#pragma unroll
+      for (int r = 0; r < 4; r++)
+        X[(16 * rb + 4 * lg + r) * ON + 16 * j + li] = a.pw_b ? acc[rb][jj][r] + pb[jj] : acc[rb][jj][r];
+  }
+  __syncthreads();
+  float *yl = a.y + (long)ln * a.y_lane_stride;
+#pragma unroll 1
+  for (int u = tid; u < P * N4; u += 256) {
+    const int p = u / N4, c4 = u - p * N4;
+    const int at = out_at(p);
+    if (at < 0) continue;
+    f32x4 v = act4(*reinterpret_cast<const f32x4 *>(X + p * ON + 4 * c4), a.pw_act);
+    if (a.res) v = act4(v + *reinterpret_cast<const f32x4 *>(R + p * N + 4 * c4), a.act2);
+    *reinterpret_cast<f32x4 *>(yl + (long)at * N + 4 * c4) = v;
+  }
+}
+
+static bool dwpw_shape_ok(const DwArgs &d, int n) {
+  return d.kh == d.kw && (d.kh == 3 || d.kh == 5) && (d.sw == 1 || d.sw == 2) && (d.sh == 1 || d.sh == 2) &&
+         d.c % 16 == 0 && d.c >= 16 && d.c <= 16 * kDwPwKq && n >= 4 && n <= 192 && n % 4 == 0 &&
+         d.lanes >= 1 && d.oh >= 1 && d.ow >= 1;
+}
+
+// The tile of a fused layer: P = 64, 32 or 16 pixels as 8 x 8, 4 x 8 or
+// 4 x 4 (narrower maps take whole rows), the largest whose LDS stays within
+// 64 KiB (two workgroups a CU or more) and that still gives 256 tiles or
+// more; rb = 0 when the fused kernel does not take the layer.
+static DwTile dwpw_tile_of(const DwArgs &d, int n, bool res, int &rb) {
+  DwTile t{};
+  rb = 0;
+  if (!dwpw_shape_ok(d, n)) return t;
+  for (int p : {64, 32, 16}) {
+    int tw = p == 16 ? 4 : 8, tr = p / tw;
+    if (d.ow < tw) tw = d.ow, tr = p / tw;
+    if (d.oh < tr) tr = d.oh, tw = std::min(d.ow, p / tr);
+    const long tiles = long(d.lanes) * ((d.oh + tr - 1) / tr) * ((d.ow + tw - 1) / tw);
+    if (size_t(dwpw_lds(d, n, tr, tw, p, res).total) * 4 > 64 * 1024) continue;
+    t = DwTile{0, tr, tw, (d.ow + tw - 1) / tw, (d.oh + tr - 1) / tr};
+    rb = p / 16;
+    if (tiles >= 256) break;
+  }
+  return t;
+}
+
+bool dwpw_supported(const DwArgs &d, int n, bool res) {
+  int rb;
+  dwpw_tile_of(d, n, res, rb);
+  return rb > 0;
+}
+
+template <int K, int S, int RB>
+static hipError_t go_dwpw(const DwPwArgs &a, const DwTile &t, size_t lds, dim3 grid, hipStream_t s) {
+  const int nbw = ((a.n + 15) / 16 + 3) / 4;
+  switch (nbw) {
+    case 1: hipLaunchKernelGGL((dwpw_tile<K, S, RB, 1>), grid, dim3(256), lds, s, a, t); break;
+    case 2: hipLaunchKernelGGL((dwpw_tile<K, S, RB, 2>), grid, dim3(256), lds, s, a, t); break;
+    case 3: hipLaunchKernelGGL((dwpw_tile<K, S, RB, 3>), grid, dim3(256), lds, s, a, t); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_dwpw(const DwPwArgs &a, hipStream_t s) {
+  const DwArgs &d = a.d;
+  int rb;
+  const DwTile t = dwpw_tile_of(d, a.n, a.res != nullptr, rb);
+  if (!rb || !a.pw || !a.y) return hipErrorInvalidValue;
+  const long blocks = long(d.lanes) * t.tiles_y * t.tiles_x;
+  if (blocks < 1 || blocks > 0x7fffffffL) return hipErrorInvalidValue;
+  const size_t lds = size_t(dwpw_lds(d, a.n, t.tr, t.tw, 16 * rb, a.res != nullptr).total) * 4;
+  const dim3 grid((unsigned)blocks);
+  const int kind = d.kh * 100 + d.sw * 10 + rb;
+#define PPOCR_DWPW(KK, SS, RR) \
+  if (kind == KK * 100 + SS * 10 + RR) return go_dwpw<KK, SS, RR>(a, t, lds, grid, s);
+  PPOCR_DWPW(3, 1, 4) PPOCR_DWPW(3, 1, 2) PPOCR_DWPW(3, 1, 1)
+  PPOCR_DWPW(3, 2, 4) PPOCR_DWPW(3, 2, 2) PPOCR_DWPW(3, 2, 1)
+  PPOCR_DWPW(5, 1, 4) PPOCR_DWPW(5, 1, 2) PPOCR_DWPW(5, 1, 1)
+  PPOCR_DWPW(5, 2, 4) PPOCR_DWPW(5, 2, 2) PPOCR_DWPW(5, 2, 1)
+#undef PPOCR_DWPW
+  return hipErrorInvalidValue;
+}
+
 bool dw_mean_supported(const DwArgs &a) { return a.c % 4 == 0 && a.c <= 1024 && dw_fixed_kind(a) != 0; }
 
 int dw_mean_blocks(const DwArgs &a) {

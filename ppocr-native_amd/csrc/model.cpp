@@ -84,8 +84,9 @@ struct Step {
   int gate = -1;     // Channelmul folded into a convolution's first input
   int add = -1;      // Add folded into a convolution's output / of a residual gate
   int resgate = -1;  // Channelmul of a residual gate, x + x * g
-  // S_GEMM: a 1x1 convolution of this step's output folded into its
-  // epilogue (the step then writes that 1x1's output), or -1.
+  // S_GEMM, S_DW: a 1x1 convolution of this step's output folded into it
+  // (the step then writes that 1x1's output, or on S_DW the sum of its
+  // folded Add), or -1.
   int pw1 = -1;
   int fc1 = -1, fc2 = -1;  // squeeze-and-excite 1x1 layers after a Mean; an encoder step's 1x1 layers
   int ln_out = -1;         // S_ENC_MLP, S_ENC_BLOCK: the LayerNorm of its sum, written in its place
@@ -287,6 +288,13 @@ std::vector<size_t> Model::step_reads(const Step &s) const {
         if (op.has_second(&x2)) r.push_back(x2);
       }
       break;
+    case S_DW:
+      r.push_back(op.x);
+      if (s.add >= 0) {  // the residual of its folded 1x1
+        const Op &a = plan.ops[s.add];
+        r.push_back(a.x == plan.ops[s.pw1].y ? a.x2 : a.x);
+      }
+      break;
     case S_ENC_LIN:
     case S_ENC_ATTN:
     case S_ENC_MLP:
@@ -308,7 +316,7 @@ std::vector<size_t> Model::step_reads(const Step &s) const {
 
 size_t Model::step_writes(const Step &s) const {
   if (s.kind == S_HEAD) return plan.ops[s.head2].y;
-  if (s.pw1 >= 0) return plan.ops[s.pw1].y;
+  if (s.pw1 >= 0) return s.add >= 0 ? plan.ops[s.add].y : plan.ops[s.pw1].y;
   if (s.kind == S_STEM) return s.st_joint ? plan.ops[s.st_pool].y : plan.ops[s.st3].y;
   if (s.kind == S_MEAN && s.fc2 >= 0) return plan.ops[s.fc2].y;
   if ((s.kind == S_ENC_MLP || s.kind == S_ENC_BLOCK) && s.ln_out >= 0) return plan.ops[s.ln_out].y;
@@ -335,6 +343,9 @@ size_t Model::step_writes(const Step &s) const {
 //  - A 1x1 convolution that is the only reader of the implicit-GEMM
 //    convolution just before it: that convolution's epilogue (decided in
 //    pack, once the convolution's tile is known).
+//  - A 1x1 convolution (with its folded Add) that is the only reader of the
+//    depthwise layer just before it, when that layer sums nothing for a
+//    mean: one launch of both (dwpw_tile), the depthwise map never stored.
 // The depthwise launch shape of an operation (pointers unset).
 static DwArgs dw_shape(const Op &op) {
   DwArgs a{};
@@ -957,6 +968,34 @@ bool Model::pack(std::string &err) {
             }
     }
   }
+  // Depthwise layers and the 1x1 convolution that alone reads each: one
+  // step, the 1x1's weights packed in MFMA operand order over its c inputs.
+  {
+    const auto &ops = plan.ops;
+    std::vector<size_t> readers(plan.pool.size(), 0);
+    for (const Op &o : ops) {
+      readers[o.x]++;
+      size_t x2;
+      if (o.has_second(&x2)) readers[x2]++;
+    }
+    for (size_t sl : plan.out_slot) readers[sl]++;
+    for (size_t k = 0; k + 1 < steps.size(); k++) {
+      Step &d = steps[k];
+      const Step &c = steps[k + 1];
+      const Op &dop = ops[size_t(d.op)], &co = ops[size_t(c.op)];
+      if (d.kind != S_DW || d.dw_sums || d.pw1 >= 0 || c.kind != S_GEMM || c.patch || c.ring || c.pw1 >= 0) continue;
+      if (co.kind != K_CONV || !co.is_pointwise() || co.n2 || co.x != dop.y || readers[dop.y] != 1) continue;
+      if (c.gate >= 0 || c.sources.size() != 1 || c.sources[0].shift || !dwpw_supported(dw_shape(dop), int(co.oc), c.add >= 0))
+        continue;
+      const int ci = int(dop.oc), n = int(co.oc);
+      d.enc_w1 = round_up(packed.size(), 64);
+      packed.resize(d.enc_w1 + enc_pack_floats(ci, n), 0.0f);
+      enc_pack(weights.data() + co.w0, ci, n, ci, packed.data() + d.enc_w1);
+      d.pw1 = c.op;
+      d.add = c.add;
+      steps.erase(steps.begin() + long(k) + 1);
+    }
+  }
   if (packed.empty()) return true;
   HIPTRY(hipMalloc(&dpacked, packed.size() * sizeof(float)), "allocating packed weights");
   HIPTRY(hipMemcpy(dpacked, packed.data(), packed.size() * sizeof(float), hipMemcpyHostToDevice),
@@ -1338,6 +1377,24 @@ void Model::build_launches(Batch &b) {
         DwArgs a{L, int(op.ih), int(op.iw), int(op.oc), int(op.oh), int(op.ow), int(op.kh), int(op.kw),
                  int(op.sh), int(op.sw), int(op.pt), int(op.pl), b.dev(op.x), b.stride(op.x), W + op.w0,
                  bias, op.fused, Y, ys, nullptr};
+        if (s.pw1 >= 0) {
+          const Op &q = p.ops[s.pw1];
+          DwPwArgs f{};
+          f.d = a;
+          f.d.y = nullptr;
+          f.pw = dpacked + s.enc_w1, f.pw_b = q.b1 ? W + q.b0 : nullptr;
+          f.n = int(q.oc), f.pw_act = q.fused;
+          if (s.add >= 0) {
+            const Op &ad = p.ops[s.add];
+            const size_t r = ad.x == q.y ? ad.x2 : ad.x;
+            f.res = b.dev(r), f.res_lane_stride = b.stride(r);
+            f.act2 = ad.fused;
+          }
+          f.y = Y, f.y_lane_stride = ys;
+          b.launches.push_back({"dwconv_pw", s.op, [f](hipStream_t st) { return launch_dwpw(f, st); }});
+          b.launches.back().member_ops = {s.op, s.pw1};
+          break;
+        }
         // The sums go to the workspace of the mean step that follows.
         if (s.dw_sums) a.mean_part = reinterpret_cast<double *>(b.ws(si + 1));
         b.launches.push_back({"dwconv", s.op, [a](hipStream_t st) { return launch_dwconv(a, st); }});
@@ -1858,6 +1915,15 @@ void Model::account(Batch &b) const {
       case S_DW:
         l.flops = 2.0 * L * out_px * op.oc * op.kh * op.kw;
         l.bytes = F * (L * in_px * op.ic + L * out_px * op.oc + double(op.kh * op.kw + 1) * op.oc);
+        if (s.pw1 >= 0) {
+          // The folded 1x1: its product, weights and residual, and its map
+          // stored in place of the depthwise one.
+          const Op &q = p.ops[size_t(s.pw1)];
+          const double M = L * out_px, N = double(q.oc);
+          l.flops += 2.0 * M * double(op.oc) * N;
+          l.bytes = F * (L * in_px * op.ic + double(op.kh * op.kw + 1) * op.oc + double(op.oc) * N +
+                         (q.b1 ? N : 0) + M * N * (s.add >= 0 ? 2 : 1));
+        }
         break;
       case S_ELT: {
         double out = L * out_px * op.oc, src = L * in_px * op.ic;

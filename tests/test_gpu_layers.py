@@ -146,6 +146,40 @@ def test_conv_then_pointwise_folded(oracle, ci, co, co2, hw, lanes):
     near(got, want)
 
 
+@pytest.mark.parametrize("k,s,c,n,hw,lanes,residual", [
+    (3, (1, 1), 32, 48, (62, 70), 1, False),    # the detector's first block, on a smaller map
+    (3, (2, 2), 48, 96, (61, 66), 1, False),    # stride 2
+    (3, (1, 1), 96, 96, (33, 40), 1, True),     # 96 channels with the block's residual
+    (5, (2, 2), 96, 192, (30, 31), 1, False),   # 5 x 5 stride 2, twelve column blocks
+    (3, (1, 1), 48, 64, (24, 40), 3, False),    # the recogniser's first block, three lanes
+    (3, (2, 1), 64, 128, (12, 20), 2, False),   # unequal strides
+    (5, (1, 1), 128, 128, (9, 13), 2, True),    # 128 channels, tiles past the map
+    (3, (1, 1), 16, 20, (5, 7), 1, False),      # columns past the last block's, one tile
+])
+def test_depthwise_then_pointwise_folded(oracle, k, s, c, n, hw, lanes, residual):
+    # A 1 x 1 convolution (and its residual Add) that alone reads a
+    # depthwise layer: one launch, the depthwise rows made in LDS and
+    # multiplied there, the depthwise map never stored.
+    p = (k - 1) // 2
+    wd = RNG.normal(0, 1 / k, (k, k, c)).astype(np.float32)
+    bd = RNG.normal(0, 0.3, c).astype(np.float32)
+    w2 = RNG.normal(0, 1 / np.sqrt(c), (1, 1, c, n)).astype(np.float32)
+    b2 = RNG.normal(0, 0.3, n).astype(np.float32)
+
+    def build(b, t):
+        d = b.dwconv(t, wd, bd, k=(k, k), s=s, pad=(p, p, p, p), fused="hardswish")
+        y = b.conv(d, w2, b2, fused="none" if residual else "hardswish")
+        return b.add(y, t) if residual else y
+
+    b = PlanBuilder(*hw, c)
+    g = GpuModel.load(b.to_bytes([build(b, b.input)]))
+    launches, ops = g.launches(), g.launch_ops()
+    g.close()
+    assert [nm for nm, _ in launches] == ["dwconv_pw"] and ops == [[0, 1]], (launches, ops)
+    got, want = both(build, (*hw, c), oracle, lanes=lanes)
+    near(got, want)
+
+
 def test_ring_upsampled_sources(oracle):
     # A 5 x 5 convolution (on the LDS ring) over a map upsampled by 2 stacked
     # with a full-size one: the direct loads read the small map at (y/2, x/2).
