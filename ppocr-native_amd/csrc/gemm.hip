@@ -546,6 +546,8 @@ __host__ __device__ inline int patch_col_stride(int taps, int row, int cb) {
 // the reduction indices of lane group b / 4, against columns 16 + 4c..+3
 // (c = 0, 1: two instructions); the four lane groups' partial sums are added
 // at the end ((p0 + p1) + (p2 + p3), the same bits in every lane).
+__device__ __attribute__((aligned(16))) float kPatchZeros[4];
+
 template <int WR, int BN, int CB, bool R8>
 __device__ __forceinline__ void conv_patch_body(const Group<ConvArgs> &grp) {
   // Each XCD takes a contiguous run of tiles (xcd_tile): neighbouring tiles
@@ -640,25 +642,30 @@ __device__ __forceinline__ void conv_patch_body(const Group<ConvArgs> &grp) {
   // remainder within three waves per SIMD.
   constexpr int PP = R8 && WR == 1 ? kPatchPerR8W1 : kPatchPer;
   f32x4 rp[PP], rw[kWeightPer];
+  // Every load of a block is unconditional (a pixel outside the image or a
+  // channel past ctot reads kPatchZeros; past the taps, a weight load
+  // repeats the first tap), so that none waits at a branch; the gate
+  // multiplies the block's image pixels as they are stored.
+  f32x4 rg;
+  unsigned rlive = 0;  // which of rp hold image pixels
+  bool rgated = false;
   auto fetch = [&](int cc) {
     const int c = cc * CB + q * 4;
     const bool live_c = c < a.ctot;
     const ConvSrc src = pick_src(a, live_c ? c : 0);
     const int cl = c - src.coff, sh = src.shift, sw_ = a.iw >> sh;
     const float *base = src.p + (long)ln * src.lane_stride + cl;
-    const bool gated = a.gate && src.coff == 0;
-    const f32x4 g = gated ? *reinterpret_cast<const f32x4 *>(a.gate + (long)ln * a.gate_lane_stride + cl)
-                          : f32x4{1.f, 1.f, 1.f, 1.f};
+    rgated = a.gate && src.coff == 0;
+    rg = *reinterpret_cast<const f32x4 *>(rgated ? a.gate + (long)ln * a.gate_lane_stride + cl : kPatchZeros);
+    rlive = 0;
     int py = p0 / PC, px = p0 - (p0 / PC) * PC;
 #pragma unroll
     for (int k = 0; k < PP; k++) {
       const int iy = iy0 + py, ix = ix0 + px;
-      f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
-      if (p0 + k * PSTEP < npx && live_c && iy >= 0 && iy < a.ih && ix >= 0 && ix < a.iw) {
-        v = *reinterpret_cast<const f32x4 *>(base + ((long)(iy >> sh) * sw_ + (ix >> sh)) * src.c);
-        if (gated) v = v * g;
-      }
-      rp[k] = v;
+      const bool in = p0 + k * PSTEP < npx && live_c && iy >= 0 && iy < a.ih && ix >= 0 && ix < a.iw;
+      rp[k] = *reinterpret_cast<const f32x4 *>(in ? base + ((long)(iy >> sh) * sw_ + (ix >> sh)) * src.c
+                                                  : kPatchZeros);
+      rlive |= (in ? 1u : 0u) << k;
       px += sx, py += sy;
       if (px >= PC) px -= PC, py++;
     }
@@ -671,13 +678,17 @@ __device__ __forceinline__ void conv_patch_body(const Group<ConvArgs> &grp) {
       const float *wsrc = a.wt + (long)(n0 + (real ? n : 0)) * a.wt_k + (long)cc * CB + qq * 4;
 #pragma unroll
       for (int tp = 0; tp < kWeightPer / PPAIRS; tp++)
-        if (real && tp < taps) rw[u * (kWeightPer / PPAIRS) + tp] = *reinterpret_cast<const f32x4 *>(wsrc + tp * wstep);
+        rw[u * (kWeightPer / PPAIRS) + tp] = *reinterpret_cast<const f32x4 *>(wsrc + (tp < taps ? tp : 0) * wstep);
     }
   };
   auto store = [&]() {
 #pragma unroll
     for (int k = 0; k < PP; k++)
-      if (p0 + k * PSTEP < npx) *reinterpret_cast<f32x4 *>(P + (p0 + k * PSTEP) * S + q * 4) = rp[k];
+      if (p0 + k * PSTEP < npx) {
+        f32x4 v = rp[k];
+        if (rgated && (rlive >> k & 1u)) v = v * rg;
+        *reinterpret_cast<f32x4 *>(P + (p0 + k * PSTEP) * S + q * 4) = v;
+      }
 #pragma unroll
     for (int u = 0; u < PPAIRS; u++) {
       const int pr = tid + 256 * u;
@@ -688,12 +699,24 @@ __device__ __forceinline__ void conv_patch_body(const Group<ConvArgs> &grp) {
           *reinterpret_cast<f32x4 *>(Bs + n * NS + tp * S + qq * 4) = rw[u * (kWeightPer / PPAIRS) + tp];
     }
   };
+  // The bias of this thread's output columns, requested with the first block.
+  const float *bsrc = a.bias ? a.bias : kPatchZeros;
+  float bcol[NT], brem[R8 ? 2 : 1];
+#pragma unroll
+  for (int j = 0; j < NT; j++) bcol[j] = bsrc[a.bias ? min(n0 + j * 16 + li, a.n - 1) : 0];
+  if constexpr (R8) {
+#pragma unroll
+    for (int c = 0; c < NR; c++) brem[c] = bsrc[a.bias ? min(n0 + 16 + 4 * c + (li & 3), a.n - 1) : 0];
+  }
   fetch(0);
   for (int cc = 0; cc < a.cpt; cc++) {
     if (cc) __syncthreads();  // every wave is done with the previous block
     store();
     __syncthreads();
     if (cc + 1 < a.cpt) fetch(cc + 1);
+    // The next block's loads stay ahead of this block's multiply-adds (the
+    // compiler would otherwise sink them below, to their use).
+    asm volatile("" ::: "memory");
     // One tap: the window offset (ky, kx) into the staged patch. A 3 x 3
     // window runs its nine taps unrolled.
     auto tap = [&](int tp, int ky, int kx) {
@@ -765,7 +788,7 @@ __device__ __forceinline__ void conv_patch_body(const Group<ConvArgs> &grp) {
         const int n = n0 + j * 16 + li;
         if (n >= a.n) continue;
         float v = acc[i][j][r];
-        if (a.bias) v = v + a.bias[n];
+        if (a.bias) v = v + bcol[j];
         v = act(v, a.act);
         if (a.res) v = act(v + a.res[(long)ln * a.res_lane_stride + rem * a.n + n], a.act2);
         a.y[(long)ln * a.y_lane_stride + rem * a.n + n] = v;
@@ -790,7 +813,7 @@ __device__ __forceinline__ void conv_patch_body(const Group<ConvArgs> &grp) {
         if (oy >= a.oh || ox >= a.ow || n >= a.n) continue;
         const long rem = (long)oy * a.ow + ox;
         float u = lg == 0 ? v[0] : (lg == 1 ? v[1] : (lg == 2 ? v[2] : v[3]));
-        if (a.bias) u = u + a.bias[n];
+        if (a.bias) u = u + brem[c];
         u = act(u, a.act);
         if (a.res) u = act(u + a.res[(long)ln * a.res_lane_stride + rem * a.n + n], a.act2);
         a.y[(long)ln * a.y_lane_stride + rem * a.n + n] = u;
