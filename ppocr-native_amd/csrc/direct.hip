@@ -25,13 +25,24 @@ constexpr int kDirectTaps = 64;  // kh * kw * ic at most
 // KH, KW, IC > 0: the window and channel count fixed at compile time, so the
 // thread issues all of its patch's loads before the first multiply (the
 // loads of a runtime loop would each wait for the previous sum). 0: any.
+// Zeros for the unconditional loads of the direct kernels (at least IC
+// floats).
+__device__ __attribute__((aligned(16))) float kDirectZeros[4];
+
 template <int KH, int KW, int IC>
 __global__ __launch_bounds__(256) void conv_direct_kernel(DirectArgs a) {
   __shared__ __attribute__((aligned(16))) float ws[kDirectTaps * 8];
   constexpr bool FIXED = KH > 0;
+  static_assert(IC <= 4, "kDirectZeros holds four floats");
   const int kh = FIXED ? KH : a.kh, kw = FIXED ? KW : a.kw, ic = FIXED ? IC : a.ic;
   const int j0 = blockIdx.y * 8;
   const int K = kh * kw * ic;
+  // The bias of the group's eight columns, requested first and
+  // unconditionally (a load under a per-lane condition would wait at once).
+  float bk[8];
+  const float *bsrc = a.bias ? a.bias : kDirectZeros;
+#pragma unroll
+  for (int k = 0; k < 8; k++) bk[k] = bsrc[a.bias ? min(j0 + k, a.oc - 1) : 0];
   for (int e = threadIdx.x; e < K * 8; e += 256) {
     const int r = e >> 3, k = e & 7;
     ws[e] = j0 + k < a.oc ? a.w[(long)r * a.oc + j0 + k] : 0.0f;
@@ -47,7 +58,7 @@ __global__ __launch_bounds__(256) void conv_direct_kernel(DirectArgs a) {
   const bool first = ox < a.first_end;
   float acc[8];
 #pragma unroll
-  for (int k = 0; k < 8; k++) acc[k] = (a.bias && first && j0 + k < a.oc) ? a.bias[j0 + k] : 0.0f;
+  for (int k = 0; k < 8; k++) acc[k] = (a.bias && first && j0 + k < a.oc) ? bk[k] : 0.0f;
   // Whether the group's eight columns all fuse is the same for the whole
   // block: branch once rather than select per column.
   const bool all_fused = j0 + 8 <= a.fused;
@@ -75,9 +86,11 @@ __global__ __launch_bounds__(256) void conv_direct_kernel(DirectArgs a) {
         const int iy = oy * a.sh + ky - a.pt, ix = ox * a.sw + kx - a.pl;
         const bool ok = iy >= 0 && iy < a.ih && ix >= 0 && ix < a.iw;
         in[ky * KW + kx] = ok;
-        const float *px = x + ((long)iy * a.iw + ix) * IC;
+        // Every load unconditional (outside the image: kDirectZeros), so
+        // that the whole patch is in flight at once.
+        const float *px = ok ? x + ((long)iy * a.iw + ix) * IC : kDirectZeros;
 #pragma unroll
-        for (int i = 0; i < IC; i++) patch[(ky * KW + kx) * IC + i] = ok ? px[i] : 0.0f;
+        for (int i = 0; i < IC; i++) patch[(ky * KW + kx) * IC + i] = px[i];
       }
     }
 #pragma unroll
@@ -103,7 +116,7 @@ __global__ __launch_bounds__(256) void conv_direct_kernel(DirectArgs a) {
   for (int k = 0; k < 8; k++) {
     if (j0 + k >= a.oc) break;
     float v = acc[k];
-    if (a.bias && !first) v = v + a.bias[j0 + k];
+    if (a.bias && !first) v = v + bk[k];
     y[k] = act(v, a.act);
   }
 }
