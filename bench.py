@@ -43,7 +43,7 @@ VALU_LAUNCHES = {"stem_block"}
 # scaled by a plain copy kernel's counters (x2.0 / x1.0), for the launches
 # the bench reports a roofline of: (kernel, plan operations) -> (read, write)
 # KiB and the profile summary the numbers come from.
-MEASURED_TRAFFIC = {("conv_patch", (65, 71, 77, 83)): (31035, 7168, "profiles/hbm_counters_detector_recognizer.md"),
+MEASURED_TRAFFIC = {("conv_patch", (65, 71, 77, 83)): (32559, 9209, "profiles/hbm_counters_detector_recognizer.md"),
                     ("conv_patch", (94,)): (9102, 5400, "profiles/hbm_counters_detector_recognizer.md")}
 
 
