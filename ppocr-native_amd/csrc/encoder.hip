@@ -94,11 +94,39 @@ __device__ __forceinline__ float sum32(float v) {
   return v + __shfl_xor(v, 16, 32);
 }
 
+__device__ __attribute__((aligned(16))) float kEncZeros[4];
+
+// A LayerNorm's parameters for the values one thread normalises in ln_tile
+// (columns p, p + 32, ... of a row, p = thread % 32), read at a kernel's
+// start. Every load is unconditional (indices clamped below k; a null `ln`
+// reads zeros, never used), so that they arrive with the kernel's first
+// loads: a load under a per-lane condition would wait at once, one round
+// trip after another. `ln` holds gamma[k], beta[k], eps.
+template <int KP>
+struct LnRegs {
+  float g[KP / 32], b[KP / 32], eps;
+};
+
+template <int KP>
+__device__ __forceinline__ LnRegs<KP> ln_regs(const float *ln, int k) {
+  LnRegs<KP> r;
+  const int p = threadIdx.x % 32;
+  const float *src = ln ? ln : kEncZeros;
+#pragma unroll
+  for (int u = 0; u < KP / 32; u++) {
+    const int i = ln ? min(p + 32 * u, k - 1) : 0;
+    r.g[u] = src[i];
+    r.b[u] = src[ln ? k + i : 0];
+  }
+  r.eps = src[ln ? 2 * k : 0];
+  return r;
+}
+
 // LayerNorm of the 16 rows of an LDS tile (row stride S, the first k of each
 // row; the padding past k holds zeros and stays so), 32 threads a row with
-// KP / 32 of its values each in registers. `ln` holds gamma[k], beta[k], eps.
+// KP / 32 of its values each in registers; `lr` from ln_regs.
 template <int KP, int S>
-__device__ __forceinline__ void ln_tile(float *t, int k, const float *ln) {
+__device__ __forceinline__ void ln_tile(float *t, int k, const LnRegs<KP> &lr) {
   constexpr int P = kEncThreads / kEncRows, V = KP / P;
   static_assert(P == 32, "sum32 joins 32 lanes");
   const int tid = threadIdx.x, r = tid / P, p = tid % P;
@@ -117,11 +145,11 @@ __device__ __forceinline__ void ln_tile(float *t, int k, const float *ln) {
     const float d = x[u] - mean;
     if (p + P * u < k) q = q + d * d;
   }
-  const float root = sqrtf(sum32(q) / (float)k + ln[2 * k]);
+  const float root = sqrtf(sum32(q) / (float)k + lr.eps);
 #pragma unroll
   for (int u = 0; u < V; u++) {
     const int i = p + P * u;
-    if (i < k) row[i] = (x[u] - mean) / root * ln[i] + ln[k + i];
+    if (i < k) row[i] = (x[u] - mean) / root * lr.g[u] + lr.b[u];
   }
 }
 
@@ -181,11 +209,12 @@ __global__ __launch_bounds__(kEncThreads) void enc_linear(EncLinArgs a) {
   const int nb = (a.n + 15) / 16, j = blockIdx.y * 8 + w;
   f32x4 b[KQ];
   load_b<KQ>(b, a.wt, j, nb, lane);
+  const LnRegs<KP> lr = ln_regs<KP>(a.ln, a.k);
   split_rows(tr, a.rows, M, m0);
   load_rows<KP, S>(xs, a.x, a.x_lane_stride, a.rows, M, m0, a.k);
   __syncthreads();
   if (a.ln) {
-    ln_tile<KP, S>(xs, a.k, a.ln);
+    ln_tile<KP, S>(xs, a.k, lr);
     __syncthreads();
   }
   f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -277,15 +306,30 @@ __global__ __launch_bounds__(kEncThreads) void enc_attn_block(EncAttnArgs a, int
   float *os = sm + L.os;
   f32x4 b[KQ];
   load_b<KQ>(b, a.wt, w, (c + 15) / 16, lane);
-  // This lane's residual and bias, for the projection's epilogue.
   const int li = lane & 15, lg = lane >> 4, col = 16 * w + li;
-  float res[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-  if (a.res && col < c) {
+  // The MLP's LayerNorm parameters, with the kernel's first loads.
+  const LnRegs<KP> lr_in = ln_regs<KP>(HP ? a.ln : nullptr, c);
+  const LnRegs<KP> lr_out = ln_regs<KP>(HP ? a.ln_out : nullptr, c);
+  // Its biases: fc1's columns 16 (w + 8 jj) + li, fc2's column 16 w + li
+  // (clamped; those past the layer are never used).
+  float fb1[2], fb2;
+  {
+    const float *s1 = HP && a.b1 ? a.b1 : kEncZeros, *s2 = HP && a.b2 ? a.b2 : kEncZeros;
 #pragma unroll
-    for (int rr = 0; rr < 4; rr++)
-      if (4 * lg + rr < nq) res[rr] = a.res[(long)ln * a.res_lane_stride + (long)(q0 + 4 * lg + rr) * c + col];
+    for (int jj = 0; jj < 2; jj++) fb1[jj] = s1[HP && a.b1 ? min(16 * (w + 8 * jj) + li, a.hidden - 1) : 0];
+    fb2 = s2[HP && a.b2 ? min(col, c - 1) : 0];
   }
-  const float bias = a.bias && col < c ? a.bias[col] : 0.0f;
+  // This lane's residual and bias, for the projection's epilogue, loaded
+  // unconditionally (rows and column clamped into the line; values past the
+  // run or the width are never stored).
+  float res[4];
+  {
+    const bool hr = a.res != nullptr;
+    const float *rs = hr ? a.res + (long)ln * a.res_lane_stride : kEncZeros;
+#pragma unroll
+    for (int rr = 0; rr < 4; rr++) res[rr] = rs[hr ? (long)min(q0 + 4 * lg + rr, t - 1) * c + min(col, c - 1) : 0];
+  }
+  const float bias = (a.bias ? a.bias : kEncZeros)[a.bias ? min(col, c - 1) : 0];
 
   // K and V: thread (key slot, part) moves four channels of one of them for
   // keys slot, slot + per, ...; where each channel lands is worked out once.
@@ -507,7 +551,7 @@ __global__ __launch_bounds__(kEncThreads) void enc_attn_block(EncAttnArgs a, int
     for (int e = tid; e < kEncRows * pad; e += kEncThreads) hs[(e / pad) * SH + 16 * nb1 + e % pad] = 0.0f;
     __syncthreads();
     if (a.ln) {
-      ln_tile<KP, S>(ns, c, a.ln);
+      ln_tile<KP, S>(ns, c, lr_in);
       __syncthreads();
     }
     {
@@ -520,7 +564,7 @@ __global__ __launch_bounds__(kEncThreads) void enc_attn_block(EncAttnArgs a, int
         if (j >= nb1) continue;
         const int hc = 16 * j + li;
         const f32x4 hv = jj ? h1 : h0;
-        const float hb = a.b1 && hc < hidden ? a.b1[hc] : 0.0f;
+        const float hb = fb1[jj];
 #pragma unroll
         for (int rr = 0; rr < 4; rr++) {
           float v = hv[rr];
@@ -534,7 +578,7 @@ __global__ __launch_bounds__(kEncThreads) void enc_attn_block(EncAttnArgs a, int
     mfma_rows<HQ, SH>(o, hs, w2, lane);
     // Each lane reads and rewrites its own (row, column) of zs.
     if (col < c) {
-      const float ob = a.b2 ? a.b2[col] : 0.0f;
+      const float ob = fb2;
 #pragma unroll
       for (int rr = 0; rr < 4; rr++) {
         float v = o[rr];
@@ -546,7 +590,7 @@ __global__ __launch_bounds__(kEncThreads) void enc_attn_block(EncAttnArgs a, int
     }
     __syncthreads();
     if (a.ln_out) {
-      ln_tile<KP, S>(zs, c, a.ln_out);
+      ln_tile<KP, S>(zs, c, lr_out);
       __syncthreads();
     }
     for (int e = tid; e < nq * c4; e += kEncThreads) {
@@ -626,13 +670,23 @@ __global__ __launch_bounds__(kEncThreads) void enc_mlp(EncMlpArgs a) {
   load_b<KQ>(b0, a.w1, w, nb1, lane);
   load_b<KQ>(b1, a.w1, w + 8, nb1, lane);
   load_b<HQ>(b2, a.w2, w, nb2, lane);
+  const LnRegs<KP> lr_in = ln_regs<KP>(a.ln, c), lr_out = ln_regs<KP>(a.ln_out, c);
+  // The biases of fc1's columns 16 (w + 8 jj) + li and fc2's 16 w + li,
+  // with the first loads (clamped; those past the layer are never used).
+  float fb1[2], fb2;
+  {
+    const float *s1 = a.b1 ? a.b1 : kEncZeros, *s2 = a.b2 ? a.b2 : kEncZeros;
+#pragma unroll
+    for (int jj = 0; jj < 2; jj++) fb1[jj] = s1[a.b1 ? min(16 * (w + 8 * jj) + li, hidden - 1) : 0];
+    fb2 = s2[a.b2 ? min(16 * w + li, c - 1) : 0];
+  }
   split_rows(tr, a.rows, M, m0);
   load_rows<KP, S>(zs, a.x, a.x_lane_stride, a.rows, M, m0, c, ns);
   const int pad = HP - 16 * nb1;
   for (int e = tid; e < kEncRows * pad; e += kEncThreads) hs[(e / pad) * SH + 16 * nb1 + e % pad] = 0.0f;
   __syncthreads();
   if (a.ln) {
-    ln_tile<KP, S>(ns, c, a.ln);
+    ln_tile<KP, S>(ns, c, lr_in);
     __syncthreads();
   }
   {
@@ -645,7 +699,7 @@ __global__ __launch_bounds__(kEncThreads) void enc_mlp(EncMlpArgs a) {
       if (j >= nb1) continue;
       const int col = 16 * j + li;
       const f32x4 acc = jj ? acc1 : acc0;
-      const float bias = a.b1 && col < hidden ? a.b1[col] : 0.0f;
+      const float bias = fb1[jj];
 #pragma unroll
       for (int r = 0; r < 4; r++) {
         float v = acc[r];
@@ -661,7 +715,7 @@ __global__ __launch_bounds__(kEncThreads) void enc_mlp(EncMlpArgs a) {
   // thread touches them until the barrier.
   const int col = 16 * w + li;
   if (col < c) {
-    const float bias = a.b2 ? a.b2[col] : 0.0f;
+    const float bias = fb2;
 #pragma unroll
     for (int r = 0; r < 4; r++) {
       float v = acc[r];
@@ -673,7 +727,7 @@ __global__ __launch_bounds__(kEncThreads) void enc_mlp(EncMlpArgs a) {
   }
   __syncthreads();
   if (a.ln_out) {
-    ln_tile<KP, S>(zs, c, a.ln_out);
+    ln_tile<KP, S>(zs, c, lr_out);
     __syncthreads();
   }
   const int c4 = c / 4;
