@@ -910,12 +910,23 @@ __global__ __launch_bounds__(256) void upadd_chain_kernel(ChainArgs a) {
     const int y = (int)(pix / a.w[0]), x = (int)(pix - (long)y * a.w[0]), ch = 4 * q;
     f32x4 v = *reinterpret_cast<const f32x4 *>(a.top + (long)ln * a.top_lane_stride +
                                               ((long)(y >> L) * top_w + (x >> L)) * a.c + ch);
+    // Every level's addend and gate first, all in flight together (none is
+    // a level's output; loaded after a level's store, each would wait for
+    // it), the gates unconditionally (kDwZeros, never used, when a level
+    // has none).
+    f32x4 us[L], gs[L];
+#pragma unroll
+    for (int k = 0; k < L; k++) {
+      const long o = ((long)(y >> k) * a.w[k] + (x >> k)) * a.c + ch;
+      us[k] = *reinterpret_cast<const f32x4 *>(a.b[k] + (long)ln * a.b_lane_stride[k] + o);
+      gs[k] = *reinterpret_cast<const f32x4 *>(a.g[k] ? a.g[k] + (long)ln * a.g_lane_stride[k] + ch : kDwZeros);
+    }
 #pragma unroll
     for (int k = L - 1; k >= 0; k--) {
       const long o = ((long)(y >> k) * a.w[k] + (x >> k)) * a.c + ch;
-      f32x4 u = *reinterpret_cast<const f32x4 *>(a.b[k] + (long)ln * a.b_lane_stride[k] + o);
+      f32x4 u = us[k];
       if (a.g[k]) {
-        const f32x4 g = *reinterpret_cast<const f32x4 *>(a.g[k] + (long)ln * a.g_lane_stride[k] + ch);
+        const f32x4 g = gs[k];
 #pragma unroll
         for (int i = 0; i < 4; i++) u[i] = u[i] + u[i] * g[i];
       }
