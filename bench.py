@@ -172,6 +172,11 @@ def bench_block(P, nets, steps, warmup):
     g.input_mut()[:] = np.random.default_rng(5).uniform(-1, 1, 160 * 160 * 96).astype(np.float32)
     g.upload()
     ms, _ = time_model(g, steps, warmup)
+    # The same runs launched eagerly, for reference: three short launches,
+    # where a graph replay's fixed cost weighs most.
+    g.set_graphs(False)
+    eager_ms, _ = time_model(g, steps, warmup)
+    g.set_graphs(True)
     rows = profile(g, 20)
     g.close()
     flops = sum(r["flops"] for r in rows)
@@ -180,6 +185,7 @@ def bench_block(P, nets, steps, warmup):
     compulsory = 2 * 160 * 160 * 96 * 4
     rate = compulsory / (ms * 1e-3) / 1e9
     return {"workload": "fused dw3x3+SE+pw block 1x96x160x160", "ms": round(ms, 4),
+            "eager_ms": round(eager_ms, 4),
             "gflops_per_s": round(flops / (ms * 1e-3) / 1e9, 1),
             "compulsory_bytes": compulsory,
             "compulsory_gb_per_s": round(rate, 1),
