@@ -135,19 +135,20 @@ __global__ __launch_bounds__(256) void conv_stem_kernel(DirectArgs a) {
   static_assert(OQ % 4 == 0 && PB % 64 == 0, "float4 columns, whole waves per part");
   __shared__ __attribute__((aligned(16))) float ws[K * OC];
   __shared__ __attribute__((aligned(16))) float out[PB * OC];
-  for (int e = threadIdx.x; e < K * OC; e += 256) ws[e] = a.w[e];
-  __syncthreads();
   const int per = a.oh * a.ow, total = a.lanes * per;
   const int pl = threadIdx.x % PB, q = threadIdx.x / PB;
   // Blocks numbered XCD by XCD (xcd_tile): neighbouring output rows, which
   // read the same input rows, meet in one L2.
   const int g0 = xcd_tile((int)blockIdx.x, (int)gridDim.x) * PB, g = g0 + pl;
+  // The pixel's patch is requested first, then every weight at once (a
+  // rolled staging loop would wait out each load before the next), so that
+  // both arrive in one round trip.
+  float patch[K];
+  bool in[9];
   if (g < total) {
     const int ln = g / per, rem = g - ln * per;
     const int oy = rem / a.ow, ox = rem - oy * a.ow;
     const float *x = a.x + (long)ln * a.x_lane_stride;
-    float patch[K];
-    bool in[9];
 #pragma unroll
     for (int ky = 0; ky < 3; ky++) {
 #pragma unroll
@@ -160,9 +161,26 @@ __global__ __launch_bounds__(256) void conv_stem_kernel(DirectArgs a) {
         for (int i = 0; i < 3; i++) patch[(ky * 3 + kx) * 3 + i] = ok ? px[i] : 0.0f;
       }
     }
+  }
+  // This part's biases, with the first loads (unconditional: a null bias
+  // reads kDirectZeros, never used).
+  float bq[OQ];
+#pragma unroll
+  for (int j = 0; j < OQ; j++) bq[j] = (a.bias ? a.bias : kDirectZeros)[a.bias ? q * OQ + j : 0];
+  {
+    constexpr int WN = (K * OC + 255) / 256;
+    float wt[WN];
+#pragma unroll
+    for (int i = 0; i < WN; i++) wt[i] = a.w[min((int)threadIdx.x + 256 * i, K * OC - 1)];
+#pragma unroll
+    for (int i = 0; i < WN; i++)
+      if ((int)threadIdx.x + 256 * i < K * OC) ws[threadIdx.x + 256 * i] = wt[i];
+  }
+  __syncthreads();
+  if (g < total) {
     float acc[OQ];
 #pragma unroll
-    for (int j = 0; j < OQ; j++) acc[j] = a.bias ? a.bias[q * OQ + j] : 0.0f;
+    for (int j = 0; j < OQ; j++) acc[j] = a.bias ? bq[j] : 0.0f;
 #pragma unroll
     for (int t = 0; t < 9; t++) {
       if (!in[t]) continue;
